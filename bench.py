@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X decoder hot path (one GPU).
+
+Headline (`value`): forward + cross-entropy loss tokens/s of the reference's
+`large` preset (1,009,338,368 parameters) at batch 4 x seq 1024, seeded
+reference init, uniform token ids, all in f32, with the weights and the token
+ids resident in HBM when the timed region starts. One step = one forward +
+loss over the batch (mmh_model_run_staged). Also reported: the tiny preset
+(B8 T256), the BASELINE GEMM sweep (M=2048, K,N in {256,1024,4096}, forward
+C=A.B and backward dA=dC.B^T, dB=A^T.dC), a per-kernel-class breakdown from
+HIP events, the roofline of the dominant kernel (the fp32 MFMA GEMM) and the
+CPU baseline (the oracle, a C restatement of the reference CPU path, on one
+host core).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-sweep]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "midman-ai_amd"))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))  # the cpu_baseline leg only
+
+import numpy as np  # noqa: E402
+
+METRIC = "forward+loss tokens/sec (tiny, large presets) + GEMM fp32 TFLOPS % of MFMA peak"
+PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
+PEAK_HBM_GBS = 8000.0
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def model_flops(cfg, B, T):
+    V, d, L, H, Hkv, ff = (int(v) for v in cfg[:6])
+    hd = d // H
+    kv = Hkv * hd
+    N = B * T
+    per_layer = {
+        "gemm_qkv": 2 * N * d * (d + 2 * kv),
+        "gemm_o": 2 * N * d * d,
+        "gemm_gate_up": 2 * N * d * 2 * ff,
+        "gemm_down": 2 * N * ff * d,
+        "attention": 4 * B * H * hd * T * (T + 1) // 2,
+    }
+    out = {k: v * L for k, v in per_layer.items()}
+    out["gemm_head"] = 2 * N * d * V
+    return out
+
+
+def model_bytes(cfg, B, T):
+    """Algorithmic HBM bytes of the bandwidth kernels (inputs read once,
+    outputs written once, f32)."""
+    V, d, L = (int(v) for v in cfg[:3])
+    N = B * T
+    return {
+        "embedding": 8 * N * d + 4 * N,
+        "rms_norm": (2 * L + 1) * (8 * N * d + 4 * d),
+        "loss": 4 * N * V + 4 * N,
+    }
+
+
+def time_model(mh, ctx, preset, B, T, steps, warmup):
+    cfg = mh.PRESETS[preset]
+    t0 = time.time()
+    m = mh.Model.new(ctx, cfg, 0)
+    log(f"{preset}: seeded init + upload {time.time() - t0:.1f}s, {m.num_parameters():,} params")
+    x, y = m.lab_tokens(B, T)
+    m.stage(x, y, B, T)
+    for _ in range(warmup):
+        m.run_staged(B, T)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(steps):
+        m.run_staged(B, T)
+    ms = ctx.timer_stop()
+    ctx.synchronize()
+    loss = m.read_loss()
+    ms_step = ms / steps
+    # the same step through the host-buffer boundary (ids upload + loss download)
+    t1 = time.perf_counter()
+    for _ in range(max(1, steps // 2)):
+        m.loss(x, y, B, T)
+    host_ms = (time.perf_counter() - t1) * 1000 / max(1, steps // 2)
+    prof = m.profile(B, T)
+    m.close()
+    return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
+            "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg}
+
+
+def gemm_sweep(mh, ctx, reps=10):
+    M = 2048
+    rows = []
+    for k in (256, 1024, 4096):
+        for n in (256, 1024, 4096):
+            a = mh.randn((M, k), 1.0, 1)
+            b = mh.randn((k, n), 0.02, 2)
+            dc = mh.randn((M, n), 1.0, 3)
+            A, B, DC = ctx.to_device(a), ctx.to_device(b), ctx.to_device(dc)
+            C, DA, DB = ctx.empty((M, n)), ctx.empty((M, k)), ctx.empty((k, n))
+            flops = 2.0 * M * n * k
+            res = {"M": M, "K": k, "N": n}
+            for form, fn in (("fwd_nn", lambda: mh.gemm(ctx, "nn", A, B, C, M, k, n)),
+                             ("dA_nt", lambda: mh.matmul_backward(ctx, A, B, DC, M, k, n, da=DA)),
+                             ("dB_tn", lambda: mh.matmul_backward(ctx, A, B, DC, M, k, n, db=DB))):
+                for _ in range(3):
+                    fn()
+                ctx.synchronize()
+                ctx.timer_start()
+                for _ in range(reps):
+                    fn()
+                ms = ctx.timer_stop() / reps
+                res[form] = round(flops / (ms / 1000) / 1e12, 2)
+            rows.append(res)
+            for x in (A, B, DC, C, DA, DB):
+                x.free()
+    return rows
+
+
+def cpu_baseline_large():
+    """The oracle (a C restatement of the reference CPU path: 4x16 AVX tile,
+    separate multiply and add, glibc libm) on ONE host core, on a bounded
+    sample of the large workload: one decoder block at B1 T1024, the final
+    norm, the tied head and the loss, extrapolated to 20 blocks."""
+    import mm_oracle as O
+
+    try:
+        os.sched_setaffinity(0, {sorted(os.sched_getaffinity(0))[0]})
+    except (AttributeError, OSError):
+        pass
+    c = O.preset("large")
+    d, ff, kv, V = c.d_model, c.d_ff, c.kv_dim, c.vocab_size
+    T = 1024
+    rng = np.random.default_rng(0)
+    nblock = 2 * d + 2 * d * d + 2 * d * kv + 3 * d * ff
+    bw = (rng.standard_normal(nblock) * 0.02).astype(np.float32)
+    bw[:d] = 1.0
+    x = rng.standard_normal((1, T, d)).astype(np.float32)
+    cos, sin = O.rope_tables(c.head_dim, T, 10000.0)
+    t0 = time.perf_counter()
+    y = O.block_forward(c, bw, cos, sin, x, threads=1)
+    t_block = time.perf_counter() - t0
+    E = (rng.standard_normal((V, d)) * 0.02).astype(np.float32)
+    targets = rng.integers(0, V, size=T).astype(np.int32)
+    t0 = time.perf_counter()
+    xn = O.rms_norm(y.reshape(T, d), np.ones(d, np.float32), 1e-5)
+    logits = O.gemm("nt", xn, E, T, d, V, threads=1)
+    loss = O.cross_entropy(logits, targets)
+    t_head = time.perf_counter() - t0
+    total = c.n_layers * t_block + t_head
+    return {"value": round(T / total, 2), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": (f"oracle single-thread AVX restatement: 1 large-preset decoder block at "
+                       f"B1 T1024 ({t_block:.1f}s) + final norm + tied head + CE ({t_head:.1f}s), "
+                       f"extrapolated to 20 blocks"),
+            "loss_sanity": loss}
+
+
+def cpu_baseline_tiny():
+    import mm_oracle as O
+
+    c = O.preset("tiny")
+    w, x, y = O.lab_setup(c, 0, 8, 256)
+    t0 = time.perf_counter()
+    runs = 0
+    while time.perf_counter() - t0 < 3.0 or runs < 2:
+        O.forward_loss(c, w, x, y, 8, 256, want_logits=False, threads=1)
+        runs += 1
+    dt = (time.perf_counter() - t0) / runs
+    return {"value": round(2048 / dt, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"oracle single-thread, full tiny forward+loss B8 T256, {runs} runs"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-tiny", action="store_true")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the reference has none either); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import midman_hip as mh
+
+    ctx = mh.Context(0)
+    name, cus = ctx.device_info()
+    log(f"device {name}, {cus} CUs")
+
+    large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup)
+    log(f"large: {large['ms_per_step']:.2f} ms/step, {large['tokens_per_s']:.0f} tok/s, "
+        f"loss {large['loss']:.5f}")
+    tiny = None
+    if not a.no_tiny:
+        tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5))
+        log(f"tiny: {tiny['ms_per_step']:.3f} ms/step, {tiny['tokens_per_s']:.0f} tok/s")
+
+    flops = model_flops(large["cfg"], 4, 1024)
+    nbytes = model_bytes(large["cfg"], 4, 1024)
+    prof = large["profile"]
+    gemm_cls = ["gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down", "gemm_head"]
+    gemm_flops = sum(flops[k] for k in gemm_cls)
+    gemm_ms = sum(prof[k][0] for k in gemm_cls)
+    gemm_launches = sum(prof[k][1] for k in gemm_cls)
+    achieved = gemm_flops / (gemm_ms / 1000) / 1e12
+    breakdown = {}
+    for k, (ms, nl) in prof.items():
+        e = {"ms": round(ms, 3), "launches": nl}
+        if k in flops:
+            e["tflops"] = round(flops[k] / (ms / 1000) / 1e12, 2) if ms > 0 else None
+        if k in nbytes:
+            e["gbs"] = round(nbytes[k] / (ms / 1000) / 1e9, 1) if ms > 0 else None
+        breakdown[k] = e
+    total_flops = sum(flops.values())
+    log(f"GEMM {achieved:.1f} TFLOP/s over {gemm_launches} launches ({gemm_ms:.1f} ms)")
+
+    sweep = None
+    if not a.no_sweep:
+        sweep = gemm_sweep(mh, ctx)
+        log("sweep: " + ", ".join(f"{r['K']}x{r['N']}:{r['fwd_nn']}/{r['dA_nt']}/{r['dB_tn']}"
+                                  for r in sweep))
+    ctx.close()
+
+    cpu = None
+    tiny_cpu = None
+    if not a.no_cpu:
+        log("CPU baseline (oracle, 1 core) ...")
+        cpu = cpu_baseline_large()
+        log(f"CPU large: {cpu['value']} tok/s")
+        tiny_cpu = cpu_baseline_tiny()
+        log(f"CPU tiny: {tiny_cpu['value']} tok/s")
+
+    out = {
+        "metric": METRIC,
+        "value": round(large["tokens_per_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(large["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: reference seeded init (Rng(0)), uniform token ids (Lab scheme)",
+        "config": {"workload": "large preset forward + cross-entropy loss", "batch": 4,
+                   "seq": 1024, "vocab": 32000, "params": 1009338368,
+                   "flops_per_step": total_flops},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                     "kernel": "gemm_f32_mfma (all GEMM launches of one large forward)",
+                     "launches": gemm_launches, "avg_launch_ms": round(gemm_ms / gemm_launches, 4)},
+        "cpu_baseline": cpu,
+        "extra": {
+            "model_tflops": round(total_flops / (large["ms_per_step"] / 1000) / 1e12, 2),
+            "pcie_inclusive_tokens_per_s": round(large["pcie_inclusive_tokens_per_s"], 1),
+            "large_loss": large["loss"],
+            "kernel_classes": breakdown,
+            "tiny": None if tiny is None else {
+                "tokens_per_s": round(tiny["tokens_per_s"], 1),
+                "ms_per_step": round(tiny["ms_per_step"], 4),
+                "pcie_inclusive_tokens_per_s": round(tiny["pcie_inclusive_tokens_per_s"], 1),
+                "cpu_baseline": tiny_cpu},
+            "gemm_sweep_tflops": sweep,
+            "device": name,
+        },
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,218 @@
+/*
+ * midman_hip.h -- C ABI of libmidman_hip.so, the MI355X (gfx950) implementation
+ * of midman-ai's decoder forward + cross-entropy loss and the autograd matmul
+ * backward.
+ *
+ * Conventions follow the reference's own C ABI (crates/midman-api/src/ffi.rs:5-32):
+ *   - Handles, not pointers, for library objects (contexts, models). A stale or
+ *     invented handle is an error status, never undefined behaviour.
+ *   - The caller owns its input buffers; outputs go to caller buffers.
+ *   - Every function returns an int32 status (codes below); the message of the
+ *     last failure on the calling thread is read with mmh_error_ptr/len.
+ *     Nothing unwinds across the boundary.
+ *   - One thread per context: a context (and the models on it) must be used
+ *     from one thread at a time.
+ *   - A model config is 10 doubles in the reference order (ffi.rs:27-32,68-79):
+ *     [vocab_size, d_model, n_layers, n_heads, n_kv_heads, d_ff, max_seq_len,
+ *      rope_theta, norm_eps, tie_embeddings].
+ *
+ * Device-buffer entry points (mmh_gemm_*, mmh_rms_norm, ...) take device
+ * pointers from mmh_alloc and are asynchronous on the context's HIP stream.
+ * Token ids and targets are always host arrays: they are validated on the host
+ * (id < V, as ops_shape.rs:250-252 and ops_reduce.rs:250-252 do) before any
+ * launch, so an out-of-range id is MMH_ERR_INDEX and nothing runs.
+ *
+ * Numerics: all arithmetic is IEEE f32 as in the reference; GEMM sums are
+ * formed by fp32 MFMA in a different order from the reference's sequential
+ * p-ascending loop, so results agree within a tolerance, not bit for bit
+ * (see each function). Embedding, RoPE, token and index handling are bit-exact.
+ */
+#ifndef MIDMAN_HIP_H
+#define MIDMAN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MMH_ABI_VERSION 1u
+
+/* Status codes: the values of ffi.rs:44-61 plus one for the device. */
+#define MMH_OK 0
+#define MMH_STOPPED 1
+#define MMH_ERR_ARGUMENT (-1) /* null pointer, bad handle, value out of range */
+#define MMH_ERR_CONFIG (-2)   /* invalid model config (config.rs:106-138) */
+#define MMH_ERR_SHAPE (-3)    /* sizes that do not fit */
+#define MMH_ERR_INDEX (-4)    /* token id or target >= vocab */
+#define MMH_ERR_OTHER (-5)    /* any other library error */
+#define MMH_ERR_DEVICE (-6)   /* a HIP runtime error (no reference counterpart) */
+#define MMH_ERR_PANIC (-99)   /* an internal exception caught at the boundary */
+
+typedef int64_t mmh_handle;
+
+/* ---- library ---------------------------------------------------------- */
+
+/* ffi.rs:42 ABI_VERSION. */
+uint32_t mmh_abi_version(void);
+/* ffi.rs midman_error_ptr/midman_error_len: the calling thread's last error
+ * message (not NUL-terminated; valid until the next call on this thread). */
+const char *mmh_error_ptr(void);
+uint32_t mmh_error_len(void);
+
+/* ---- context: one HIP device + one stream ------------------------------ */
+
+/* No reference counterpart (the reference has no device); the analogue of
+ * midman_lab_create's handle table (ffi.rs:473). */
+int32_t mmh_context_create(int32_t device, mmh_handle *out_ctx);
+int32_t mmh_context_destroy(mmh_handle ctx);
+/* Waits for all work queued on the context's stream. */
+int32_t mmh_synchronize(mmh_handle ctx);
+/* Device name (NUL-terminated, truncated to cap) and compute-unit count. */
+int32_t mmh_device_info(mmh_handle ctx, char *name, uint32_t cap, int32_t *cu_count);
+
+/* Device memory owned by the caller through the context. */
+int32_t mmh_alloc(mmh_handle ctx, uint64_t bytes, void **out_dev);
+int32_t mmh_free(mmh_handle ctx, void *dev);
+/* Synchronous copies host <-> device, ordered after queued work. */
+int32_t mmh_upload(mmh_handle ctx, void *dst_dev, const void *src_host, uint64_t bytes);
+int32_t mmh_download(mmh_handle ctx, void *dst_host, const void *src_dev, uint64_t bytes);
+/* HIP-event timing of the context's stream: start records, stop records and
+ * waits, and returns the milliseconds between the two. */
+int32_t mmh_timer_start(mmh_handle ctx);
+int32_t mmh_timer_stop(mmh_handle ctx, float *ms);
+
+/* Tensor::randn(shape, std, &mut Rng::seed_from_u64(seed)) (tensor.rs:158-162,
+ * rng.rs:36-84) into a host array of n values: the reference's bits. */
+int32_t mmh_randn(uint64_t seed, float std, float *out_host, int64_t n);
+
+/* ---- the GEMM seam: midman-tensor/src/kernels.rs:49-84 ------------------ */
+
+/* All matrices row-major f32. accumulate != 0 adds into C (the reference
+ * kernels always accumulate, kernels.rs:48); accumulate == 0 overwrites C.
+ * Tolerance against the reference order: |diff| <= 1e-5 * sum_p |a_p b_p|. */
+
+/* kernels.rs:49 gemm_nn: C[m,n] (+)= A[m,k] B[k,n] */
+int32_t mmh_gemm_nn(mmh_handle ctx, const float *a, const float *b, float *c, int64_t m,
+                    int64_t k, int64_t n, int32_t accumulate);
+/* kernels.rs:66 gemm_nt: C[m,n] (+)= A[m,k] B[n,k]^T (no transpose is materialized) */
+int32_t mmh_gemm_nt(mmh_handle ctx, const float *a, const float *b, float *c, int64_t m,
+                    int64_t k, int64_t n, int32_t accumulate);
+/* kernels.rs:78 gemm_tn: C[m,n] (+)= A[k,m]^T B[k,n] */
+int32_t mmh_gemm_tn(mmh_handle ctx, const float *a, const float *b, float *c, int64_t m,
+                    int64_t k, int64_t n, int32_t accumulate);
+/* ops_matmul.rs:87-96, batched form: C[i] = A[i] B[i] for i < batch, each
+ * [m,k] x [k,n], contiguous. */
+int32_t mmh_matmul_batched(mmh_handle ctx, const float *a, const float *b, float *c,
+                           int64_t batch, int64_t m, int64_t k, int64_t n);
+/* ops_matmul.rs:62-74, the shared-rhs matmul backward: for C[rows,n] =
+ * A[rows,k] B[k,n], dA = dC B^T ([rows,k]) and dB = A^T dC ([k,n]). A NULL
+ * output is "not needed" (the reference's need flags). Outputs overwritten. */
+int32_t mmh_matmul_backward(mmh_handle ctx, const float *a, const float *b, const float *dc,
+                            float *da, float *db, int64_t rows, int64_t k, int64_t n);
+
+/* ---- layer ops: midman-nn/src/lib.rs:45-56 ------------------------------ */
+
+/* ops_shape.rs:230-257: out[i,:] = table[ids[i],:]; ids on the host. Bit-exact. */
+int32_t mmh_embedding(mmh_handle ctx, const float *table, int64_t vocab, int64_t d,
+                      const int32_t *ids_host, int64_t n, float *out);
+/* norm.rs:21-39: out = x * (mean(x^2) + eps)^(-1/2) * w over rows of d. */
+int32_t mmh_rms_norm(mmh_handle ctx, const float *x, const float *w, int64_t rows, int64_t d,
+                     float eps, float *out);
+/* rope.rs:54-85: cos/sin tables [max_seq_len, head_dim/2] (angles in f64,
+ * stored f32; bit-exact), written to device buffers. */
+int32_t mmh_rope_tables(mmh_handle ctx, int64_t head_dim, int64_t max_seq_len, float theta,
+                        float *cos_dev, float *sin_dev);
+/* rope.rs:20-33 / :114-128: x [bh, t, hd], positions 0..t-1. Bit-exact. */
+int32_t mmh_apply_rope(mmh_handle ctx, const float *x, int64_t bh, int64_t t, int64_t hd,
+                       const float *cos_dev, const float *sin_dev, float *out);
+/* attention.rs:97-101: q [B,H,T,hd], k/v [B,Hkv,T,hd] (already rotated),
+ * out [B,H,T,hd]; head j reads kv head j / (H/Hkv). hd in {8,16,32,64,128}. */
+int32_t mmh_causal_attention(mmh_handle ctx, const float *q, const float *k, const float *v,
+                             int64_t b, int64_t h, int64_t hkv, int64_t t, int64_t hd,
+                             float *out);
+/* attention.rs:146-170: x [B,T,d] -> out [B,T,d]; weights [d,d],[d,kv],[d,kv],[d,d]. */
+int32_t mmh_attention_forward(mmh_handle ctx, const float *x, const float *wq, const float *wk,
+                              const float *wv, const float *wo, const float *cos_dev,
+                              const float *sin_dev, int64_t b, int64_t t, int64_t d,
+                              int64_t h, int64_t hkv, float *out);
+/* mlp.rs:20-24: out = (silu(x Wg) * (x Wu)) Wd; x [rows,d]. */
+int32_t mmh_swiglu(mmh_handle ctx, const float *x, const float *wg, const float *wu,
+                   const float *wd, int64_t rows, int64_t d, int64_t ff, float *out);
+/* ops_elementwise.rs:249-259 same-shape add: out = a + b. Bit-exact. */
+int32_t mmh_add(mmh_handle ctx, const float *a, const float *b, float *out, int64_t n);
+/* ops_reduce.rs:236-259: mean over rows of max + ln(sum exp(z - max)) - z[t],
+ * accumulated in f64; targets on the host; the loss is returned to the host. */
+int32_t mmh_cross_entropy(mmh_handle ctx, const float *logits, const int32_t *targets_host,
+                          int64_t n, int64_t vocab, float *loss_host);
+
+/* ---- model: midman-model/src/model.rs ---------------------------------- */
+
+/* model.rs:51-83 with weights given by the caller in the reference parameter
+ * order (docs/midman-model.md:20): embed; per block attn_norm, q, k, v, o,
+ * mlp_norm, gate, up, down; final_norm; lm_head if untied. */
+int32_t mmh_model_create(mmh_handle ctx, const double config[10], const float *weights_host,
+                         int64_t n_weights, mmh_handle *out_model);
+/* MidManModel::with_init_std(config, std, &mut Rng::seed_from_u64(seed))
+ * (model.rs:51-83): the same weights bit for bit. The model keeps the Rng
+ * after the draws for mmh_model_lab_tokens. */
+int32_t mmh_model_create_seeded(mmh_handle ctx, const double config[10], uint64_t seed,
+                                float std, mmh_handle *out_model);
+/* Lab::new's task (lab.rs:194-203): continues the model's Rng with batch
+ * sequences of seq+1 draws of below(vocab); inputs = tokens[..seq],
+ * targets = tokens[1..]. Bit-exact. */
+int32_t mmh_model_lab_tokens(mmh_handle model, int64_t batch, int64_t seq, int32_t *inputs,
+                             int32_t *targets);
+int32_t mmh_model_param_count(mmh_handle model, int64_t *out);
+/* Copies the weights back in the reference parameter order. */
+int32_t mmh_model_download_weights(mmh_handle model, float *out_host, int64_t n);
+/* model.rs:103: logits [B,T,V] to the host. */
+int32_t mmh_model_forward(mmh_handle model, const int32_t *ids_host, int64_t batch, int64_t seq,
+                          float *logits_host);
+/* model.rs:174: the mean next-token cross-entropy. */
+int32_t mmh_model_loss(mmh_handle model, const int32_t *inputs_host,
+                       const int32_t *targets_host, int64_t batch, int64_t seq,
+                       float *loss_host);
+/* forward + loss in one pass; logits_host may be NULL. Tolerances against the
+ * reference CPU path: loss <= 1e-4 relative; logits max|diff| per row
+ * <= 1e-3 * max|row|. */
+int32_t mmh_model_forward_loss(mmh_handle model, const int32_t *inputs_host,
+                               const int32_t *targets_host, int64_t batch, int64_t seq,
+                               float *logits_host, float *loss_host);
+int32_t mmh_model_destroy(mmh_handle model);
+
+/* Device-resident steps (no reference counterpart: the reference has no
+ * device; these split model.rs:174's loss into upload / run / read so a caller
+ * can keep the tokens in HBM and queue steps without host round trips).
+ * stage validates the ids on the host (MMH_ERR_INDEX for id >= V) and copies
+ * them into the model's token buffers; run_staged queues forward + loss on
+ * them and returns without waiting; read_loss waits and returns the loss of
+ * the last staged run. */
+int32_t mmh_model_stage(mmh_handle model, const int32_t *inputs_host,
+                        const int32_t *targets_host, int64_t batch, int64_t seq);
+int32_t mmh_model_run_staged(mmh_handle model, int64_t batch, int64_t seq);
+int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
+
+/* Kernel classes timed by mmh_model_profile. */
+#define MMH_PROF_EMBEDDING 0
+#define MMH_PROF_RMS_NORM 1
+#define MMH_PROF_GEMM_QKV 2
+#define MMH_PROF_GEMM_O 3
+#define MMH_PROF_GEMM_GATE_UP 4
+#define MMH_PROF_GEMM_DOWN 5
+#define MMH_PROF_GEMM_HEAD 6
+#define MMH_PROF_ATTENTION 7
+#define MMH_PROF_LOSS 8
+#define MMH_PROF_CLASSES 9
+/* One staged forward + loss with a HIP event pair around every launch (the
+ * analogue of forward_traced for timing, model.rs:116-125): per class, the
+ * summed milliseconds and the number of launches. Arrays hold
+ * MMH_PROF_CLASSES entries. */
+int32_t mmh_model_profile(mmh_handle model, int64_t batch, int64_t seq, float *class_ms,
+                          int32_t *class_launches);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,31 @@
+// Host-only declarations (no HIP headers), shared by host_math.cpp (built with
+// g++) and the HIP translation units.
+#pragma once
+
+#include <cstdint>
+
+namespace mmh {
+
+// midman-foundation/src/rng.rs restated: SplitMix64 seeding, xoshiro256**,
+// Box-Muller normals with a cached spare, Lemire's below().
+struct HostRng {
+    uint64_t s[4];
+    bool has_spare = false;
+    float spare = 0.0f;
+    static HostRng seed(uint64_t seed);
+    uint64_t next_u64();
+    double next_f64();
+    float normal();
+    uint64_t below(uint64_t n);
+};
+
+// Tensor::randn (tensor.rs:158-162) for n values: dst[i] = std * normal(),
+// the same bits as the sequential loop, with the transcendental work spread
+// over threads.
+void randn_parallel(HostRng &rng, float *dst, int64_t n, float stdv);
+
+// RotaryTables::new (rope.rs:54-85): [max_seq_len, head_dim/2] cos and sin.
+void rope_tables_host(int64_t head_dim, int64_t max_seq_len, float theta, float *cos_t,
+                      float *sin_t);
+
+}  // namespace mmh

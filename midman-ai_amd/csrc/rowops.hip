@@ -1,0 +1,311 @@
+// Bandwidth-bound kernels of the decoder path: embedding gather, RMSNorm,
+// residual add, silu*mul, RoPE, the cross-entropy loss and weight packing.
+//
+// Each reads its inputs once and writes its outputs once with float4 accesses
+// where the row length allows, and reduces within a wave64 with DPP/shuffles.
+// Element-wise arithmetic uses the explicitly rounded intrinsics
+// (__fmul_rn, __fadd_rn, ...) so that no multiply-add is contracted and each
+// operation rounds exactly where the reference's does; that makes the
+// embedding, RoPE and add bit-exact, and leaves RMSNorm and the loss differing
+// from the reference only by summation order.
+#include "mmh_internal.h"
+
+namespace mmh {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---- embedding: ops_shape.rs:249-257 ---------------------------------------
+__global__ __launch_bounds__(256) void embedding_kernel(const float *__restrict__ table,
+                                                        int64_t d, const int32_t *__restrict__ ids,
+                                                        int64_t n, float *__restrict__ out,
+                                                        int vec) {
+    const int64_t total = vec ? n * (d / 4) : n * d;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        if (vec) {
+            const int64_t d4 = d / 4, row = i / d4, c = i - row * d4;
+            const float4 v = reinterpret_cast<const float4 *>(table + (int64_t)ids[row] * d)[c];
+            reinterpret_cast<float4 *>(out + row * d)[c] = v;
+        } else {
+            const int64_t row = i / d, c = i - row * d;
+            out[i] = table[(int64_t)ids[row] * d + c];
+        }
+    }
+}
+
+// ---- RMSNorm: norm.rs:36-38 -------------------------------------------------
+// One wave per row: sum of squares (wave reduction), mean = sum * (1/d),
+// inv = (mean + eps)^(-1/2), out = (x * inv) * w.
+__global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__ x,
+                                                       const float *__restrict__ w, int64_t rows,
+                                                       int64_t d, float eps,
+                                                       float *__restrict__ out, int vec) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * d;
+    float *o = out + row * d;
+    float ss = 0.0f;
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        for (int64_t j = lane; j < d / 4; j += 64) {
+            const float4 v = x4[j];
+            ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
+            ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
+            ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));
+            ss = __fadd_rn(ss, __fmul_rn(v.w, v.w));
+        }
+    } else {
+        for (int64_t j = lane; j < d; j += 64) ss = __fadd_rn(ss, __fmul_rn(xr[j], xr[j]));
+    }
+    ss = wave_sum(ss);
+    const float mean = __fmul_rn(ss, __fdiv_rn(1.0f, (float)d));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    if (vec) {
+        const float4 *x4 = reinterpret_cast<const float4 *>(xr);
+        const float4 *w4 = reinterpret_cast<const float4 *>(w);
+        float4 *o4 = reinterpret_cast<float4 *>(o);
+        for (int64_t j = lane; j < d / 4; j += 64) {
+            const float4 v = x4[j], g = w4[j];
+            float4 r;
+            r.x = __fmul_rn(__fmul_rn(v.x, inv), g.x);
+            r.y = __fmul_rn(__fmul_rn(v.y, inv), g.y);
+            r.z = __fmul_rn(__fmul_rn(v.z, inv), g.z);
+            r.w = __fmul_rn(__fmul_rn(v.w, inv), g.w);
+            o4[j] = r;
+        }
+    } else {
+        for (int64_t j = lane; j < d; j += 64) o[j] = __fmul_rn(__fmul_rn(xr[j], inv), w[j]);
+    }
+}
+
+// ---- add: ops_elementwise.rs:249-259 (same-shape path) -----------------------
+__global__ __launch_bounds__(256) void add_kernel(const float *__restrict__ a,
+                                                  const float *__restrict__ b,
+                                                  float *__restrict__ out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        out[i] = __fadd_rn(a[i], b[i]);
+}
+
+// ---- silu(g) * u: mlp.rs:21-23 ---------------------------------------------
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float *__restrict__ g,
+                                                       const float *__restrict__ u,
+                                                       float *__restrict__ out, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float x = g[i];
+        const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
+        out[i] = __fmul_rn(__fmul_rn(x, s), u[i]);
+    }
+}
+
+// ---- RoPE: rope.rs:28-32 (rotate-half) ---------------------------------------
+__global__ __launch_bounds__(256) void rope_kernel(const float *__restrict__ x, int64_t bh,
+                                                   int64_t t, int64_t hd,
+                                                   const float *__restrict__ cos_t,
+                                                   const float *__restrict__ sin_t,
+                                                   float *__restrict__ out) {
+    const int64_t half = hd / 2, total = bh * t * half;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t row = i / half, c = i - row * half;
+        const int64_t pos = row % t;
+        const float *xr = x + row * hd;
+        const float x1 = xr[c], x2 = xr[c + half];
+        const float cs = cos_t[pos * half + c], sn = sin_t[pos * half + c];
+        out[row * hd + c] = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
+        out[row * hd + c + half] = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
+    }
+}
+
+// ---- cross-entropy: ops_reduce.rs:253-259 --------------------------------------
+// One workgroup per row, one pass over the logits: each thread keeps a running
+// (max, sum of exp(z - max)) pair that is rescaled when the max grows; pairs
+// merge across the workgroup. The row term is formed as the reference forms it,
+// (max + ln(sum)) - z[target], in f32.
+__device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2) {
+    if (m2 == -INFINITY) return;
+    if (m == -INFINITY) {
+        m = m2;
+        s = s2;
+        return;
+    }
+    if (m2 > m) {
+        s = __fadd_rn(__fmul_rn(s, expf(m - m2)), s2);
+        m = m2;
+    } else {
+        s = __fadd_rn(s, __fmul_rn(s2, expf(m2 - m)));
+    }
+}
+
+__global__ __launch_bounds__(256) void ce_rows_kernel(const float *__restrict__ logits,
+                                                      const int32_t *__restrict__ targets,
+                                                      int64_t n, int64_t v,
+                                                      float *__restrict__ row_loss, int vec) {
+    const int64_t row = blockIdx.x;
+    const float *z = logits + row * v;
+    float m = -INFINITY, s = 0.0f;
+    auto add = [&](float x) {
+        if (x > m) {
+            s = (m == -INFINITY) ? 1.0f : __fadd_rn(__fmul_rn(s, expf(m - x)), 1.0f);
+            m = x;
+        } else {
+            s = __fadd_rn(s, expf(x - m));
+        }
+    };
+    if (vec) {
+        const float4 *z4 = reinterpret_cast<const float4 *>(z);
+        for (int64_t j = threadIdx.x; j < v / 4; j += 256) {
+            const float4 q = z4[j];
+            add(q.x);
+            add(q.y);
+            add(q.z);
+            add(q.w);
+        }
+    } else {
+        for (int64_t j = threadIdx.x; j < v; j += 256) add(z[j]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
+        lse_merge(m, s, m2, s2);
+    }
+    __shared__ float sm[4], ss[4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+        sm[wave] = m;
+        ss[wave] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float M = sm[0], S = ss[0];
+        for (int i = 1; i < 4; ++i) lse_merge(M, S, sm[i], ss[i]);
+        const float lse = __fadd_rn(M, logf(S));
+        row_loss[row] = __fsub_rn(lse, z[targets[row]]);
+    }
+}
+
+// Mean of the row terms in f64 (ops_reduce.rs:258-259), fixed reduction order.
+__global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__ row_loss,
+                                                       int64_t n, float *__restrict__ out) {
+    __shared__ double part[256];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)row_loss[i];
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if ((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = (float)(part[0] / (double)n);
+}
+
+// ---- weight packing (model creation) ------------------------------------------
+__global__ __launch_bounds__(256) void pack_cols_kernel(const float *__restrict__ src,
+                                                        int64_t rows, int64_t cols,
+                                                        float *__restrict__ dst, int64_t ld_dst,
+                                                        int64_t col_off) {
+    const int64_t total = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c = i - r * cols;
+        dst[r * ld_dst + col_off + c] = src[i];
+    }
+}
+
+// dst [rows, 2*ff_pad]: column 64g+c is gate column 32g+c (c < 32) and column
+// 64g+32+c is up column 32g+c; columns past ff are zero.
+__global__ __launch_bounds__(256) void pack_gate_up_kernel(const float *__restrict__ wg,
+                                                           const float *__restrict__ wu,
+                                                           int64_t rows, int64_t ff,
+                                                           int64_t ff_pad,
+                                                           float *__restrict__ dst) {
+    const int64_t cols = 2 * ff_pad, total = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c2 = i - r * cols;
+        const int64_t g = c2 >> 6, c = c2 & 63;
+        const int64_t col = g * 32 + (c & 31);
+        const float *src = c < 32 ? wg : wu;
+        dst[i] = col < ff ? src[r * ff + col] : 0.0f;
+    }
+}
+
+unsigned grid_for(int64_t work, int per_block = 256) {
+    int64_t b = (work + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > 65536) b = 65536;
+    return (unsigned)b;
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+void launch_embedding(Context &ctx, const float *table, int64_t d, const int32_t *ids_dev,
+                      int64_t n, float *out) {
+    const int vec = (d % 4 == 0) && al16(table) && al16(out);
+    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(vec ? n * d / 4 : n * d)), dim3(256), 0,
+                       ctx.stream, table, d, ids_dev, n, out, vec);
+    check_hip(hipGetLastError(), "embedding launch");
+}
+
+void launch_rms_norm(Context &ctx, const float *x, const float *w, int64_t rows, int64_t d,
+                     float eps, float *out) {
+    const int vec = (d % 4 == 0) && al16(x) && al16(w) && al16(out);
+    hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       ctx.stream, x, w, rows, d, eps, out, vec);
+    check_hip(hipGetLastError(), "rms_norm launch");
+}
+
+void launch_add(Context &ctx, const float *a, const float *b, float *out, int64_t n) {
+    hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, ctx.stream, a, b, out, n);
+    check_hip(hipGetLastError(), "add launch");
+}
+
+void launch_silu_mul(Context &ctx, const float *g, const float *u, float *out, int64_t n) {
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n)), dim3(256), 0, ctx.stream, g, u, out,
+                       n);
+    check_hip(hipGetLastError(), "silu_mul launch");
+}
+
+void launch_rope(Context &ctx, const float *x, int64_t bh, int64_t t, int64_t hd,
+                 const float *cos_t, const float *sin_t, float *out) {
+    hipLaunchKernelGGL(rope_kernel, dim3(grid_for(bh * t * (hd / 2))), dim3(256), 0, ctx.stream,
+                       x, bh, t, hd, cos_t, sin_t, out);
+    check_hip(hipGetLastError(), "rope launch");
+}
+
+void launch_cross_entropy(Context &ctx, const float *logits, const int32_t *targets_dev,
+                          int64_t n, int64_t v, float *row_loss, float *loss_dev) {
+    if (n > 0x7fffffff) fail(MMH_ERR_SHAPE, "cross_entropy: too many rows");
+    const int vec = (v % 4 == 0) && al16(logits);
+    hipLaunchKernelGGL(ce_rows_kernel, dim3((unsigned)n), dim3(256), 0, ctx.stream, logits,
+                       targets_dev, n, v, row_loss, vec);
+    check_hip(hipGetLastError(), "cross_entropy launch");
+    hipLaunchKernelGGL(mean_f64_kernel, dim3(1), dim3(256), 0, ctx.stream, row_loss, n,
+                       loss_dev);
+    check_hip(hipGetLastError(), "loss mean launch");
+}
+
+void launch_pack_cols(Context &ctx, const float *src, int64_t rows, int64_t cols, float *dst,
+                      int64_t ld_dst, int64_t col_off) {
+    hipLaunchKernelGGL(pack_cols_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, ctx.stream,
+                       src, rows, cols, dst, ld_dst, col_off);
+    check_hip(hipGetLastError(), "pack launch");
+}
+
+void launch_pack_gate_up(Context &ctx, const float *wg, const float *wu, int64_t rows,
+                         int64_t ff, int64_t ff_pad, float *dst) {
+    hipLaunchKernelGGL(pack_gate_up_kernel, dim3(grid_for(rows * 2 * ff_pad)), dim3(256), 0,
+                       ctx.stream, wg, wu, rows, ff, ff_pad, dst);
+    check_hip(hipGetLastError(), "pack launch");
+}
+
+}  // namespace mmh

@@ -1,0 +1,522 @@
+"""Python host side of libmidman_hip.so, over its C ABI (include/midman_hip.h).
+
+Mirrors the reference's operator surface for the decoder path
+(midman-tensor matmul and its backward, midman-nn's rms_norm / apply_rope /
+causal_attention / attention_forward / swiglu / embedding, cross_entropy, and
+MidManModel::{new, forward, loss}) with the same argument meaning and the same
+error kinds (midman-foundation/src/error.rs:18-65): a bad argument raises
+ArgumentError, a bad config ConfigError, mismatched sizes ShapeError, an id or
+target >= vocab IndexOutOfRange, and a HIP failure DeviceError.
+
+There is no CPU fallback: if the library is not built, importing works but
+every call raises LibraryMissing.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional, Sequence
+
+import numpy as np
+
+_PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(_PKG_DIR, "libmidman_hip.so")
+HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "midman_hip.h")
+
+OK, STOPPED = 0, 1
+ERR_ARGUMENT, ERR_CONFIG, ERR_SHAPE, ERR_INDEX, ERR_OTHER, ERR_DEVICE, ERR_PANIC = (
+    -1, -2, -3, -4, -5, -6, -99)
+
+
+class MidmanError(Exception):
+    """A non-zero status from the library, with its message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+        self.message = message
+
+
+class ArgumentError(MidmanError, ValueError):
+    pass
+
+
+class ConfigError(MidmanError, ValueError):
+    pass
+
+
+class ShapeError(MidmanError, ValueError):
+    pass
+
+
+class IndexOutOfRange(MidmanError, IndexError):
+    pass
+
+
+class DeviceError(MidmanError, RuntimeError):
+    pass
+
+
+class LibraryMissing(RuntimeError):
+    pass
+
+
+_ERRORS = {ERR_ARGUMENT: ArgumentError, ERR_CONFIG: ConfigError, ERR_SHAPE: ShapeError,
+           ERR_INDEX: IndexOutOfRange, ERR_DEVICE: DeviceError}
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_vp = ctypes.c_void_p
+_h = ctypes.c_int64
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+# name -> argtypes (all return int32 unless listed in _RESTYPES)
+_SIGNATURES = {
+    "mmh_abi_version": [],
+    "mmh_error_ptr": [],
+    "mmh_error_len": [],
+    "mmh_context_create": [_i32, ctypes.POINTER(_h)],
+    "mmh_context_destroy": [_h],
+    "mmh_synchronize": [_h],
+    "mmh_device_info": [_h, ctypes.c_char_p, ctypes.c_uint32, ctypes.POINTER(_i32)],
+    "mmh_alloc": [_h, ctypes.c_uint64, ctypes.POINTER(_vp)],
+    "mmh_free": [_h, _vp],
+    "mmh_upload": [_h, _vp, _vp, ctypes.c_uint64],
+    "mmh_download": [_h, _vp, _vp, ctypes.c_uint64],
+    "mmh_timer_start": [_h],
+    "mmh_timer_stop": [_h, ctypes.POINTER(ctypes.c_float)],
+    "mmh_randn": [ctypes.c_uint64, ctypes.c_float, _f32p, _i64],
+    "mmh_gemm_nn": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
+    "mmh_gemm_nt": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
+    "mmh_gemm_tn": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
+    "mmh_matmul_batched": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i64],
+    "mmh_matmul_backward": [_h, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64],
+    "mmh_embedding": [_h, _vp, _i64, _i64, _i32p, _i64, _vp],
+    "mmh_rms_norm": [_h, _vp, _vp, _i64, _i64, ctypes.c_float, _vp],
+    "mmh_rope_tables": [_h, _i64, _i64, ctypes.c_float, _vp, _vp],
+    "mmh_apply_rope": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
+    "mmh_causal_attention": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
+    "mmh_attention_forward": [_h, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                              _i64, _vp],
+    "mmh_swiglu": [_h, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "mmh_add": [_h, _vp, _vp, _vp, _i64],
+    "mmh_cross_entropy": [_h, _vp, _i32p, _i64, _i64, _f32p],
+    "mmh_model_create": [_h, ctypes.POINTER(ctypes.c_double), _f32p, _i64, ctypes.POINTER(_h)],
+    "mmh_model_create_seeded": [_h, ctypes.POINTER(ctypes.c_double), ctypes.c_uint64,
+                                ctypes.c_float, ctypes.POINTER(_h)],
+    "mmh_model_lab_tokens": [_h, _i64, _i64, _i32p, _i32p],
+    "mmh_model_param_count": [_h, ctypes.POINTER(_i64)],
+    "mmh_model_download_weights": [_h, _f32p, _i64],
+    "mmh_model_forward": [_h, _i32p, _i64, _i64, _f32p],
+    "mmh_model_loss": [_h, _i32p, _i32p, _i64, _i64, _f32p],
+    "mmh_model_forward_loss": [_h, _i32p, _i32p, _i64, _i64, _f32p, _f32p],
+    "mmh_model_destroy": [_h],
+    "mmh_model_stage": [_h, _i32p, _i32p, _i64, _i64],
+    "mmh_model_run_staged": [_h, _i64, _i64],
+    "mmh_model_read_loss": [_h, _f32p],
+    "mmh_model_profile": [_h, _i64, _i64, _f32p, _i32p],
+}
+
+PROFILE_CLASSES = ("embedding", "rms_norm", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down",
+                   "gemm_head", "attention", "loss")
+_RESTYPES = {"mmh_abi_version": ctypes.c_uint32, "mmh_error_ptr": ctypes.c_void_p,
+             "mmh_error_len": ctypes.c_uint32}
+
+_lib = None
+
+
+def lib():
+    """The loaded libmidman_hip.so; raises LibraryMissing if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise LibraryMissing(
+                f"{LIB_PATH} is not built (run python midman-ai_amd/build.py); "
+                "there is no CPU fallback")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, _i32)
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    L = lib()
+    n = L.mmh_error_len()
+    p = L.mmh_error_ptr()
+    return ctypes.string_at(p, n).decode("utf-8", "replace") if n else ""
+
+
+def check(status: int) -> int:
+    if status < 0:
+        raise _ERRORS.get(status, MidmanError)(status, last_error())
+    return status
+
+
+def abi_version() -> int:
+    return lib().mmh_abi_version()
+
+
+def randn(shape, std: float, seed: int) -> np.ndarray:
+    """Tensor::randn(shape, std, &mut Rng::seed_from_u64(seed)) on the host."""
+    shape = tuple(shape) if isinstance(shape, (tuple, list)) else (shape,)
+    out = np.empty(shape, np.float32)
+    check(lib().mmh_randn(seed, std, out.ctypes.data_as(_f32p), out.size))
+    return out
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+def _ip(a: np.ndarray):
+    return a.ctypes.data_as(_i32p)
+
+
+class Context:
+    """One GPU and one HIP stream (mmh_context_*)."""
+
+    def __init__(self, device: int = 0):
+        h = _h()
+        check(lib().mmh_context_create(device, ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self):
+        if getattr(self, "handle", 0):
+            check(lib().mmh_context_destroy(self.handle))
+            self.handle = 0
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def synchronize(self):
+        check(lib().mmh_synchronize(self.handle))
+
+    def device_info(self):
+        buf = ctypes.create_string_buffer(256)
+        cu = _i32()
+        check(lib().mmh_device_info(self.handle, buf, 256, ctypes.byref(cu)))
+        return buf.value.decode(), cu.value
+
+    def empty(self, shape, dtype=np.float32) -> "DeviceArray":
+        return DeviceArray(self, shape, dtype)
+
+    def to_device(self, a: np.ndarray) -> "DeviceArray":
+        a = np.ascontiguousarray(a)
+        d = DeviceArray(self, a.shape, a.dtype)
+        d.upload(a)
+        return d
+
+    def timer_start(self):
+        check(lib().mmh_timer_start(self.handle))
+
+    def timer_stop(self) -> float:
+        ms = ctypes.c_float()
+        check(lib().mmh_timer_stop(self.handle, ctypes.byref(ms)))
+        return ms.value
+
+
+class DeviceArray:
+    """A device buffer from mmh_alloc with a shape and dtype."""
+
+    def __init__(self, ctx: Context, shape, dtype=np.float32):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.size = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = self.size * self.dtype.itemsize
+        p = _vp()
+        check(lib().mmh_alloc(ctx.handle, max(self.nbytes, 1), ctypes.byref(p)))
+        self.ptr = p.value
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.size == self.size, (a.shape, self.shape)
+        check(lib().mmh_upload(self.ctx.handle, self.ptr, a.ctypes.data, self.nbytes))
+
+    def numpy(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        check(lib().mmh_download(self.ctx.handle, out.ctypes.data, self.ptr, self.nbytes))
+        return out
+
+    def free(self):
+        if self.ptr:
+            check(lib().mmh_free(self.ctx.handle, self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and getattr(self.ctx, "handle", 0):
+                lib().mmh_free(self.ctx.handle, self.ptr)
+        except Exception:
+            pass
+
+    def offset(self, elements: int) -> int:
+        return self.ptr + elements * self.dtype.itemsize
+
+
+def _ptr(x):
+    if x is None:
+        return None
+    return x.ptr if isinstance(x, DeviceArray) else x
+
+
+# ---- the GEMM seam: kernels.rs:49-84 -------------------------------------------
+
+def gemm(ctx: Context, form: str, a, b, c, m: int, k: int, n: int, accumulate: bool = False):
+    """C (+)= op(A) op(B) for form in {"nn", "nt", "tn"} (kernels.rs layouts)."""
+    fn = {"nn": "mmh_gemm_nn", "nt": "mmh_gemm_nt", "tn": "mmh_gemm_tn"}[form]
+    check(getattr(lib(), fn)(ctx.handle, _ptr(a), _ptr(b), _ptr(c), m, k, n,
+                             1 if accumulate else 0))
+
+
+def matmul(ctx: Context, a: DeviceArray, b: DeviceArray) -> DeviceArray:
+    """Tensor::matmul (ops_matmul.rs:34): [.., m, k] x [k, n] or batched [b.., m, k] x [b.., k, n]."""
+    if len(a.shape) < 2 or len(b.shape) < 2:
+        raise ShapeError(ERR_SHAPE, "matmul: both operands need at least 2 axes")
+    m, k = a.shape[-2], a.shape[-1]
+    k2, n = b.shape[-2], b.shape[-1]
+    if k != k2:
+        raise ShapeError(ERR_SHAPE, f"matmul: inner dimensions differ: {a.shape} x {b.shape}")
+    if len(b.shape) == 2:
+        rows = a.size // k
+        out = ctx.empty(a.shape[:-1] + (n,))
+        gemm(ctx, "nn", a, b, out, rows, k, n)
+        return out
+    if a.shape[:-2] != b.shape[:-2]:
+        raise ShapeError(ERR_SHAPE, "matmul: batched operands need the same leading axes")
+    batch = int(np.prod(a.shape[:-2]))
+    out = ctx.empty(a.shape[:-2] + (m, n))
+    check(lib().mmh_matmul_batched(ctx.handle, a.ptr, b.ptr, out.ptr, batch, m, k, n))
+    return out
+
+
+def matmul_backward(ctx: Context, a, b, dc, rows: int, k: int, n: int, da=None, db=None):
+    """The matmul backward closure (ops_matmul.rs:62-74): dA = dC B^T, dB = A^T dC."""
+    check(lib().mmh_matmul_backward(ctx.handle, _ptr(a), _ptr(b), _ptr(dc), _ptr(da), _ptr(db),
+                                    rows, k, n))
+
+
+# ---- layer ops: midman-nn/src/lib.rs:45-56 --------------------------------------
+
+def embedding(ctx: Context, table: DeviceArray, ids: np.ndarray, out: DeviceArray = None):
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    V, d = table.shape
+    out = out or ctx.empty(ids.shape + (d,))
+    check(lib().mmh_embedding(ctx.handle, table.ptr, V, d, _ip(ids), ids.size, out.ptr))
+    return out
+
+
+def rms_norm(ctx: Context, x: DeviceArray, w: DeviceArray, eps: float, out: DeviceArray = None):
+    d = x.shape[-1]
+    if w.shape != (d,):
+        raise ShapeError(ERR_SHAPE, f"rms_norm: weight must have shape [{d}], got {w.shape}")
+    out = out or ctx.empty(x.shape)
+    check(lib().mmh_rms_norm(ctx.handle, x.ptr, w.ptr, x.size // d, d, eps, out.ptr))
+    return out
+
+
+class RotaryTables:
+    """RotaryTables::new (rope.rs:54-85) on the device."""
+
+    def __init__(self, ctx: Context, head_dim: int, max_seq_len: int, theta: float = 10000.0):
+        self.head_dim, self.max_seq_len = head_dim, max_seq_len
+        self.cos = ctx.empty((max_seq_len, head_dim // 2))
+        self.sin = ctx.empty((max_seq_len, head_dim // 2))
+        check(lib().mmh_rope_tables(ctx.handle, head_dim, max_seq_len, theta, self.cos.ptr,
+                                    self.sin.ptr))
+
+
+def apply_rope(ctx: Context, x: DeviceArray, tables: RotaryTables, out: DeviceArray = None):
+    """RotaryTables::apply (rope.rs:114-128): x [.., T, hd], positions 0..T-1."""
+    t, hd = x.shape[-2], x.shape[-1]
+    if t > tables.max_seq_len:
+        raise ShapeError(ERR_SHAPE, "rope: sequence longer than the tables")
+    out = out or ctx.empty(x.shape)
+    check(lib().mmh_apply_rope(ctx.handle, x.ptr, x.size // (t * hd), t, hd, tables.cos.ptr,
+                               tables.sin.ptr, out.ptr))
+    return out
+
+
+def causal_attention(ctx: Context, q: DeviceArray, k: DeviceArray, v: DeviceArray,
+                     out: DeviceArray = None):
+    """attention.rs:97-101: q [B,H,T,hd], k/v [B,Hkv,T,hd] -> [B,H,T,hd]."""
+    if len(q.shape) != 4 or len(k.shape) != 4 or k.shape != v.shape:
+        raise ShapeError(ERR_SHAPE, "causal_attention: expected q [B,H,T,D] and k, v [B,Hkv,T,D]")
+    B, H, T, hd = q.shape
+    if k.shape[0] != B or k.shape[2] != T or k.shape[3] != hd:
+        raise ShapeError(ERR_SHAPE, "causal_attention: q and k disagree on batch, time or head size")
+    out = out or ctx.empty(q.shape)
+    check(lib().mmh_causal_attention(ctx.handle, q.ptr, k.ptr, v.ptr, B, H, k.shape[1], T, hd,
+                                     out.ptr))
+    return out
+
+
+def attention_forward(ctx: Context, x: DeviceArray, wq, wk, wv, wo, n_heads: int,
+                      n_kv_heads: int, tables: RotaryTables, out: DeviceArray = None):
+    """attention.rs:146-170: x [B,T,d] -> [B,T,d]."""
+    B, T, d = x.shape
+    out = out or ctx.empty(x.shape)
+    check(lib().mmh_attention_forward(ctx.handle, x.ptr, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(wo),
+                                      tables.cos.ptr, tables.sin.ptr, B, T, d, n_heads,
+                                      n_kv_heads, out.ptr))
+    return out
+
+
+def swiglu(ctx: Context, x: DeviceArray, wg: DeviceArray, wu: DeviceArray, wd: DeviceArray,
+           out: DeviceArray = None):
+    """mlp.rs:20-24: (silu(x Wg) * (x Wu)) Wd."""
+    d = x.shape[-1]
+    ff = wg.shape[1]
+    out = out or ctx.empty(x.shape)
+    check(lib().mmh_swiglu(ctx.handle, x.ptr, wg.ptr, wu.ptr, wd.ptr, x.size // d, d, ff, out.ptr))
+    return out
+
+
+def add(ctx: Context, a: DeviceArray, b: DeviceArray, out: DeviceArray = None):
+    if a.shape != b.shape:
+        raise ShapeError(ERR_SHAPE, f"add: shapes {a.shape} and {b.shape} differ")
+    out = out or ctx.empty(a.shape)
+    check(lib().mmh_add(ctx.handle, a.ptr, b.ptr, out.ptr, a.size))
+    return out
+
+
+def cross_entropy(ctx: Context, logits: DeviceArray, targets: np.ndarray) -> float:
+    """Tensor::cross_entropy (ops_reduce.rs:236-259): mean over rows, f64 accumulation."""
+    if len(logits.shape) != 2:
+        raise ShapeError(ERR_SHAPE, f"cross_entropy: logits must have shape [N, V], got {logits.shape}")
+    n, v = logits.shape
+    targets = np.ascontiguousarray(targets, dtype=np.int32)
+    if targets.size != n:
+        raise ShapeError(ERR_SHAPE, f"cross_entropy: {n} logit rows but {targets.size} targets")
+    loss = ctypes.c_float()
+    check(lib().mmh_cross_entropy(ctx.handle, logits.ptr, _ip(targets), n, v, ctypes.byref(loss)))
+    return loss.value
+
+
+# ---- the model: midman-model/src/model.rs ------------------------------------------
+
+CONFIG_FIELDS = ("vocab_size", "d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff",
+                 "max_seq_len", "rope_theta", "norm_eps", "tie_embeddings")
+
+# presets.rs:52-83 at their default vocabularies
+PRESETS = {
+    "smoke": [256, 64, 2, 4, 4, 176, 128, 10000.0, 1e-5, 1],
+    "tiny": [4096, 128, 4, 4, 4, 344, 256, 10000.0, 1e-5, 1],
+    "small": [32000, 384, 6, 6, 6, 1024, 512, 10000.0, 1e-5, 1],
+    "base": [32000, 768, 12, 12, 12, 2048, 1024, 10000.0, 1e-5, 1],
+    "medium": [32000, 1024, 24, 16, 8, 2816, 2048, 10000.0, 1e-5, 1],
+    "large": [32000, 2048, 20, 16, 8, 5632, 2048, 10000.0, 1e-5, 1],
+}
+
+
+def _config_array(config: Sequence[float]):
+    if len(config) != 10:
+        raise ArgumentError(ERR_ARGUMENT, "a config is 10 numbers (ffi.rs:27-32)")
+    return (ctypes.c_double * 10)(*[float(v) for v in config])
+
+
+class Model:
+    """MidManModel on the device."""
+
+    def __init__(self, ctx: Context, handle: int, config):
+        self.ctx, self.handle, self.config = ctx, handle, list(config)
+        self.vocab_size = int(config[0])
+
+    @classmethod
+    def new(cls, ctx: Context, config, seed: int, std: float = 0.02) -> "Model":
+        """MidManModel::with_init_std(config, std, Rng::seed_from_u64(seed))."""
+        h = _h()
+        check(lib().mmh_model_create_seeded(ctx.handle, _config_array(config), seed, std,
+                                            ctypes.byref(h)))
+        return cls(ctx, h.value, config)
+
+    @classmethod
+    def from_weights(cls, ctx: Context, config, weights: np.ndarray) -> "Model":
+        w = np.ascontiguousarray(weights, dtype=np.float32)
+        h = _h()
+        check(lib().mmh_model_create(ctx.handle, _config_array(config), _fp(w), w.size,
+                                     ctypes.byref(h)))
+        return cls(ctx, h.value, config)
+
+    def lab_tokens(self, batch: int, seq: int):
+        """Lab::new's task (lab.rs:194-203), continuing the model's Rng."""
+        x = np.empty(batch * seq, np.int32)
+        y = np.empty(batch * seq, np.int32)
+        check(lib().mmh_model_lab_tokens(self.handle, batch, seq, _ip(x), _ip(y)))
+        return x, y
+
+    def num_parameters(self) -> int:
+        n = _i64()
+        check(lib().mmh_model_param_count(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def weights(self) -> np.ndarray:
+        n = self.num_parameters()
+        out = np.empty(n, np.float32)
+        check(lib().mmh_model_download_weights(self.handle, _fp(out), n))
+        return out
+
+    def forward(self, ids, batch: int, seq: int) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        if ids.size != batch * seq:
+            raise ArgumentError(ERR_ARGUMENT,
+                                f"forward: {ids.size} ids do not fill {batch} sequences of {seq} tokens")
+        out = np.empty((batch, seq, self.vocab_size), np.float32)
+        check(lib().mmh_model_forward(self.handle, _ip(ids), batch, seq, _fp(out)))
+        return out
+
+    def loss(self, inputs, targets, batch: int, seq: int) -> float:
+        x, y = self._pair(inputs, targets, batch, seq)
+        loss = ctypes.c_float()
+        check(lib().mmh_model_loss(self.handle, _ip(x), _ip(y), batch, seq, ctypes.byref(loss)))
+        return loss.value
+
+    def forward_loss(self, inputs, targets, batch: int, seq: int, want_logits: bool = True):
+        x, y = self._pair(inputs, targets, batch, seq)
+        logits = np.empty((batch, seq, self.vocab_size), np.float32) if want_logits else None
+        loss = ctypes.c_float()
+        check(lib().mmh_model_forward_loss(self.handle, _ip(x), _ip(y), batch, seq,
+                                           _fp(logits) if want_logits else None,
+                                           ctypes.byref(loss)))
+        return loss.value, logits
+
+    def _pair(self, inputs, targets, batch, seq):
+        x = np.ascontiguousarray(inputs, dtype=np.int32)
+        y = np.ascontiguousarray(targets, dtype=np.int32)
+        if x.size != batch * seq or y.size != batch * seq:
+            raise ArgumentError(ERR_ARGUMENT, "inputs/targets do not hold batch * seq ids")
+        return x, y
+
+    def stage(self, inputs, targets, batch: int, seq: int):
+        """Validates and copies the ids into the model's device buffers."""
+        x, y = self._pair(inputs, targets, batch, seq)
+        check(lib().mmh_model_stage(self.handle, _ip(x), _ip(y), batch, seq))
+
+    def run_staged(self, batch: int, seq: int):
+        """Queues forward + loss on the staged ids; does not wait."""
+        check(lib().mmh_model_run_staged(self.handle, batch, seq))
+
+    def read_loss(self) -> float:
+        loss = ctypes.c_float()
+        check(lib().mmh_model_read_loss(self.handle, ctypes.byref(loss)))
+        return loss.value
+
+    def profile(self, batch: int, seq: int) -> dict:
+        """One staged run with per-launch HIP events: {class: (ms, launches)}."""
+        n = len(PROFILE_CLASSES)
+        ms = (ctypes.c_float * n)()
+        cnt = (ctypes.c_int32 * n)()
+        check(lib().mmh_model_profile(self.handle, batch, seq, ms, cnt))
+        return {name: (ms[i], cnt[i]) for i, name in enumerate(PROFILE_CLASSES)}
+
+    def close(self):
+        if self.handle:
+            check(lib().mmh_model_destroy(self.handle))
+            self.handle = 0

@@ -1,0 +1,378 @@
+"""ctypes binding of the CPU oracle (oracle/libmm_oracle.so).
+
+TEST INFRASTRUCTURE ONLY. The oracle restates the reference's CPU algorithm
+(midman-ai, Rust) op for op and is the parity checker for the HIP path and
+the CPU timing baseline. Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module; the product never does.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libmm_oracle.so")
+_REF_PATH = os.path.join(_HERE, "_ref", "libmmb_ref.so")
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64 = ctypes.c_int64
+_i32 = ctypes.c_int32
+
+OK, ERR_ARGUMENT, ERR_CONFIG, ERR_SHAPE, ERR_INDEX = 0, -1, -2, -3, -4
+PRESETS = ("smoke", "tiny", "small", "base", "medium", "large")
+
+
+class Rng(ctypes.Structure):
+    """mmo_rng: xoshiro256** state plus the cached Box-Muller spare."""
+
+    _fields_ = [("s", ctypes.c_uint64 * 4), ("has_spare", ctypes.c_int32),
+                ("spare", ctypes.c_float)]
+
+
+class Config(ctypes.Structure):
+    """mmo_config, the reference ModelConfig (config.rs:20-43)."""
+
+    _fields_ = [("vocab_size", _i64), ("d_model", _i64), ("n_layers", _i64),
+                ("n_heads", _i64), ("n_kv_heads", _i64), ("d_ff", _i64),
+                ("max_seq_len", _i64), ("rope_theta", ctypes.c_float),
+                ("norm_eps", ctypes.c_float), ("tie_embeddings", ctypes.c_int32)]
+
+    def as_list(self):
+        """The reference's 10-field config order (ffi.rs:68-79)."""
+        return [self.vocab_size, self.d_model, self.n_layers, self.n_heads,
+                self.n_kv_heads, self.d_ff, self.max_seq_len, float(self.rope_theta),
+                float(self.norm_eps), int(self.tie_embeddings)]
+
+    @property
+    def head_dim(self):
+        return self.d_model // self.n_heads
+
+    @property
+    def kv_dim(self):
+        return self.n_kv_heads * self.head_dim
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(f"oracle not built: {_LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(_LIB_PATH)
+        R = ctypes.POINTER(Rng)
+        C = ctypes.POINTER(Config)
+        sig = {
+            "mmo_rng_seed": (None, [R, ctypes.c_uint64]),
+            "mmo_rng_next_u64": (ctypes.c_uint64, [R]),
+            "mmo_rng_next_f32": (ctypes.c_float, [R]),
+            "mmo_rng_next_f64": (ctypes.c_double, [R]),
+            "mmo_rng_normal": (ctypes.c_float, [R]),
+            "mmo_rng_below": (ctypes.c_uint64, [R, ctypes.c_uint64]),
+            "mmo_randn": (None, [R, _f32p, _i64, ctypes.c_float]),
+            "mmo_config_validate": (_i32, [C]),
+            "mmo_param_count": (_i64, [C]),
+            "mmo_preset": (_i32, [_i32, C]),
+            "mmo_init_weights": (_i32, [C, ctypes.c_float, R, _f32p, _i64]),
+            "mmo_lab_tokens": (None, [R, _i64, _i64, _i64, _i32p, _i32p]),
+            "mmo_gemm_nn": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i32]),
+            "mmo_gemm_nt": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i32]),
+            "mmo_gemm_tn": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i32]),
+            "mmo_matmul_backward": (None, [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, _i64,
+                                           _i64, _i32]),
+            "mmo_embedding": (_i32, [_f32p, _i64, _i64, _i32p, _i64, _f32p]),
+            "mmo_rms_norm": (None, [_f32p, _f32p, _i64, _i64, ctypes.c_float, _f32p]),
+            "mmo_rope_tables": (None, [_i64, _i64, ctypes.c_float, _f32p, _f32p]),
+            "mmo_apply_rope": (None, [_f32p, _i64, _i64, _i64, _f32p, _f32p, _f32p]),
+            "mmo_causal_attention": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i64,
+                                            _i64, _f32p, _i32]),
+            "mmo_attention_forward": (None, [_f32p] * 7 + [_i64] * 5 + [_f32p, _i32]),
+            "mmo_swiglu": (None, [_f32p] * 4 + [_i64] * 3 + [_f32p, _i32]),
+            "mmo_cross_entropy": (_i32, [_f32p, _i32p, _i64, _i64, _f32p]),
+            "mmo_cross_entropy_rows": (_i32, [_f32p, _i32p, _i64, _i64, _f32p]),
+            "mmo_block_forward": (_i32, [C, _f32p, _f32p, _f32p, _f32p, _i64, _i64, _f32p,
+                                         _i32]),
+            "mmo_forward": (_i32, [C, _f32p, _i32p, _i64, _i64, _f32p, _i32]),
+            "mmo_forward_loss": (_i32, [C, _f32p, _i32p, _i32p, _i64, _i64, _f32p, _f32p,
+                                        _i32]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def default_threads():
+    return max(1, min(8, os.cpu_count() or 1))
+
+
+def fp(a):
+    """float32 pointer of a C-contiguous array (or NULL for None)."""
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_f32p)
+
+
+def ip(a):
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_i32p)
+
+
+def f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+# ---- rng -----------------------------------------------------------------
+
+def rng(seed):
+    r = Rng()
+    lib().mmo_rng_seed(ctypes.byref(r), seed)
+    return r
+
+
+def normals(r, n, std=1.0):
+    """Tensor::randn(n, std) drawn from r (std * normal() in f32)."""
+    out = np.empty(n, np.float32)
+    lib().mmo_randn(ctypes.byref(r), fp(out), n, std)
+    return out
+
+
+def randn(shape, std, r):
+    """Tensor::randn(shape, std, rng) (tensor.rs:158-162)."""
+    return normals(r, int(np.prod(shape)), std).reshape(shape)
+
+
+# ---- config / init -------------------------------------------------------
+
+def preset(name):
+    c = Config()
+    assert lib().mmo_preset(PRESETS.index(name), ctypes.byref(c)) == OK
+    return c
+
+
+def config(vocab, d, layers, heads, kv_heads, ff, max_seq, theta=10000.0, eps=1e-5, tie=True):
+    return Config(vocab, d, layers, heads, kv_heads, ff, max_seq, theta, eps, 1 if tie else 0)
+
+
+def param_count(c):
+    return lib().mmo_param_count(ctypes.byref(c))
+
+
+def init_weights(c, r, std=0.02):
+    n = param_count(c)
+    w = np.empty(n, np.float32)
+    st = lib().mmo_init_weights(ctypes.byref(c), std, ctypes.byref(r), fp(w), n)
+    if st != OK:
+        raise ValueError(f"mmo_init_weights status {st}")
+    return w
+
+
+def lab_tokens(r, vocab, batch, seq):
+    inputs = np.empty(batch * seq, np.int32)
+    targets = np.empty(batch * seq, np.int32)
+    lib().mmo_lab_tokens(ctypes.byref(r), vocab, batch, seq, ip(inputs), ip(targets))
+    return inputs, targets
+
+
+def lab_setup(c, seed, batch, seq, std=0.02):
+    """Lab::new / overfit.rs memorize: weights then tokens from one stream."""
+    r = rng(seed)
+    w = init_weights(c, r, std)
+    inputs, targets = lab_tokens(r, c.vocab_size, batch, seq)
+    return w, inputs, targets
+
+
+def weight_views(c, w):
+    """Named views into the flat reference-order parameter vector."""
+    d, ff, kv, V = c.d_model, c.d_ff, c.kv_dim, c.vocab_size
+    out, o = {}, 0
+
+    def take(name, shape):
+        nonlocal o
+        n = int(np.prod(shape))
+        out[name] = w[o:o + n].reshape(shape)
+        o += n
+
+    take("embed_tokens.weight", (V, d))
+    for l in range(c.n_layers):
+        p = f"blocks.{l}."
+        take(p + "attn_norm.weight", (d,))
+        take(p + "attn.q_proj.weight", (d, d))
+        take(p + "attn.k_proj.weight", (d, kv))
+        take(p + "attn.v_proj.weight", (d, kv))
+        take(p + "attn.o_proj.weight", (d, d))
+        take(p + "mlp_norm.weight", (d,))
+        take(p + "mlp.gate_proj.weight", (d, ff))
+        take(p + "mlp.up_proj.weight", (d, ff))
+        take(p + "mlp.down_proj.weight", (ff, d))
+    take("final_norm.weight", (d,))
+    if not c.tie_embeddings:
+        take("lm_head.weight", (d, V))
+    assert o == w.size
+    return out
+
+
+# ---- ops -----------------------------------------------------------------
+
+def gemm(form, a, b, m, k, n, c=None, threads=None):
+    """C (+)= op(A) op(B); form in nn/nt/tn with the reference layouts."""
+    a, b = f32(a), f32(b)
+    out = np.zeros((m, n), np.float32) if c is None else f32(c).copy()
+    getattr(lib(), f"mmo_gemm_{form}")(fp(a), fp(b), fp(out), m, k, n,
+                                       threads or default_threads())
+    return out
+
+
+def matmul_backward(a, b, dc, rows, k, n, need_a=True, need_b=True, threads=None):
+    a, b, dc = f32(a), f32(b), f32(dc)
+    da = np.empty((rows, k), np.float32) if need_a else None
+    db = np.empty((k, n), np.float32) if need_b else None
+    lib().mmo_matmul_backward(fp(a), fp(b), fp(dc), fp(da), fp(db), rows, k, n,
+                              threads or default_threads())
+    return da, db
+
+
+def embedding(table, ids):
+    table, ids = f32(table), i32(ids)
+    V, d = table.shape
+    out = np.empty((ids.size, d), np.float32)
+    st = lib().mmo_embedding(fp(table), V, d, ip(ids), ids.size, fp(out))
+    if st != OK:
+        raise IndexError(f"embedding status {st}")
+    return out
+
+
+def rms_norm(x, w, eps):
+    x, w = f32(x), f32(w)
+    d = x.shape[-1]
+    out = np.empty_like(x)
+    lib().mmo_rms_norm(fp(x), fp(w), x.size // d, d, eps, fp(out))
+    return out
+
+
+def rope_tables(hd, max_seq, theta=10000.0):
+    half = hd // 2
+    cos = np.empty((max_seq, half), np.float32)
+    sin = np.empty((max_seq, half), np.float32)
+    lib().mmo_rope_tables(hd, max_seq, theta, fp(cos), fp(sin))
+    return cos, sin
+
+
+def apply_rope(x, cos, sin):
+    """x [..., T, hd]"""
+    x = f32(x)
+    t, hd = x.shape[-2], x.shape[-1]
+    out = np.empty_like(x)
+    lib().mmo_apply_rope(fp(x), x.size // (t * hd), t, hd, fp(f32(cos)), fp(f32(sin)), fp(out))
+    return out
+
+
+def causal_attention(q, k, v, threads=None):
+    q, k, v = f32(q), f32(k), f32(v)
+    B, H, T, hd = q.shape
+    out = np.empty_like(q)
+    lib().mmo_causal_attention(fp(q), fp(k), fp(v), B, H, k.shape[1], T, hd, fp(out),
+                               threads or default_threads())
+    return out
+
+
+def attention_forward(x, wq, wk, wv, wo, cos, sin, heads, kv_heads, threads=None):
+    x = f32(x)
+    B, T, d = x.shape
+    out = np.empty_like(x)
+    lib().mmo_attention_forward(fp(x), fp(f32(wq)), fp(f32(wk)), fp(f32(wv)), fp(f32(wo)),
+                                fp(f32(cos)), fp(f32(sin)), B, T, d, heads, kv_heads, fp(out),
+                                threads or default_threads())
+    return out
+
+
+def swiglu(x, wg, wu, wd, threads=None):
+    x = f32(x)
+    d = x.shape[-1]
+    ff = wg.shape[1]
+    out = np.empty_like(x)
+    lib().mmo_swiglu(fp(x), fp(f32(wg)), fp(f32(wu)), fp(f32(wd)), x.size // d, d, ff,
+                     fp(out), threads or default_threads())
+    return out
+
+
+def cross_entropy(logits, targets):
+    logits, targets = f32(logits), i32(targets)
+    n, v = logits.shape
+    loss = ctypes.c_float()
+    st = lib().mmo_cross_entropy(fp(logits), ip(targets), n, v, ctypes.byref(loss))
+    if st != OK:
+        raise IndexError(f"cross_entropy status {st}")
+    return loss.value
+
+
+def cross_entropy_rows(logits, targets):
+    logits, targets = f32(logits), i32(targets)
+    n, v = logits.shape
+    out = np.empty(n, np.float32)
+    st = lib().mmo_cross_entropy_rows(fp(logits), ip(targets), n, v, fp(out))
+    if st != OK:
+        raise IndexError(f"cross_entropy status {st}")
+    return out
+
+
+def block_forward(c, block_w, cos, sin, x, threads=None):
+    x = f32(x)
+    B, T, d = x.shape
+    out = np.empty_like(x)
+    st = lib().mmo_block_forward(ctypes.byref(c), fp(f32(block_w)), fp(f32(cos)),
+                                 fp(f32(sin)), fp(x), B, T, fp(out),
+                                 threads or default_threads())
+    assert st == OK, st
+    return out
+
+
+def forward(c, w, ids, batch, seq, threads=None):
+    ids = i32(ids)
+    logits = np.empty((batch, seq, c.vocab_size), np.float32)
+    st = lib().mmo_forward(ctypes.byref(c), fp(w), ip(ids), batch, seq, fp(logits),
+                           threads or default_threads())
+    if st != OK:
+        raise ValueError(f"forward status {st}")
+    return logits
+
+
+def forward_loss(c, w, ids, targets, batch, seq, want_logits=True, threads=None):
+    ids, targets = i32(ids), i32(targets)
+    logits = np.empty((batch, seq, c.vocab_size), np.float32) if want_logits else None
+    loss = ctypes.c_float()
+    st = lib().mmo_forward_loss(ctypes.byref(c), fp(w), ip(ids), ip(targets), batch, seq,
+                                fp(logits), ctypes.byref(loss), threads or default_threads())
+    if st != OK:
+        raise ValueError(f"forward_loss status {st}")
+    return loss.value, logits
+
+
+# ---- the reference's own C twins (oracle/_ref) -----------------------------
+
+def ref_lib():
+    """benches/midman-bench/c/baseline_kernels.c built into oracle/_ref, or None."""
+    if not os.path.exists(_REF_PATH):
+        return None
+    L = ctypes.CDLL(_REF_PATH)
+    sz = ctypes.c_size_t
+    L.mmb_matmul_ikj.argtypes = [_f32p, _f32p, _f32p, sz]
+    L.mmb_matmul_ijk.argtypes = [_f32p, _f32p, _f32p, sz]
+    L.mmb_softmax_rows.argtypes = [_f32p, _f32p, sz, sz]
+    L.mmb_silu.argtypes = [_f32p, _f32p, sz]
+    L.mmb_rms_norm.argtypes = [_f32p, _f32p, _f32p, sz, sz, ctypes.c_float]
+    for n in ("mmb_matmul_ikj", "mmb_matmul_ijk", "mmb_softmax_rows", "mmb_silu",
+              "mmb_rms_norm"):
+        getattr(L, n).restype = None
+    return L

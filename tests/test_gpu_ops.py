@@ -1,0 +1,197 @@
+"""GPU parity of the layer ops (midman-nn/src/lib.rs:45-56 surface) against
+the oracle, plus the reference's closed forms and error kinds.
+
+Tolerances, stated per op:
+  embedding, rope tables, apply_rope, add: bit-exact.
+  rms_norm: 4e-7 relative (sum-of-squares order; the rest is rounded as the
+            reference rounds it).
+  causal_attention: |diff| <= 2e-5 * max|v| + 1e-5 * |ref| (online softmax and
+            MFMA dot order).
+  attention_forward / swiglu: |diff| <= 1e-4 * max|ref| per tensor (three or
+            four chained GEMMs).
+  cross_entropy: 2e-6 relative on the mean.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import midman_hip as mh
+import mm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_max(got, want):
+    return float(np.max(np.abs(got.astype(np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def test_embedding_bit_exact_and_index_error(ctx):
+    print("\n[embedding]", flush=True)
+    table = O.randn((300, 48), 0.02, O.rng(5))
+    ids = np.random.default_rng(0).integers(0, 300, size=257).astype(np.int32)
+    T = ctx.to_device(table)
+    out = mh.embedding(ctx, T, ids)
+    assert np.array_equal(out.numpy(), O.embedding(table, ids))
+    # odd width takes the scalar path
+    t2 = O.randn((10, 7), 1.0, O.rng(6))
+    assert np.array_equal(mh.embedding(ctx, ctx.to_device(t2), [9, 0, 3]).numpy(), t2[[9, 0, 3]])
+    before = out.numpy()
+    with pytest.raises(mh.IndexOutOfRange):
+        mh.embedding(ctx, T, np.array([1, 300], np.int32), out=out)
+    with pytest.raises(mh.IndexOutOfRange):
+        mh.embedding(ctx, T, np.array([-1], np.int32), out=out)
+    assert np.array_equal(out.numpy(), before)  # nothing ran
+
+
+@pytest.mark.parametrize("rows,d", [(1, 2), (5, 64), (33, 100), (4096, 2048), (17, 1023)])
+def test_rms_norm(ctx, rows, d):
+    print(f"\n[rms_norm] rows={rows} d={d}", flush=True)
+    x = O.randn((rows, d), 1.0, O.rng(rows + d))
+    w = O.randn((d,), 1.0, O.rng(d))
+    got = mh.rms_norm(ctx, ctx.to_device(x), ctx.to_device(w), 1e-5).numpy()
+    want = O.rms_norm(x, w, 1e-5)
+    np.testing.assert_allclose(got, want, rtol=4e-7, atol=0)
+
+
+def test_rms_norm_known_row_and_errors(ctx, goldens):
+    g = goldens["rms_norm_row"]
+    y = mh.rms_norm(ctx, ctx.to_device(np.array([g["x"]], np.float32)),
+                    ctx.to_device(np.array(g["w"], np.float32)), g["eps"]).numpy()
+    r = math.sqrt(12.5)
+    assert abs(y[0, 0] - 3 / r) < 1e-6 and abs(y[0, 1] - 8 / r) < 1e-6
+    x = ctx.to_device(np.ones((2, 4), np.float32))
+    with pytest.raises(mh.ArgumentError):
+        mh.rms_norm(ctx, x, ctx.to_device(np.ones(4, np.float32)), 0.0)
+    with pytest.raises(mh.ShapeError):
+        mh.rms_norm(ctx, x, ctx.to_device(np.ones(3, np.float32)), 1e-5)
+
+
+@pytest.mark.parametrize("hd,t", [(8, 16), (16, 128), (128, 2048), (64, 1000)])
+def test_rope_tables_and_apply_bit_exact(ctx, hd, t):
+    print(f"\n[rope] hd={hd} t={t}", flush=True)
+    tabs = mh.RotaryTables(ctx, hd, t, 10000.0)
+    cos, sin = O.rope_tables(hd, t, 10000.0)
+    assert np.array_equal(tabs.cos.numpy(), cos) and np.array_equal(tabs.sin.numpy(), sin)
+    x = O.randn((3, 2, min(t, 300), hd), 1.0, O.rng(hd))
+    got = mh.apply_rope(ctx, ctx.to_device(x), tabs).numpy()
+    assert np.array_equal(got, O.apply_rope(x, cos, sin))
+
+
+ATTN_CASES = [
+    # B, H, Hkv, T, hd
+    (1, 2, 1, 2, 8),
+    (2, 2, 1, 12, 8),
+    (2, 4, 4, 32, 16),
+    (1, 4, 2, 33, 16),
+    (8, 4, 4, 256, 32),
+    (2, 16, 16, 100, 64),
+    (1, 16, 8, 1024, 128),
+    (2, 16, 8, 77, 128),
+    (3, 6, 3, 1, 64),
+]
+
+
+@pytest.mark.parametrize("B,H,Hkv,T,hd", ATTN_CASES)
+def test_causal_attention(ctx, B, H, Hkv, T, hd):
+    print(f"\n[attention] B={B} H={H} Hkv={Hkv} T={T} hd={hd}", flush=True)
+    r = O.rng(B * 1000 + T)
+    q = O.randn((B, H, T, hd), 1.0, r)
+    k = O.randn((B, Hkv, T, hd), 1.0, r)
+    v = O.randn((B, Hkv, T, hd), 1.0, r)
+    got = mh.causal_attention(ctx, ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)).numpy()
+    want = O.causal_attention(q, k, v)
+    err = np.abs(got.astype(np.float64) - want)
+    tol = 2e-5 * np.max(np.abs(v)) + 1e-5 * np.abs(want)
+    print(f"  max|diff| {err.max():.3g} (max|v| {np.abs(v).max():.3g})", flush=True)
+    assert np.all(err <= tol)
+
+
+def test_attention_known_answer(ctx, goldens):
+    g = goldens["attention_scale"]
+    shp = g["shape"]
+    q, k, v = (np.array(g[n], np.float32).reshape(shp) for n in ("q", "k", "v"))
+    out = mh.causal_attention(ctx, ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)).numpy()
+    w0 = 1.0 / (1.0 + math.exp(-1.0))
+    want = np.array([1, 0, 0, 0, w0, 1 - w0, 0, 0], np.float32).reshape(shp)
+    assert np.all(np.abs(out - want) < 1e-6)
+
+
+def test_attention_rejects_bad_shapes(ctx):
+    q = ctx.empty((1, 3, 4, 8))
+    k = ctx.empty((1, 2, 4, 8))
+    with pytest.raises(mh.ShapeError):
+        mh.causal_attention(ctx, q, k, k)
+    q2 = ctx.empty((1, 2, 4, 12))
+    k2 = ctx.empty((1, 2, 4, 12))
+    with pytest.raises(mh.ShapeError):  # head dim outside the device sizes
+        mh.causal_attention(ctx, q2, k2, k2)
+
+
+@pytest.mark.parametrize("B,T,d,H,Hkv", [(2, 12, 16, 2, 1), (2, 64, 256, 4, 2),
+                                         (1, 300, 2048, 16, 8)])
+def test_attention_forward(ctx, B, T, d, H, Hkv):
+    print(f"\n[attention_forward] B={B} T={T} d={d} H={H} Hkv={Hkv}", flush=True)
+    hd, kv = d // H, Hkv * (d // H)
+    r = O.rng(d + T)
+    x = O.randn((B, T, d), 1.0, r)
+    wq, wk, wv = O.randn((d, d), 0.02, r), O.randn((d, kv), 0.02, r), O.randn((d, kv), 0.02, r)
+    wo = O.randn((d, d), 0.02, r)
+    tabs = mh.RotaryTables(ctx, hd, T, 10000.0)
+    cos, sin = O.rope_tables(hd, T, 10000.0)
+    dev = [ctx.to_device(a) for a in (x, wq, wk, wv, wo)]
+    got = mh.attention_forward(ctx, dev[0], *dev[1:], H, Hkv, tabs).numpy()
+    want = O.attention_forward(x, wq, wk, wv, wo, cos, sin, H, Hkv)
+    e = rel_max(got, want)
+    print(f"  max|diff|/max|ref| {e:.3g}", flush=True)
+    assert e <= 1e-4
+
+
+@pytest.mark.parametrize("rows,d,ff", [(1, 1, 1), (64, 64, 176), (2048, 128, 344), (1024, 2048, 5632)])
+def test_swiglu(ctx, rows, d, ff):
+    print(f"\n[swiglu] rows={rows} d={d} ff={ff}", flush=True)
+    r = O.rng(rows + ff)
+    x = O.randn((rows, d), 1.0, r)
+    wg, wu, wd = O.randn((d, ff), 0.02, r), O.randn((d, ff), 0.02, r), O.randn((ff, d), 0.02, r)
+    dev = [ctx.to_device(a) for a in (x, wg, wu, wd)]
+    got = mh.swiglu(ctx, *dev).numpy()
+    want = O.swiglu(x, wg, wu, wd)
+    e = rel_max(got, want)
+    print(f"  max|diff|/max|ref| {e:.3g}", flush=True)
+    assert e <= 1e-4
+
+
+def test_swiglu_known_value(ctx, goldens):
+    g = goldens["swiglu_value"]
+    one = lambda v: ctx.to_device(np.array([[v]], np.float32))
+    out = mh.swiglu(ctx, one(g["x"]), one(g["wg"]), one(g["wu"]), one(g["wd"])).numpy()
+    assert abs(out[0, 0] - 2.0 / (1.0 + math.exp(-2.0)) * 12.0) < 1e-5
+
+
+def test_add_bit_exact(ctx):
+    a = O.randn((1001,), 1.0, O.rng(1))
+    b = O.randn((1001,), 1.0, O.rng(2))
+    got = mh.add(ctx, ctx.to_device(a), ctx.to_device(b)).numpy()
+    assert np.array_equal(got, a + b)
+
+
+@pytest.mark.parametrize("n,v", [(1, 2), (7, 5), (2048, 4096), (4096, 32000), (3, 100003)])
+def test_cross_entropy(ctx, n, v):
+    print(f"\n[cross_entropy] n={n} v={v}", flush=True)
+    r = O.rng(n + v)
+    logits = O.randn((n, v), 3.0, r)
+    targets = np.random.default_rng(n).integers(0, v, size=n).astype(np.int32)
+    got = mh.cross_entropy(ctx, ctx.to_device(logits), targets)
+    want = O.cross_entropy(logits, targets)
+    assert abs(got - want) <= 2e-6 * abs(want), (got, want)
+
+
+def test_cross_entropy_known_values_and_errors(ctx):
+    L = lambda a: ctx.to_device(np.array(a, np.float32))
+    assert abs(mh.cross_entropy(ctx, L([[0.0, 0.0]]), [0]) - math.log(2)) < 1e-6
+    assert mh.cross_entropy(ctx, L([[20.0, 0, 0]]), [0]) < 1e-6
+    assert abs(mh.cross_entropy(ctx, L([[0.0, 0], [50, -50]]), [1, 0]) - math.log(2) / 2) < 1e-6
+    with pytest.raises(mh.IndexOutOfRange):
+        mh.cross_entropy(ctx, L([[0.0, 0.0, 0.0]]), [3])
+    with pytest.raises(mh.ShapeError):
+        mh.cross_entropy(ctx, L([[0.0, 0.0, 0.0]]), [0, 1])
