@@ -185,6 +185,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-tiny", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run one add kernel over 2^26 floats (read 512 MiB, write "
+                         "256 MiB) to calibrate HBM byte counters")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -196,6 +199,14 @@ def main():
     ctx = mh.Context(0)
     name, cus = ctx.device_info()
     log(f"device {name}, {cus} CUs")
+    if a.copy_probe:
+        n = 1 << 26
+        bufs = [ctx.empty((n,)) for _ in range(3)]
+        mh.check(mh.lib().mmh_add(ctx.handle, bufs[0].ptr, bufs[1].ptr, bufs[2].ptr, n))
+        ctx.synchronize()
+        for b in bufs:
+            b.free()
+        log("copy probe: add over 2^26 floats done")
 
     large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup)
     log(f"large: {large['ms_per_step']:.2f} ms/step, {large['tokens_per_s']:.0f} tok/s, "

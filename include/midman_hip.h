@@ -127,7 +127,7 @@ int32_t mmh_rope_tables(mmh_handle ctx, int64_t head_dim, int64_t max_seq_len, f
 int32_t mmh_apply_rope(mmh_handle ctx, const float *x, int64_t bh, int64_t t, int64_t hd,
                        const float *cos_dev, const float *sin_dev, float *out);
 /* attention.rs:97-101: q [B,H,T,hd], k/v [B,Hkv,T,hd] (already rotated),
- * out [B,H,T,hd]; head j reads kv head j / (H/Hkv). hd in {8,16,32,64,128}. */
+ * out [B,H,T,hd]; head j reads kv head j / (H/Hkv). hd in {4,8,16,32,64,128}. */
 int32_t mmh_causal_attention(mmh_handle ctx, const float *q, const float *k, const float *v,
                              int64_t b, int64_t h, int64_t hkv, int64_t t, int64_t hd,
                              float *out);

@@ -27,6 +27,10 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall",
     "-Wno-unused-result",
+    # No multiply-add contraction: element-wise ops round where the reference's
+    # Rust code rounds (hipcc's default would fuse x*c - y*s into one FMA;
+    # the __fmul_rn-style intrinsics are not a barrier against that).
+    "-ffp-contract=off",
     # Packed FP32 instructions stay off: v_pk_{add,mul,fma}_f32 are not used.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]

@@ -216,12 +216,13 @@ void attention(Context &ctx, const AttnDesc &d) {
     const bool rope = d.cos_t != nullptr;
     dim3 grid((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
     switch (d.hd) {
+        case 4: launch_hd<4>(ctx, p, grid, rope); break;
         case 8: launch_hd<8>(ctx, p, grid, rope); break;
         case 16: launch_hd<16>(ctx, p, grid, rope); break;
         case 32: launch_hd<32>(ctx, p, grid, rope); break;
         case 64: launch_hd<64>(ctx, p, grid, rope); break;
         case 128: launch_hd<128>(ctx, p, grid, rope); break;
-        default: fail(MMH_ERR_SHAPE, "attention: head_dim must be 8, 16, 32, 64 or 128");
+        default: fail(MMH_ERR_SHAPE, "attention: head_dim must be 4, 8, 16, 32, 64 or 128");
     }
     check_hip(hipGetLastError(), "attention launch");
 }

@@ -75,9 +75,9 @@ Config parse_config(const double *v) {
     if (c.heads % c.kv_heads) fail(MMH_ERR_CONFIG, "n_heads is not divisible by n_kv_heads");
     if (c.hd() & 1) fail(MMH_ERR_CONFIG, "head dimension must be even for rotary embeddings");
     const int64_t hd = c.hd();
-    if (hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
+    if (hd != 4 && hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
         fail(MMH_ERR_CONFIG, "head dimension " + std::to_string(hd) +
-                                 " is not one of the device attention sizes 8, 16, 32, 64, 128");
+                                 " is not one of the device attention sizes 4, 8, 16, 32, 64, 128");
     return c;
 }
 

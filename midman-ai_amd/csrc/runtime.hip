@@ -131,7 +131,7 @@ int32_t mmh_context_create(int32_t device, mmh_handle *out_ctx) {
         hipDeviceProp_t prop;
         check_hip(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
         c->cu_count = prop.multiProcessorCount;
-        c->name = prop.name;
+        c->name = prop.name[0] ? prop.name : prop.gcnArchName;
         check_hip(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream create");
         check_hip(hipEventCreate(&c->t0), "event create");
         check_hip(hipEventCreate(&c->t1), "event create");

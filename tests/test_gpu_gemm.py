@@ -44,6 +44,18 @@ def check(got, want, bnd, what):
     assert worst <= 1.0, what
 
 
+def test_hand_calculation_exact(ctx, goldens):
+    g = goldens["gemm_hand"]
+    a = np.array(g["a"], np.float32).reshape(2, 3)
+    b = np.array(g["b"], np.float32).reshape(3, 2)
+    want = np.array(g["c"], np.float32).reshape(2, 2)
+    for form, aa, bb in (("nn", a, b), ("nt", a, np.array(g["bt"], np.float32).reshape(2, 3)),
+                         ("tn", np.array(g["at"], np.float32).reshape(3, 2), b)):
+        A, B, C = ctx.to_device(aa), ctx.to_device(bb), ctx.empty((2, 2))
+        mh.gemm(ctx, form, A, B, C, 2, 3, 2)
+        assert np.array_equal(C.numpy(), want), form
+
+
 @pytest.mark.parametrize("k", SIZES)
 @pytest.mark.parametrize("n", SIZES)
 def test_sweep_forward_and_backward(ctx, k, n):
@@ -83,18 +95,6 @@ def test_ragged_shapes_and_accumulate(ctx, m, k, n, form):
     check(C.numpy(), O.gemm(form, aa, bb, m, k, n), bound(a, b), f"{form} store")
     for x in (A, B, C):
         x.free()
-
-
-def test_hand_calculation_exact(ctx, goldens):
-    g = goldens["gemm_hand"]
-    a = np.array(g["a"], np.float32).reshape(2, 3)
-    b = np.array(g["b"], np.float32).reshape(3, 2)
-    want = np.array(g["c"], np.float32).reshape(2, 2)
-    for form, aa, bb in (("nn", a, b), ("nt", a, np.array(g["bt"], np.float32).reshape(2, 3)),
-                         ("tn", np.array(g["at"], np.float32).reshape(3, 2), b)):
-        A, B, C = ctx.to_device(aa), ctx.to_device(bb), ctx.empty((2, 2))
-        mh.gemm(ctx, form, A, B, C, 2, 3, 2)
-        assert np.array_equal(C.numpy(), want), form
 
 
 def test_special_values_propagate(ctx):

@@ -119,8 +119,17 @@ def test_large_preset_full_size_invariants(ctx):
     assert m.num_parameters() == 1_009_338_368
     x, y = m.lab_tokens(4, 1024)
     loss, logits = m.forward_loss(x, y, 4, 1024)
-    print(f"  loss {loss:.6f} (ln V = {math.log(32000):.6f})", flush=True)
-    assert abs(loss - math.log(32000)) < 0.05  # a fresh model is near uniform
+    # The loss equals the mean CE of the returned logits, evaluated in float64.
+    L = logits.reshape(-1, 32000).astype(np.float64)
+    mx = L.max(1, keepdims=True)
+    f64 = float(np.mean(np.log(np.exp(L - mx).sum(1)) + mx[:, 0] - L[np.arange(4096), y]))
+    print(f"  loss {loss:.6f}, float64 CE of the logits {f64:.6f}, ln V {math.log(32000):.6f}",
+          flush=True)
+    assert abs(loss - f64) <= 2e-6 * f64
+    # A fresh tied model's logits are x.E^T with unit-RMS x and E ~ N(0, 0.02):
+    # variance ~ d * 0.02^2, so the loss sits near ln V + var/2.
+    var = float(L.var(axis=1).mean())
+    assert abs(loss - (math.log(32000) + var / 2)) < 0.05, (loss, var)
     # batch independence and the loss identity (wiring.rs:146-154, 207-217)
     l0, lg0 = m.forward_loss(x[:1024], y[:1024], 1, 1024)
     check_logits(lg0, logits[:1], "sequence 0 alone vs in the batch")

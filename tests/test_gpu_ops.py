@@ -3,13 +3,17 @@ the oracle, plus the reference's closed forms and error kinds.
 
 Tolerances, stated per op:
   embedding, rope tables, apply_rope, add: bit-exact.
-  rms_norm: 4e-7 relative (sum-of-squares order; the rest is rounded as the
-            reference rounds it).
+  rms_norm: 4e-6 relative. The sum of squares runs in a different order
+            (the reference's sequential f32 sum over d terms is itself off by
+            up to ~d*2^-24 relative); the rest rounds as the reference rounds.
   causal_attention: |diff| <= 2e-5 * max|v| + 1e-5 * |ref| (online softmax and
             MFMA dot order).
   attention_forward / swiglu: |diff| <= 1e-4 * max|ref| per tensor (three or
             four chained GEMMs).
-  cross_entropy: 2e-6 relative on the mean.
+  cross_entropy: 1e-4 relative to the oracle (the north-star loss
+            tolerance; the reference's sequential f32 sum of V exponentials
+            drifts by up to ~1e-5 relative at V = 1e5) and 2e-6 relative to a
+            float64 evaluation.
 """
 import math
 
@@ -51,7 +55,7 @@ def test_rms_norm(ctx, rows, d):
     w = O.randn((d,), 1.0, O.rng(d))
     got = mh.rms_norm(ctx, ctx.to_device(x), ctx.to_device(w), 1e-5).numpy()
     want = O.rms_norm(x, w, 1e-5)
-    np.testing.assert_allclose(got, want, rtol=4e-7, atol=0)
+    np.testing.assert_allclose(got, want, rtol=4e-6, atol=0)
 
 
 def test_rms_norm_known_row_and_errors(ctx, goldens):
@@ -183,7 +187,12 @@ def test_cross_entropy(ctx, n, v):
     targets = np.random.default_rng(n).integers(0, v, size=n).astype(np.int32)
     got = mh.cross_entropy(ctx, ctx.to_device(logits), targets)
     want = O.cross_entropy(logits, targets)
-    assert abs(got - want) <= 2e-6 * abs(want), (got, want)
+    L = logits.astype(np.float64)
+    m = L.max(1, keepdims=True)
+    f64 = float(np.mean(np.log(np.exp(L - m).sum(1)) + m[:, 0] - L[np.arange(n), targets]))
+    print(f"  gpu {got:.7f} oracle {want:.7f} float64 {f64:.7f}", flush=True)
+    assert abs(got - want) <= 1e-4 * abs(want), (got, want)
+    assert abs(got - f64) <= 2e-6 * abs(f64), (got, f64)
 
 
 def test_cross_entropy_known_values_and_errors(ctx):
