@@ -2,24 +2,32 @@
 // the reference's materialised path (midman-nn/src/attention.rs:79-101,146-170):
 // repeat_interleave of K/V, Q.K^T, scale, additive -1e9 mask, softmax, P.V.
 //
-// One wave64 owns 32 query rows of one (batch, head) and walks the key blocks
-// of 32 up to the diagonal with an online softmax, so no [T,T] tensor exists.
-// It computes the transposed products so that every per-query quantity lives in
-// the lane that owns the query:
-//   S^T[key][q] = K_blk . Q^T   (A = K from LDS, B = Q from registers)
-//   O^T[d][q]  += V^T . P^T     (A = V from LDS, B = P straight from the S^T
-//                                accumulators, no LDS round trip)
+// A 256-thread workgroup (4 wave64s) owns 128 query rows of one (batch, head);
+// each wave owns 32 of them. The workgroup walks 32-key tiles of K and V up to
+// its last diagonal: every tile is loaded once with float4 loads into
+// registers, written to a double-buffered LDS stage, and shared by the four
+// waves; the next tile's loads are in flight while the current one is used.
+// Each wave keeps an online softmax for its rows, so no [T,T] tensor exists.
+//
+// The products are computed transposed so that every per-query quantity lives
+// in the lane that owns the query:
+//   S^T[key][q] = K_tile . Q^T   (A = K from LDS, B = Q from registers)
+//   O^T[d][q]  += V^T . P^T      (A = V from LDS, B = P straight from the S^T
+//                                 accumulators, no LDS round trip)
 // With the MFMA layout (lane l: column l%32; register r: row
 // 8*(r/4) + 4*(l/32) + r%4), query q = l%32 is fixed per lane in both
-// products, so the row max/sum need one cross-lane exchange (lanes l, l^32)
-// and the rescale of O is a per-lane scalar.
+// products, so a row's max and sum need one exchange between lanes l and l^32
+// and the rescale of O is a per-lane scalar. In S^T the lanes 0-31 feed head
+// dims [0, hd/2) and lanes 32-63 feed [hd/2, hd), so each lane reads its Q
+// operands as one contiguous run.
 //
-// RoPE (rope.rs:28-32) is applied in registers to Q and while staging K into
-// LDS, with explicitly rounded multiplies and adds, so rotated values equal
-// the reference's bit for bit. The score scale is applied after the dot
-// product as attention.rs:83 does. Keys above the diagonal are skipped: the
-// reference's -1e9 mask gives them exp(.) == 0 exactly. Query head j reads kv
-// head j / (H/Hkv) (repeat_interleave, ops_shape.rs:192-200).
+// RoPE (rope.rs:28-32) is applied once, in place, to the q and k rows before
+// the attention kernel (rope_strided below), with separately rounded
+// multiplies and adds, so rotated values equal the reference's bit for bit.
+// The score scale is applied after the dot product as attention.rs:83 does.
+// Keys above the diagonal are skipped: the reference's -1e9 mask gives them
+// exp(.) == 0 exactly. Query head j reads kv head j / (H/Hkv)
+// (repeat_interleave, ops_shape.rs:192-200).
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -33,57 +41,93 @@ struct AttnP {
     int64_t sqb, sqh, sqt, skb, skh, skt, svb, svh, svt, sob, soh, sot;
     int h, hkv, t, nqb;
     float scale;
-    const float *cos_t, *sin_t;
 };
 
-template <int HD, bool ROPE>
-__global__ __launch_bounds__(64) void attn_fwd_kernel(AttnP p) {
-    constexpr int HALF = HD / 2;
-    constexpr int NS = HD / 2;            // MFMA k-steps over the head dim
-    constexpr int NDB = (HD + 31) / 32;   // 32-wide blocks of the head dim
-    __shared__ float Ks[32][HD + 1];
-    __shared__ float Vs[32][HD];
+template <int HD>
+__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
+    constexpr int NS = HD / 2;               // MFMA k-steps over the head dim
+    constexpr int NDB = (HD + 31) / 32;      // 32-wide blocks of the head dim
+    constexpr int KS = HD + 1;               // K row stride in LDS (odd: no bank conflicts)
+    constexpr int F4 = 32 * HD / 4;          // float4s per K or V tile
+    constexpr int PER = (F4 + 255) / 256;    // float4s per thread per tile
+    // Two K stages [32][KS] and two V stages [32][HD]; at the end the same
+    // memory holds the 4 waves' outputs as [128][KS], which is the larger size.
+    constexpr int STAGES = 2 * 32 * KS + 2 * 32 * HD;
+    constexpr int OUT = 128 * KS;
+    __shared__ __attribute__((aligned(16))) float smem[STAGES > OUT ? STAGES : OUT];
+    auto Ks = [&](int buf) { return smem + buf * 32 * KS; };
+    auto Vs = [&](int buf) { return smem + 64 * KS + buf * 32 * HD; };
 
-    const int lane = threadIdx.x;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lq = lane & 31, lh = lane >> 5;
     const int head = blockIdx.x, b = blockIdx.y;
-    const int qb = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
+    const int qblk = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
     const int kvh = head / (p.h / p.hkv);
     const int T = p.t;
-    const int q0 = qb * 32;
+    const int q_first = qblk * 128;
+    const int q_last = min(q_first + 127, T - 1);
+    const int ntiles = q_last / 32 + 1;            // key tiles the workgroup needs
+    const int q0 = q_first + wave * 32;            // this wave's first query
+    const int my_tiles = q0 < T ? q0 / 32 + 1 : 0; // tiles this wave needs
 
     const float *Q = p.q + b * p.sqb + head * p.sqh;
     const float *K = p.k + b * p.skb + kvh * p.skh;
     const float *V = p.v + b * p.svb + kvh * p.svh;
 
-    // ---- stage Q through LDS, pick this lane's operand values, rotate ----
-    for (int idx = lane; idx < 32 * HD; idx += 64) {
-        const int j = idx / HD, c = idx - j * HD;
-        Ks[j][c] = (q0 + j < T) ? Q[(int64_t)(q0 + j) * p.sqt + c] : 0.0f;
-    }
-    __syncthreads();
+    // Q operand: lane holds Q[q0 + lq][lh * NS + s], s < NS.
     float qr[NS];
+    {
+        const int qi = min(q0 + lq, T - 1);
+        const float4 *src = reinterpret_cast<const float4 *>(Q + (int64_t)qi * p.sqt + lh * NS);
+        if (NS % 4 == 0) {
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qr[s] = Ks[lq][2 * s + lh];
-    __syncthreads();
-    if (ROPE) {
-        const int pos = min(q0 + lq, T - 1);
-        float rot[NS];
+            for (int s = 0; s < NS / 4; ++s) {
+                const float4 v = src[s];
+                qr[4 * s + 0] = v.x;
+                qr[4 * s + 1] = v.y;
+                qr[4 * s + 2] = v.z;
+                qr[4 * s + 3] = v.w;
+            }
+        } else {
+            const float *s1 = Q + (int64_t)qi * p.sqt + lh * NS;
 #pragma unroll
-        for (int s = 0; s < NS; ++s) {
-            const int pd = 2 * s + lh;
-            if (pd < HALF) {
-                const float cs = p.cos_t[pos * HALF + pd], sn = p.sin_t[pos * HALF + pd];
-                rot[s] = __fsub_rn(__fmul_rn(qr[s], cs), __fmul_rn(qr[s + HALF / 2], sn));
-            } else {
-                const int pp = pd - HALF;
-                const float cs = p.cos_t[pos * HALF + pp], sn = p.sin_t[pos * HALF + pp];
-                rot[s] = __fadd_rn(__fmul_rn(qr[s], cs), __fmul_rn(qr[s - HALF / 2], sn));
+            for (int s = 0; s < NS; ++s) qr[s] = s1[s];
+        }
+    }
+
+    float4 kreg[PER], vreg[PER];
+    auto load_tile = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * 256;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (f < F4) {
+                const int j = (4 * f) / HD, c = (4 * f) % HD;
+                const int key = kt * 32 + j;
+                if (key < T) {
+                    kv = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + c);
+                    vv = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + c);
+                }
+            }
+            kreg[i] = kv;
+            vreg[i] = vv;
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * 256;
+            if (f < F4) {
+                const int j = (4 * f) / HD, c = (4 * f) % HD;
+                float *kd = Ks(buf) + j * KS + c;
+                kd[0] = kreg[i].x;
+                kd[1] = kreg[i].y;
+                kd[2] = kreg[i].z;
+                kd[3] = kreg[i].w;
+                *reinterpret_cast<float4 *>(Vs(buf) + j * HD + c) = vreg[i];
             }
         }
-#pragma unroll
-        for (int s = 0; s < NS; ++s) qr[s] = rot[s];
-    }
+    };
 
     floatx16 o[NDB];
 #pragma unroll
@@ -93,103 +137,132 @@ __global__ __launch_bounds__(64) void attn_fwd_kernel(AttnP p) {
     float m_run = -INFINITY, l_run = 0.0f;
     const int qi = q0 + lq;
 
-    for (int kb = 0; kb <= qb; ++kb) {
-        const int k0 = kb * 32;
-        // K block (rotated) and V block into LDS.
-        for (int idx = lane; idx < 32 * HALF; idx += 64) {
-            const int j = idx / HALF, c = idx - j * HALF;
-            const int key = k0 + j;
-            float y1 = 0.0f, y2 = 0.0f;
-            if (key < T) {
-                const float x1 = K[(int64_t)key * p.skt + c], x2 = K[(int64_t)key * p.skt + c + HALF];
-                if (ROPE) {
-                    const float cs = p.cos_t[key * HALF + c], sn = p.sin_t[key * HALF + c];
-                    y1 = __fsub_rn(__fmul_rn(x1, cs), __fmul_rn(x2, sn));
-                    y2 = __fadd_rn(__fmul_rn(x2, cs), __fmul_rn(x1, sn));
-                } else {
-                    y1 = x1;
-                    y2 = x2;
-                }
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < ntiles) load_tile(kt + 1);
+        if (kt < my_tiles) {
+            const float *Kb = Ks(cur);
+            const float *Vb = Vs(cur);
+            floatx16 sacc;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Kb[lq * KS + lh * NS + s], qr[s], sacc,
+                                                            0, 0, 0);
+            // Scale, mask, online softmax for query qi (shared by lanes l, l^32).
+            const int k0 = kt * 32;
+            float pv[16];
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const float sv = sacc[r] * p.scale;
+                pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
+                mloc = fmaxf(mloc, pv[r]);
             }
-            Ks[j][c] = y1;
-            Ks[j][c + HALF] = y2;
-        }
-        for (int idx = lane; idx < 32 * HD; idx += 64) {
-            const int j = idx / HD, c = idx - j * HD;
-            Vs[j][c] = (k0 + j < T) ? V[(int64_t)(k0 + j) * p.svt + c] : 0.0f;
-        }
-        __syncthreads();
-
-        // S^T = K . Q^T over the head dim.
-        floatx16 sacc;
+            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+            const float m_new = fmaxf(m_run, mloc);
+            const float alpha = expf(m_run - m_new);
+            float lsum = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+            for (int r = 0; r < 16; ++r) {
+                pv[r] = expf(pv[r] - m_new);
+                lsum += pv[r];
+            }
+            lsum += __shfl_xor(lsum, 32, 64);
+            l_run = l_run * alpha + lsum;
+            m_run = m_new;
 #pragma unroll
-        for (int s = 0; s < NS; ++s)
-            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Ks[lq][2 * s + lh], qr[s], sacc, 0, 0, 0);
-
-        // Scale, mask, online softmax for query qi (shared by lanes l, l^32).
-        float pv[16];
-        float mloc = -INFINITY;
+            for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            const float sv = __fmul_rn(sacc[r], p.scale);
-            const bool ok = key <= qi && key < T;
-            pv[r] = ok ? sv : -INFINITY;
-            mloc = fmaxf(mloc, pv[r]);
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        const float m_new = fmaxf(m_run, mloc);
-        const float alpha = expf(m_run - m_new);
-        float lsum = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            pv[r] = expf(pv[r] - m_new);
-            lsum += pv[r];
-        }
-        lsum += __shfl_xor(lsum, 32, 64);
-        l_run = l_run * alpha + lsum;
-        m_run = m_new;
-
-        // O^T += V^T . P^T; P^T's operand is pv[s] in place.
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-            const int dcol = db * 32 + lq;
+                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            // s outer, head-dim block inner: consecutive MFMAs are independent.
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
                 const int key = 8 * (s >> 2) + 4 * lh + (s & 3);
-                const float a = (HD >= 32 || dcol < HD) ? Vs[key][dcol < HD ? dcol : 0] : 0.0f;
-                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, pv[s], o[db], 0, 0, 0);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    const int dcol = db * 32 + lq;
+                    const float a = (HD >= 32 || dcol < HD) ? Vb[key * HD + (dcol < HD ? dcol : 0)] : 0.0f;
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, pv[s], o[db], 0, 0, 0);
+                }
             }
         }
+        if (kt + 1 < ntiles) store_tile(cur ^ 1);
         __syncthreads();
     }
 
-    if (qi < T) {
+    // O^T -> LDS as [q][d], then coalesced row stores.
+    float *Os = smem + wave * 32 * KS;
+    if (my_tiles > 0) {
         const float inv = 1.0f / l_run;
-        float *O = p.out + b * p.sob + head * p.soh + (int64_t)qi * p.sot;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int d = db * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (d < HD) O[d] = o[db][r] * inv;
+                if (d < HD) Os[lq * KS + d] = o[db][r] * inv;
             }
+    }
+    __syncthreads();
+    if (my_tiles > 0) {
+        for (int idx = lane; idx < 32 * HD; idx += 64) {
+            const int j = idx / HD, c = idx - j * HD;
+            const int q = q0 + j;
+            if (q < T) p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = Os[j * KS + c];
+        }
+    }
+}
+
+// In-place RoPE (rope.rs:28-32) on heads of a strided layout: element
+// (b, h, t, p) at x[b*sb + h*sh + t*st + p], positions t = 0..T-1.
+__global__ __launch_bounds__(256) void rope_strided_kernel(float *__restrict__ x, int64_t sb,
+                                                           int64_t sh, int64_t st, int64_t nb,
+                                                           int64_t nh, int64_t t, int64_t hd,
+                                                           const float *__restrict__ cos_t,
+                                                           const float *__restrict__ sin_t) {
+    const int64_t half = hd / 2, total = nb * nh * t * half;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r = i;
+        const int64_t c = r % half;
+        r /= half;
+        const int64_t pos = r % t;
+        r /= t;
+        const int64_t hh = r % nh;
+        const int64_t bb = r / nh;
+        float *row = x + bb * sb + hh * sh + pos * st;
+        const float x1 = row[c], x2 = row[c + half];
+        const float cs = cos_t[pos * half + c], sn = sin_t[pos * half + c];
+        row[c] = x1 * cs - x2 * sn;
+        row[c + half] = x2 * cs + x1 * sn;
     }
 }
 
 template <int HD>
-void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool rope) {
-    if (rope)
-        hipLaunchKernelGGL((attn_fwd_kernel<HD, true>), grid, dim3(64), 0, ctx.stream, p);
-    else
-        hipLaunchKernelGGL((attn_fwd_kernel<HD, false>), grid, dim3(64), 0, ctx.stream, p);
+void launch_hd(Context &ctx, const AttnP &p, dim3 grid) {
+    hipLaunchKernelGGL((attn_fwd_kernel<HD>), grid, dim3(256), 0, ctx.stream, p);
 }
 
+bool al16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
 }  // namespace
+
+void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,
+                         int64_t nh, int64_t t, int64_t hd, const float *cos_t,
+                         const float *sin_t) {
+    const int64_t work = nb * nh * t * (hd / 2);
+    int64_t blocks = (work + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL(rope_strided_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx.stream, x,
+                       sb, sh, st, nb, nh, t, hd, cos_t, sin_t);
+    check_hip(hipGetLastError(), "rope launch");
+}
 
 void attention(Context &ctx, const AttnDesc &d) {
     if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
@@ -197,6 +270,20 @@ void attention(Context &ctx, const AttnDesc &d) {
     if (d.h % d.hkv != 0) fail(MMH_ERR_SHAPE, "attention: n_heads is not a multiple of n_kv_heads");
     if (d.b > 65535 || d.h > 0x7fffffff || d.t > 0x3fffffff)
         fail(MMH_ERR_SHAPE, "attention: shape too large");
+    if (d.hd != 4 && d.hd != 8 && d.hd != 16 && d.hd != 32 && d.hd != 64 && d.hd != 128)
+        fail(MMH_ERR_SHAPE, "attention: head_dim must be 4, 8, 16, 32, 64 or 128");
+    const int64_t strides[] = {d.sqb, d.sqh, d.sqt, d.skb, d.skh, d.skt, d.svb, d.svh, d.svt};
+    for (int64_t s : strides)
+        if (s % 4) fail(MMH_ERR_SHAPE, "attention: strides must be multiples of 4 floats");
+    if (!al16(d.q) || !al16(d.k) || !al16(d.v))
+        fail(MMH_ERR_ARGUMENT, "attention: q, k and v must be 16-byte aligned");
+    if (d.cos_t) {
+        // q and k rows are rotated in place before the kernel reads them.
+        launch_rope_strided(ctx, const_cast<float *>(d.q), d.sqb, d.sqh, d.sqt, d.b, d.h, d.t, d.hd,
+                            d.cos_t, d.sin_t);
+        launch_rope_strided(ctx, const_cast<float *>(d.k), d.skb, d.skh, d.skt, d.b, d.hkv, d.t,
+                            d.hd, d.cos_t, d.sin_t);
+    }
     AttnP p{};
     p.q = d.q;
     p.k = d.k;
@@ -209,20 +296,16 @@ void attention(Context &ctx, const AttnDesc &d) {
     p.h = (int)d.h;
     p.hkv = (int)d.hkv;
     p.t = (int)d.t;
-    p.nqb = (int)((d.t + 31) / 32);
+    p.nqb = (int)((d.t + 127) / 128);
     p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
-    p.cos_t = d.cos_t;
-    p.sin_t = d.sin_t;
-    const bool rope = d.cos_t != nullptr;
     dim3 grid((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
     switch (d.hd) {
-        case 4: launch_hd<4>(ctx, p, grid, rope); break;
-        case 8: launch_hd<8>(ctx, p, grid, rope); break;
-        case 16: launch_hd<16>(ctx, p, grid, rope); break;
-        case 32: launch_hd<32>(ctx, p, grid, rope); break;
-        case 64: launch_hd<64>(ctx, p, grid, rope); break;
-        case 128: launch_hd<128>(ctx, p, grid, rope); break;
-        default: fail(MMH_ERR_SHAPE, "attention: head_dim must be 4, 8, 16, 32, 64 or 128");
+        case 4: launch_hd<4>(ctx, p, grid); break;
+        case 8: launch_hd<8>(ctx, p, grid); break;
+        case 16: launch_hd<16>(ctx, p, grid); break;
+        case 32: launch_hd<32>(ctx, p, grid); break;
+        case 64: launch_hd<64>(ctx, p, grid); break;
+        default: launch_hd<128>(ctx, p, grid); break;
     }
     check_hip(hipGetLastError(), "attention launch");
 }

@@ -55,14 +55,182 @@ __device__ __forceinline__ float silu_f(float x) {
     return __fmul_rn(x, s);
 }
 
+// Row strides of the LDS stages, chosen so the transposing scalar stores
+// spread over the banks and the float4 stores stay 16-byte aligned.
+template <bool TA>
+struct LdsA {
+    static constexpr int S = BM + (TA ? 4 : 2);
+};
+template <bool TB>
+struct LdsB {
+    static constexpr int S = BN + (TB ? 2 : 4);
+};
+
+// The K loop of one 128x128 tile. FAST: the whole tile lies inside M, N and
+// the K range is a multiple of BK with 16-byte aligned rows, so no load needs
+// a predicate; otherwise every element is bounds-checked and zero-filled.
+template <bool TA, bool TB, bool FAST>
+__device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__restrict__ A,
+                                              const float *__restrict__ B, int64_t m0, int64_t n0,
+                                              int64_t kbeg, int64_t kend,
+                                              float (*As)[BK][LdsA<TA>::S],
+                                              float (*Bs)[BK][LdsB<TB>::S],
+                                              floatx16 (&acc)[2][2]) {
+    const int tid = threadIdx.x;
+    const int64_t M = p.m, N = p.n;
+    // One K-tile is 2 float4 of A and 2 float4 of B per thread, held in
+    // named registers (an indexed array here ends up in scratch memory).
+    float4 ra0, ra1, rb0, rb1;
+
+    auto load_a = [&](int idx, int64_t k0) -> float4 {
+        if (FAST) {
+            if (!TA)
+                return *reinterpret_cast<const float4 *>(A + (m0 + (idx >> 2)) * p.lda + k0 + (idx & 3) * 4);
+            return *reinterpret_cast<const float4 *>(A + (k0 + (idx >> 5)) * p.lda + m0 + (idx & 31) * 4);
+        }
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!TA) {
+            const int64_t gm = m0 + (idx >> 2), gk = k0 + (idx & 3) * 4;
+            if (gm < M) {
+                const float *src = A + gm * p.lda + gk;
+                if (gk + 0 < kend) v.x = src[0];
+                if (gk + 1 < kend) v.y = src[1];
+                if (gk + 2 < kend) v.z = src[2];
+                if (gk + 3 < kend) v.w = src[3];
+            }
+        } else {
+            const int64_t gk = k0 + (idx >> 5), gm = m0 + (idx & 31) * 4;
+            if (gk < kend) {
+                const float *src = A + gk * p.lda + gm;
+                if (gm + 0 < M) v.x = src[0];
+                if (gm + 1 < M) v.y = src[1];
+                if (gm + 2 < M) v.z = src[2];
+                if (gm + 3 < M) v.w = src[3];
+            }
+        }
+        return v;
+    };
+    auto load_b = [&](int idx, int64_t k0) -> float4 {
+        if (FAST) {
+            if (!TB)
+                return *reinterpret_cast<const float4 *>(B + (k0 + (idx >> 5)) * p.ldb + n0 + (idx & 31) * 4);
+            return *reinterpret_cast<const float4 *>(B + (n0 + (idx >> 2)) * p.ldb + k0 + (idx & 3) * 4);
+        }
+        float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (!TB) {
+            const int64_t gk = k0 + (idx >> 5), gn = n0 + (idx & 31) * 4;
+            if (gk < kend) {
+                const float *src = B + gk * p.ldb + gn;
+                if (gn + 0 < N) w.x = src[0];
+                if (gn + 1 < N) w.y = src[1];
+                if (gn + 2 < N) w.z = src[2];
+                if (gn + 3 < N) w.w = src[3];
+            }
+        } else {
+            const int64_t gn = n0 + (idx >> 2), gk = k0 + (idx & 3) * 4;
+            if (gn < N) {
+                const float *src = B + gn * p.ldb + gk;
+                if (gk + 0 < kend) w.x = src[0];
+                if (gk + 1 < kend) w.y = src[1];
+                if (gk + 2 < kend) w.z = src[2];
+                if (gk + 3 < kend) w.w = src[3];
+            }
+        }
+        return w;
+    };
+    auto load = [&](int64_t k0) {
+        ra0 = load_a(tid, k0);
+        ra1 = load_a(tid + 256, k0);
+        rb0 = load_b(tid, k0);
+        rb1 = load_b(tid + 256, k0);
+    };
+    auto store_a = [&](int buf, int idx, const float4 &v) {
+        if (!TA) {
+            const int row = idx >> 2, kq = (idx & 3) * 4;
+            As[buf][kq + 0][row] = v.x;
+            As[buf][kq + 1][row] = v.y;
+            As[buf][kq + 2][row] = v.z;
+            As[buf][kq + 3][row] = v.w;
+        } else {
+            *reinterpret_cast<float4 *>(&As[buf][idx >> 5][(idx & 31) * 4]) = v;
+        }
+    };
+    auto store_b = [&](int buf, int idx, const float4 &v) {
+        if (!TB) {
+            *reinterpret_cast<float4 *>(&Bs[buf][idx >> 5][(idx & 31) * 4]) = v;
+        } else {
+            const int col = idx >> 2, kq = (idx & 3) * 4;
+            Bs[buf][kq + 0][col] = v.x;
+            Bs[buf][kq + 1][col] = v.y;
+            Bs[buf][kq + 2][col] = v.z;
+            Bs[buf][kq + 3][col] = v.w;
+        }
+    };
+    auto store = [&](int buf) {
+        store_a(buf, tid, ra0);
+        store_a(buf, tid + 256, ra1);
+        store_b(buf, tid, rb0);
+        store_b(buf, tid + 256, rb1);
+    };
+
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+
+    // MFMA operands of one K-tile, read from LDS a tile ahead of their use.
+    float a0[BK / 2][2], b0[BK / 2][2], a1[BK / 2][2], b1[BK / 2][2];
+    auto lread = [&](int buf, float (&a)[BK / 2][2], float (&b)[BK / 2][2]) {
+#pragma unroll
+        for (int kk = 0; kk < BK / 2; ++kk) {
+            a[kk][0] = As[buf][2 * kk + lk][wm * 64 + lr];
+            a[kk][1] = As[buf][2 * kk + lk][wm * 64 + 32 + lr];
+            b[kk][0] = Bs[buf][2 * kk + lk][wn * 64 + lr];
+            b[kk][1] = Bs[buf][2 * kk + lk][wn * 64 + 32 + lr];
+        }
+    };
+    auto mfma_tile = [&](float (&a)[BK / 2][2], float (&b)[BK / 2][2]) {
+#pragma unroll
+        for (int kk = 0; kk < BK / 2; ++kk) {
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][0], b[kk][0], acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][0], b[kk][1], acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][1], b[kk][0], acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][1], b[kk][1], acc[1][1], 0, 0, 0);
+        }
+    };
+
+    // Pipeline: while the MFMAs of tile t run from registers, the operands of
+    // tile t+1 come out of LDS and the global loads of tile t+2 are in flight;
+    // tile t+2 then goes into the LDS stage tile t used. One barrier per tile.
+    const int64_t nk = (kend - kbeg + BK - 1) / BK;
+    if (nk > 0) {
+        load(kbeg);
+        store(0);
+    }
+    __syncthreads();
+    if (nk > 0) lread(0, a0, b0);
+    if (nk > 1) {
+        load(kbeg + BK);
+        store(1);
+    }
+    __syncthreads();
+    auto step = [&](int64_t it, float (&ca)[BK / 2][2], float (&cb)[BK / 2][2],
+                    float (&na)[BK / 2][2], float (&nb)[BK / 2][2]) {
+        if (it + 2 < nk) load(kbeg + (it + 2) * BK);
+        if (it + 1 < nk) lread((int)((it + 1) & 1), na, nb);
+        mfma_tile(ca, cb);
+        if (it + 2 < nk) store((int)(it & 1));
+        __syncthreads();
+    };
+    for (int64_t it = 0; it < nk; it += 2) {
+        step(it, a0, b0, a1, b1);
+        if (it + 1 < nk) step(it + 1, a1, b1, a0, b0);
+    }
+}
+
 template <bool TA, bool TB, int EPI>
-__global__ __launch_bounds__(256) void gemm_f32_mfma(KParams p) {
-    // Row strides chosen so the transposing scalar stores spread over the banks
-    // and the float4 stores stay 16-byte aligned.
-    constexpr int LDA_S = BM + (TA ? 4 : 2);
-    constexpr int LDB_S = BN + (TB ? 2 : 4);
-    __shared__ float As[2][BK][LDA_S];
-    __shared__ float Bs[2][BK][LDB_S];
+__global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
+    __shared__ float As[2][BK][LdsA<TA>::S];
+    __shared__ float Bs[2][BK][LdsB<TB>::S];
 
     const int tid = threadIdx.x;
 
@@ -90,104 +258,6 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(KParams p) {
     const int64_t kend = min(p.k, kbeg + p.k_per_split);
     const int64_t M = p.m, N = p.n;
 
-    float4 ra[2], rb[2];
-
-    auto load = [&](int64_t k0) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = tid + i * 256;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (!TA) {
-                const int64_t gm = m0 + (idx >> 2), gk = k0 + (idx & 3) * 4;
-                if (gm < M) {
-                    const float *src = A + gm * p.lda + gk;
-                    if (p.vec_a && gk + 3 < kend) {
-                        v = *reinterpret_cast<const float4 *>(src);
-                    } else {
-                        if (gk + 0 < kend) v.x = src[0];
-                        if (gk + 1 < kend) v.y = src[1];
-                        if (gk + 2 < kend) v.z = src[2];
-                        if (gk + 3 < kend) v.w = src[3];
-                    }
-                }
-            } else {
-                const int64_t gk = k0 + (idx >> 5), gm = m0 + (idx & 31) * 4;
-                if (gk < kend) {
-                    const float *src = A + gk * p.lda + gm;
-                    if (p.vec_a && gm + 3 < M) {
-                        v = *reinterpret_cast<const float4 *>(src);
-                    } else {
-                        if (gm + 0 < M) v.x = src[0];
-                        if (gm + 1 < M) v.y = src[1];
-                        if (gm + 2 < M) v.z = src[2];
-                        if (gm + 3 < M) v.w = src[3];
-                    }
-                }
-            }
-            ra[i] = v;
-            float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (!TB) {
-                const int64_t gk = k0 + (idx >> 5), gn = n0 + (idx & 31) * 4;
-                if (gk < kend) {
-                    const float *src = B + gk * p.ldb + gn;
-                    if (p.vec_b && gn + 3 < N) {
-                        w = *reinterpret_cast<const float4 *>(src);
-                    } else {
-                        if (gn + 0 < N) w.x = src[0];
-                        if (gn + 1 < N) w.y = src[1];
-                        if (gn + 2 < N) w.z = src[2];
-                        if (gn + 3 < N) w.w = src[3];
-                    }
-                }
-            } else {
-                const int64_t gn = n0 + (idx >> 2), gk = k0 + (idx & 3) * 4;
-                if (gn < N) {
-                    const float *src = B + gn * p.ldb + gk;
-                    if (p.vec_b && gk + 3 < kend) {
-                        w = *reinterpret_cast<const float4 *>(src);
-                    } else {
-                        if (gk + 0 < kend) w.x = src[0];
-                        if (gk + 1 < kend) w.y = src[1];
-                        if (gk + 2 < kend) w.z = src[2];
-                        if (gk + 3 < kend) w.w = src[3];
-                    }
-                }
-            }
-            rb[i] = w;
-        }
-    };
-
-    auto store = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int idx = tid + i * 256;
-            if (!TA) {
-                const int row = idx >> 2, kq = (idx & 3) * 4;
-                As[buf][kq + 0][row] = ra[i].x;
-                As[buf][kq + 1][row] = ra[i].y;
-                As[buf][kq + 2][row] = ra[i].z;
-                As[buf][kq + 3][row] = ra[i].w;
-            } else {
-                const int kr = idx >> 5, mq = (idx & 31) * 4;
-                *reinterpret_cast<float4 *>(&As[buf][kr][mq]) = ra[i];
-            }
-            if (!TB) {
-                const int kr = idx >> 5, nq = (idx & 31) * 4;
-                *reinterpret_cast<float4 *>(&Bs[buf][kr][nq]) = rb[i];
-            } else {
-                const int col = idx >> 2, kq = (idx & 3) * 4;
-                Bs[buf][kq + 0][col] = rb[i].x;
-                Bs[buf][kq + 1][col] = rb[i].y;
-                Bs[buf][kq + 2][col] = rb[i].z;
-                Bs[buf][kq + 3][col] = rb[i].w;
-            }
-        }
-    };
-
-    const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
-    const int lr = lane & 31, lk = lane >> 5;
-
     floatx16 acc[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -196,29 +266,16 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma(KParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-    const int64_t nk = (kend - kbeg + BK - 1) / BK;
-    if (nk > 0) {
-        load(kbeg);
-        store(0);
-    }
-    __syncthreads();
-    for (int64_t it = 0; it < nk; ++it) {
-        const int cur = (int)(it & 1);
-        if (it + 1 < nk) load(kbeg + (it + 1) * BK);
-#pragma unroll
-        for (int kk = 0; kk < BK; kk += 2) {
-            const float a0 = As[cur][kk + lk][wm * 64 + lr];
-            const float a1 = As[cur][kk + lk][wm * 64 + 32 + lr];
-            const float b0 = Bs[cur][kk + lk][wn * 64 + lr];
-            const float b1 = Bs[cur][kk + lk][wn * 64 + 32 + lr];
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc[1][1], 0, 0, 0);
-        }
-        if (it + 1 < nk) store(cur ^ 1);
-        __syncthreads();
-    }
+    const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
+                      (kend - kbeg) % BK == 0;
+    if (fast)
+        gemm_mainloop<TA, TB, true>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+    else
+        gemm_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
 
     // ---- epilogue ----
     if (p.splits > 1) {
