@@ -3,18 +3,26 @@
 // Replaces the reference's three CPU kernels (midman-tensor/src/kernels.rs:49-108,
 // kernels_avx.rs:45-250): C = A.B (nn), A.B^T (nt) and A^T.B (tn). The
 // transposed forms never materialize a transpose (the reference copies B^T,
-// kernels.rs:68-73): the operand is read in its stored layout and written into
-// LDS k-major, which is the layout the MFMA operand reads want.
+// kernels.rs:68-73): each operand is read in its stored layout and written into
+// LDS k-major, the layout the MFMA operand reads want.
 //
 // Tiling: a 256-thread workgroup (4 wave64s, 2x2) owns a 128x128 tile of C;
-// each wave owns 64x64 = 2x2 MFMA 32x32 blocks (64 accumulators per lane).
-// K advances 16 at a time through a double-buffered LDS stage: the next tile's
-// global loads are issued before the current tile's 32 MFMAs per wave and
-// written to the other LDS buffer after them, with one barrier per step.
+// each wave owns 64x64 as 2x2 MFMA 32x32 blocks (64 accumulators per lane).
+// The wave's two row blocks take the even and the odd rows of its 64 (and the
+// two column blocks the even and odd columns), so one 8-byte LDS read gives a
+// lane its operand for both blocks, at an immediate offset from one base
+// address, and the epilogue writes column pairs.
 //
 // MFMA 32x32x2 f32 operand layout (wave64): lane l supplies A[i=l%32][k=l/32]
 // and B[k=l/32][j=l%32]; accumulator register r of lane l holds
 // D[i = 8*(r/4) + 4*(l/32) + r%4][j = l%32].
+//
+// K advances 32 at a time through two LDS stages, software-pipelined: while
+// the 64 MFMAs per wave of tile t run, tile t+1 waits in registers and tile
+// t+2's global loads are issued as soon as tile t+1 is in LDS. One barrier per
+// tile. Interior tiles take a path with no
+// load predicates and 32-bit offsets from uniform base pointers; edge tiles
+// zero-fill outside [M, N, K).
 //
 // Workgroup -> tile mapping is XCD-aware: the dispatcher hands workgroup w to
 // XCD w % 8, so w is renumbered to make each XCD's share a contiguous run of
@@ -31,7 +39,7 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int BM = 128, BN = 128, BK = 32;
 constexpr int GROUP_M = 8;
 
 struct KParams {
@@ -46,7 +54,7 @@ struct KParams {
     int64_t swiglu_ff;
     int tiles_m, tiles_n;
     int splits;
-    int vec_a, vec_b;
+    int vec_a, vec_b, vec_c;
 };
 
 __device__ __forceinline__ float silu_f(float x) {
@@ -55,8 +63,9 @@ __device__ __forceinline__ float silu_f(float x) {
     return __fmul_rn(x, s);
 }
 
-// Row strides of the LDS stages, chosen so the transposing scalar stores
-// spread over the banks and the float4 stores stay 16-byte aligned.
+// Row strides (floats) of the k-major LDS stages: even, so the 8-byte operand
+// reads stay aligned; +2 where the stores transpose (spreads consecutive k rows
+// over the banks), +4 where they are float4 (keeps 16-byte alignment).
 template <bool TA>
 struct LdsA {
     static constexpr int S = BM + (TA ? 4 : 2);
@@ -66,9 +75,7 @@ struct LdsB {
     static constexpr int S = BN + (TB ? 2 : 4);
 };
 
-// The K loop of one 128x128 tile. FAST: the whole tile lies inside M, N and
-// the K range is a multiple of BK with 16-byte aligned rows, so no load needs
-// a predicate; otherwise every element is bounds-checked and zero-filled.
+// The K loop of one 128x128 tile; see the file comment.
 template <bool TA, bool TB, bool FAST>
 __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__restrict__ A,
                                               const float *__restrict__ B, int64_t m0, int64_t n0,
@@ -78,19 +85,29 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                                               floatx16 (&acc)[2][2]) {
     const int tid = threadIdx.x;
     const int64_t M = p.m, N = p.n;
-    // One K-tile is 2 float4 of A and 2 float4 of B per thread, held in
-    // named registers (an indexed array here ends up in scratch memory).
-    float4 ra0, ra1, rb0, rb1;
+    // A K-tile of each operand is 128 x 32 floats = 1024 float4; thread tid
+    // moves float4 idx = tid + 256*i, i < 4.
+    // Row-major-in-k operands (A for nn/nt, B for nt): row idx/8, k (idx%8)*4.
+    // k-major operands (A for tn, B for nn/tn): k idx/32, column (idx%32)*4.
+    constexpr int NL = 4;
+    // Uniform bases (moved by the tile's k) and 32-bit per-thread offsets.
+    const float *a_base = TA ? A + m0 : A + m0 * p.lda;
+    const float *b_base = TB ? B + n0 * p.ldb : B + n0;
+    const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)p.ldb;
+    uint32_t ao[NL], bo[NL];
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int idx = tid + 256 * i;
+        ao[i] = TA ? (uint32_t)(idx >> 5) * lda + (idx & 31) * 4 : (uint32_t)(idx >> 3) * lda + (idx & 7) * 4;
+        bo[i] = TB ? (uint32_t)(idx >> 3) * ldb + (idx & 7) * 4 : (uint32_t)(idx >> 5) * ldb + (idx & 31) * 4;
+    }
 
-    auto load_a = [&](int idx, int64_t k0) -> float4 {
-        if (FAST) {
-            if (!TA)
-                return *reinterpret_cast<const float4 *>(A + (m0 + (idx >> 2)) * p.lda + k0 + (idx & 3) * 4);
-            return *reinterpret_cast<const float4 *>(A + (k0 + (idx >> 5)) * p.lda + m0 + (idx & 31) * 4);
-        }
+    float4 ra[NL], rb[NL];
+
+    auto load_a_edge = [&](int idx, int64_t k0) __attribute__((always_inline)) -> float4 {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (!TA) {
-            const int64_t gm = m0 + (idx >> 2), gk = k0 + (idx & 3) * 4;
+            const int64_t gm = m0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
             if (gm < M) {
                 const float *src = A + gm * p.lda + gk;
                 if (gk + 0 < kend) v.x = src[0];
@@ -110,12 +127,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
         }
         return v;
     };
-    auto load_b = [&](int idx, int64_t k0) -> float4 {
-        if (FAST) {
-            if (!TB)
-                return *reinterpret_cast<const float4 *>(B + (k0 + (idx >> 5)) * p.ldb + n0 + (idx & 31) * 4);
-            return *reinterpret_cast<const float4 *>(B + (n0 + (idx >> 2)) * p.ldb + k0 + (idx & 3) * 4);
-        }
+    auto load_b_edge = [&](int idx, int64_t k0) __attribute__((always_inline)) -> float4 {
         float4 w = make_float4(0.f, 0.f, 0.f, 0.f);
         if (!TB) {
             const int64_t gk = k0 + (idx >> 5), gn = n0 + (idx & 31) * 4;
@@ -127,7 +139,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                 if (gn + 3 < N) w.w = src[3];
             }
         } else {
-            const int64_t gn = n0 + (idx >> 2), gk = k0 + (idx & 3) * 4;
+            const int64_t gn = n0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
             if (gn < N) {
                 const float *src = B + gn * p.ldb + gk;
                 if (gk + 0 < kend) w.x = src[0];
@@ -138,99 +150,104 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
         }
         return w;
     };
-    auto load = [&](int64_t k0) {
-        ra0 = load_a(tid, k0);
-        ra1 = load_a(tid + 256, k0);
-        rb0 = load_b(tid, k0);
-        rb1 = load_b(tid + 256, k0);
-    };
-    auto store_a = [&](int buf, int idx, const float4 &v) {
-        if (!TA) {
-            const int row = idx >> 2, kq = (idx & 3) * 4;
-            As[buf][kq + 0][row] = v.x;
-            As[buf][kq + 1][row] = v.y;
-            As[buf][kq + 2][row] = v.z;
-            As[buf][kq + 3][row] = v.w;
+    auto load = [&](int64_t k0) __attribute__((always_inline)) {
+        if (FAST) {
+            const float *ak = TA ? a_base + k0 * p.lda : a_base + k0;
+            const float *bk = TB ? b_base + k0 : b_base + k0 * p.ldb;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) ra[i] = *reinterpret_cast<const float4 *>(ak + ao[i]);
+#pragma unroll
+            for (int i = 0; i < NL; ++i) rb[i] = *reinterpret_cast<const float4 *>(bk + bo[i]);
         } else {
-            *reinterpret_cast<float4 *>(&As[buf][idx >> 5][(idx & 31) * 4]) = v;
+#pragma unroll
+            for (int i = 0; i < NL; ++i) ra[i] = load_a_edge(tid + 256 * i, k0);
+#pragma unroll
+            for (int i = 0; i < NL; ++i) rb[i] = load_b_edge(tid + 256 * i, k0);
         }
     };
-    auto store_b = [&](int buf, int idx, const float4 &v) {
-        if (!TB) {
-            *reinterpret_cast<float4 *>(&Bs[buf][idx >> 5][(idx & 31) * 4]) = v;
-        } else {
-            const int col = idx >> 2, kq = (idx & 3) * 4;
-            Bs[buf][kq + 0][col] = v.x;
-            Bs[buf][kq + 1][col] = v.y;
-            Bs[buf][kq + 2][col] = v.z;
-            Bs[buf][kq + 3][col] = v.w;
+    auto store = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int idx = tid + 256 * i;
+            if (!TA) {
+                const int row = idx >> 3, kq = (idx & 7) * 4;
+                As[buf][kq + 0][row] = ra[i].x;
+                As[buf][kq + 1][row] = ra[i].y;
+                As[buf][kq + 2][row] = ra[i].z;
+                As[buf][kq + 3][row] = ra[i].w;
+            } else {
+                float *dst = &As[buf][idx >> 5][(idx & 31) * 4];
+                dst[0] = ra[i].x;
+                dst[1] = ra[i].y;
+                dst[2] = ra[i].z;
+                dst[3] = ra[i].w;
+            }
+            if (!TB) {
+                float *dst = &Bs[buf][idx >> 5][(idx & 31) * 4];
+                dst[0] = rb[i].x;
+                dst[1] = rb[i].y;
+                dst[2] = rb[i].z;
+                dst[3] = rb[i].w;
+            } else {
+                const int col = idx >> 3, kq = (idx & 7) * 4;
+                Bs[buf][kq + 0][col] = rb[i].x;
+                Bs[buf][kq + 1][col] = rb[i].y;
+                Bs[buf][kq + 2][col] = rb[i].z;
+                Bs[buf][kq + 3][col] = rb[i].w;
+            }
         }
-    };
-    auto store = [&](int buf) {
-        store_a(buf, tid, ra0);
-        store_a(buf, tid + 256, ra1);
-        store_b(buf, tid, rb0);
-        store_b(buf, tid + 256, rb1);
     };
 
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, lk = lane >> 5;
 
-    // MFMA operands of one K-tile, read from LDS a tile ahead of their use.
-    float a0[BK / 2][2], b0[BK / 2][2], a1[BK / 2][2], b1[BK / 2][2];
-    auto lread = [&](int buf, float (&a)[BK / 2][2], float (&b)[BK / 2][2]) {
+    // One tile's MFMAs from LDS stage `buf`: all operand reads are issued
+    // first (for each k-pair kk the float2 holds the operand of row or column
+    // block 0 and of block 1); the MFMAs consume them in order as they land.
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        const float *pa = &As[buf][lk][wm * 64 + 2 * lr];
+        const float *pb = &Bs[buf][lk][wn * 64 + 2 * lr];
+        float2 a[BK / 2], b[BK / 2];
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) {
-            a[kk][0] = As[buf][2 * kk + lk][wm * 64 + lr];
-            a[kk][1] = As[buf][2 * kk + lk][wm * 64 + 32 + lr];
-            b[kk][0] = Bs[buf][2 * kk + lk][wn * 64 + lr];
-            b[kk][1] = Bs[buf][2 * kk + lk][wn * 64 + 32 + lr];
+            a[kk] = *reinterpret_cast<const float2 *>(pa + 2 * kk * LdsA<TA>::S);
+            b[kk] = *reinterpret_cast<const float2 *>(pb + 2 * kk * LdsB<TB>::S);
         }
-    };
-    auto mfma_tile = [&](float (&a)[BK / 2][2], float (&b)[BK / 2][2]) {
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) {
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][0], b[kk][0], acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][0], b[kk][1], acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][1], b[kk][0], acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][1], b[kk][1], acc[1][1], 0, 0, 0);
+            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].x, b[kk].x, acc[0][0], 0, 0, 0);
+            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].x, b[kk].y, acc[0][1], 0, 0, 0);
+            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].y, b[kk].x, acc[1][0], 0, 0, 0);
+            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].y, b[kk].y, acc[1][1], 0, 0, 0);
         }
     };
 
-    // Pipeline: while the MFMAs of tile t run from registers, the operands of
-    // tile t+1 come out of LDS and the global loads of tile t+2 are in flight;
-    // tile t+2 then goes into the LDS stage tile t used. One barrier per tile.
-    const int64_t nk = (kend - kbeg + BK - 1) / BK;
+    // Pipeline: stage t%2 holds tile t and the registers hold tile t+1 when
+    // iteration t starts. The MFMAs of tile t run; tile t+1 then goes into the
+    // other stage (last read in iteration t-1, before its barrier), the global
+    // loads of tile t+2 are issued, and one barrier ends the iteration; those
+    // loads land while tile t+1 is being multiplied.
+    const int nk = (int)((kend - kbeg + BK - 1) / BK);
     if (nk > 0) {
         load(kbeg);
         store(0);
     }
+    if (nk > 1) load(kbeg + BK);
     __syncthreads();
-    if (nk > 0) lread(0, a0, b0);
-    if (nk > 1) {
-        load(kbeg + BK);
-        store(1);
-    }
-    __syncthreads();
-    auto step = [&](int64_t it, float (&ca)[BK / 2][2], float (&cb)[BK / 2][2],
-                    float (&na)[BK / 2][2], float (&nb)[BK / 2][2]) {
-        if (it + 2 < nk) load(kbeg + (it + 2) * BK);
-        if (it + 1 < nk) lread((int)((it + 1) & 1), na, nb);
-        mfma_tile(ca, cb);
-        if (it + 2 < nk) store((int)(it & 1));
+    for (int it = 0; it < nk; ++it) {
+        const int cur = it & 1;
+        compute(cur);
+        if (it + 1 < nk) store(cur ^ 1);
+        if (it + 2 < nk) load(kbeg + (int64_t)(it + 2) * BK);
         __syncthreads();
-    };
-    for (int64_t it = 0; it < nk; it += 2) {
-        step(it, a0, b0, a1, b1);
-        if (it + 1 < nk) step(it + 1, a1, b1, a0, b0);
     }
 }
 
 template <bool TA, bool TB, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
-    __shared__ float As[2][BK][LdsA<TA>::S];
-    __shared__ float Bs[2][BK][LdsB<TB>::S];
+    __shared__ __attribute__((aligned(16))) float As[2][BK][LdsA<TA>::S];
+    __shared__ __attribute__((aligned(16))) float Bs[2][BK][LdsB<TB>::S];
 
     const int tid = threadIdx.x;
 
@@ -273,57 +290,61 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
     else
         gemm_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
 
+    // ---- epilogue: block (i, j) register r of lane l is C[row][col] with
+    // row = base_row + 2*(8*(r/4) + 4*(l/32) + r%4) + i, col = base_col + 2*(l%32) + j.
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, lk = lane >> 5;
-
-    // ---- epilogue ----
+    const int64_t col = n0 + wn * 64 + 2 * lr;
     if (p.splits > 1) {
         float *P = p.partial + (int64_t)split * M * N;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + lk * 4 + (r & 3);
-                    const int64_t col = n0 + wn * 64 + j * 32 + lr;
-                    if (row < M && col < N) P[row * N + col] = acc[i][j][r];
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
+                if (row < M) {
+                    if (col < N) P[row * N + col] = acc[i][0][r];
+                    if (col + 1 < N) P[row * N + col + 1] = acc[i][1][r];
                 }
+            }
         return;
     }
     float *C = p.c + batch * p.stride_c;
     if (EPI == EPI_SWIGLU) {
-        // Packed columns: each 64-column group g holds 32 gate columns then the
-        // 32 matching up columns, so a wave's j=0 block is gate and j=1 is up.
-        const int64_t g = (n0 + wn * 64) >> 6;
-        const int64_t col = g * 32 + lr;
+        // Packed columns interleave gate and up: column 2f is gate f, 2f+1 up f.
+        const int64_t f = col >> 1;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + lk * 4 + (r & 3);
-                if (row < M && col < p.swiglu_ff)
-                    C[row * p.ldc + col] = __fmul_rn(silu_f(acc[i][0][r]), acc[i][1][r]);
+                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
+                if (row < M && f < p.swiglu_ff)
+                    C[row * p.ldc + f] = __fmul_rn(silu_f(acc[i][0][r]), acc[i][1][r]);
             }
         return;
     }
+    const bool pair = p.vec_c && col + 1 < N;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 64 + i * 32 + (r >> 2) * 8 + lk * 4 + (r & 3);
-                const int64_t col = n0 + wn * 64 + j * 32 + lr;
-                if (row < M && col < N) {
-                    float *dst = C + row * p.ldc + col;
-                    if (EPI == EPI_ACCUM)
-                        *dst = __fadd_rn(*dst, acc[i][j][r]);
-                    else
-                        *dst = acc[i][j][r];
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
+            if (row >= M) continue;
+            float *dst = C + row * p.ldc + col;
+            float v0 = acc[i][0][r], v1 = acc[i][1][r];
+            if (pair) {
+                if (EPI == EPI_ACCUM) {
+                    const float2 o = *reinterpret_cast<const float2 *>(dst);
+                    v0 = __fadd_rn(o.x, v0);
+                    v1 = __fadd_rn(o.y, v1);
                 }
+                *reinterpret_cast<float2 *>(dst) = make_float2(v0, v1);
+            } else {
+                if (col < N) dst[0] = EPI == EPI_ACCUM ? __fadd_rn(dst[0], v0) : v0;
+                if (col + 1 < N) dst[1] = EPI == EPI_ACCUM ? __fadd_rn(dst[1], v1) : v1;
             }
+        }
 }
 
 // Sums split partials in split order, then applies the epilogue.
@@ -380,8 +401,14 @@ void gemm(Context &ctx, const GemmDesc &d) {
     p.swiglu_ff = d.swiglu_ff;
     p.tiles_m = (int)((d.m + BM - 1) / BM);
     p.tiles_n = (int)((d.n + BN - 1) / BN);
-    p.vec_a = (d.lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(d.a);
-    p.vec_b = (d.ldb % 4 == 0) && (d.batch == 1 || d.stride_b % 4 == 0) && aligned16(d.b);
+    // The interior path addresses a tile with 32-bit offsets (< 128 rows of ld).
+    const int64_t off_limit = int64_t(1) << 31;
+    p.vec_a = (d.lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(d.a) &&
+              d.lda * BM < off_limit;
+    p.vec_b = (d.ldb % 4 == 0) && (d.batch == 1 || d.stride_b % 4 == 0) && aligned16(d.b) &&
+              d.ldb * BN < off_limit;
+    p.vec_c = (d.ldc % 2 == 0) && (d.batch == 1 || d.stride_c % 2 == 0) &&
+              (reinterpret_cast<uintptr_t>(d.c) & 7) == 0;
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     const int64_t ktiles = (d.k + BK - 1) / BK;

@@ -84,6 +84,53 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__
     }
 }
 
+// The same for rows of d <= 256*NV floats (d % 4 == 0): the wave keeps its row
+// in registers, so x is read once, and all NV float4 loads per lane are issued
+// before the first is used.
+template <int NV>
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *__restrict__ x,
+                                                            const float *__restrict__ w,
+                                                            int64_t rows, int d, float eps,
+                                                            float *__restrict__ out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int d4 = d >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + row * d);
+    float4 v[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int j = lane + 64 * i;
+        v[i] = j < d4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        ss = __fadd_rn(ss, __fmul_rn(v[i].x, v[i].x));
+        ss = __fadd_rn(ss, __fmul_rn(v[i].y, v[i].y));
+        ss = __fadd_rn(ss, __fmul_rn(v[i].z, v[i].z));
+        ss = __fadd_rn(ss, __fmul_rn(v[i].w, v[i].w));
+    }
+    ss = wave_sum(ss);
+    const float mean = __fmul_rn(ss, __fdiv_rn(1.0f, (float)d));
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 *o4 = reinterpret_cast<float4 *>(out + row * d);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int j = lane + 64 * i;
+        if (j < d4) {
+            const float4 g = w4[j];
+            float4 r;
+            r.x = __fmul_rn(__fmul_rn(v[i].x, inv), g.x);
+            r.y = __fmul_rn(__fmul_rn(v[i].y, inv), g.y);
+            r.z = __fmul_rn(__fmul_rn(v[i].z, inv), g.z);
+            r.w = __fmul_rn(__fmul_rn(v[i].w, inv), g.w);
+            o4[j] = r;
+        }
+    }
+}
+
 // ---- add: ops_elementwise.rs:249-259 (same-shape path) -----------------------
 __global__ __launch_bounds__(256) void add_kernel(const float *__restrict__ a,
                                                   const float *__restrict__ b,
@@ -125,9 +172,11 @@ __global__ __launch_bounds__(256) void rope_kernel(const float *__restrict__ x, 
 }
 
 // ---- cross-entropy: ops_reduce.rs:253-259 --------------------------------------
-// One workgroup per row, one pass over the logits: each thread keeps a running
-// (max, sum of exp(z - max)) pair that is rescaled when the max grows; pairs
-// merge across the workgroup. The row term is formed as the reference forms it,
+// One workgroup per row and one pass over the logits. Each thread loads chunks
+// of 4 float4, takes the chunk max (fmaxf, which ignores NaN like f32::max),
+// rescales its running sum of exp(z - max) once per chunk when the max grows,
+// and adds the chunk's 16 exponentials; (max, sum) pairs then merge across the
+// workgroup. The row term is formed as the reference forms it,
 // (max + ln(sum)) - z[target], in f32.
 __device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2) {
     if (m2 == -INFINITY) return;
@@ -137,10 +186,10 @@ __device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2
         return;
     }
     if (m2 > m) {
-        s = __fadd_rn(__fmul_rn(s, expf(m - m2)), s2);
+        s = s * expf(m - m2) + s2;
         m = m2;
     } else {
-        s = __fadd_rn(s, __fmul_rn(s2, expf(m2 - m)));
+        s = s + s2 * expf(m2 - m);
     }
 }
 
@@ -148,28 +197,39 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float *__restrict__ 
                                                       const int32_t *__restrict__ targets,
                                                       int64_t n, int64_t v,
                                                       float *__restrict__ row_loss, int vec) {
+    constexpr int CH = 4;
     const int64_t row = blockIdx.x;
     const float *z = logits + row * v;
+    const float4 *z4 = reinterpret_cast<const float4 *>(z);
+    const int64_t v4 = vec ? v / 4 : 0;
     float m = -INFINITY, s = 0.0f;
-    auto add = [&](float x) {
+    for (int64_t j0 = threadIdx.x; j0 < v4; j0 += 256 * CH) {
+        float4 a[CH];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t j = j0 + 256 * c;
+            a[c] = j < v4 ? z4[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            cm = fmaxf(cm, fmaxf(fmaxf(a[c].x, a[c].y), fmaxf(a[c].z, a[c].w)));
+        }
+        if (cm == -INFINITY) continue;
+        if (cm > m) {
+            s = s * expf(m - cm);
+            m = cm;
+        }
+        float cs = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+            cs += expf(a[c].x - m) + expf(a[c].y - m) + expf(a[c].z - m) + expf(a[c].w - m);
+        s += cs;
+    }
+    for (int64_t k = v4 * 4 + threadIdx.x; k < v; k += 256) {
+        const float x = z[k];
         if (x > m) {
-            s = (m == -INFINITY) ? 1.0f : __fadd_rn(__fmul_rn(s, expf(m - x)), 1.0f);
+            s = (m == -INFINITY) ? 0.0f : s * expf(m - x);
             m = x;
-        } else {
-            s = __fadd_rn(s, expf(x - m));
         }
-    };
-    if (vec) {
-        const float4 *z4 = reinterpret_cast<const float4 *>(z);
-        for (int64_t j = threadIdx.x; j < v / 4; j += 256) {
-            const float4 q = z4[j];
-            add(q.x);
-            add(q.y);
-            add(q.z);
-            add(q.w);
-        }
-    } else {
-        for (int64_t j = threadIdx.x; j < v; j += 256) add(z[j]);
+        s += expf(x - m);
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) {
@@ -219,8 +279,8 @@ __global__ __launch_bounds__(256) void pack_cols_kernel(const float *__restrict_
     }
 }
 
-// dst [rows, 2*ff_pad]: column 64g+c is gate column 32g+c (c < 32) and column
-// 64g+32+c is up column 32g+c; columns past ff are zero.
+// dst [rows, 2*ff_pad]: column 2f is gate column f and column 2f+1 is up
+// column f; columns of f >= ff are zero.
 __global__ __launch_bounds__(256) void pack_gate_up_kernel(const float *__restrict__ wg,
                                                            const float *__restrict__ wu,
                                                            int64_t rows, int64_t ff,
@@ -230,10 +290,9 @@ __global__ __launch_bounds__(256) void pack_gate_up_kernel(const float *__restri
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * blockDim.x) {
         const int64_t r = i / cols, c2 = i - r * cols;
-        const int64_t g = c2 >> 6, c = c2 & 63;
-        const int64_t col = g * 32 + (c & 31);
-        const float *src = c < 32 ? wg : wu;
-        dst[i] = col < ff ? src[r * ff + col] : 0.0f;
+        const int64_t f = c2 >> 1;
+        const float *src = (c2 & 1) ? wu : wg;
+        dst[i] = f < ff ? src[r * ff + f] : 0.0f;
     }
 }
 
@@ -259,6 +318,22 @@ void launch_embedding(Context &ctx, const float *table, int64_t d, const int32_t
 void launch_rms_norm(Context &ctx, const float *x, const float *w, int64_t rows, int64_t d,
                      float eps, float *out) {
     const int vec = (d % 4 == 0) && al16(x) && al16(w) && al16(out);
+    if (vec && d <= 4096) {
+        const dim3 grid((unsigned)((rows + 3) / 4)), block(256);
+        const int dd = (int)d;
+        if (d <= 256)
+            hipLaunchKernelGGL(rms_norm_rows_kernel<1>, grid, block, 0, ctx.stream, x, w, rows, dd, eps, out);
+        else if (d <= 512)
+            hipLaunchKernelGGL(rms_norm_rows_kernel<2>, grid, block, 0, ctx.stream, x, w, rows, dd, eps, out);
+        else if (d <= 1024)
+            hipLaunchKernelGGL(rms_norm_rows_kernel<4>, grid, block, 0, ctx.stream, x, w, rows, dd, eps, out);
+        else if (d <= 2048)
+            hipLaunchKernelGGL(rms_norm_rows_kernel<8>, grid, block, 0, ctx.stream, x, w, rows, dd, eps, out);
+        else
+            hipLaunchKernelGGL(rms_norm_rows_kernel<16>, grid, block, 0, ctx.stream, x, w, rows, dd, eps, out);
+        check_hip(hipGetLastError(), "rms_norm launch");
+        return;
+    }
     hipLaunchKernelGGL(rms_norm_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
                        ctx.stream, x, w, rows, d, eps, out, vec);
     check_hip(hipGetLastError(), "rms_norm launch");
