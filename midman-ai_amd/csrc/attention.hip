@@ -44,16 +44,17 @@ struct AttnP {
 };
 
 template <int HD>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
-    constexpr int NS = HD / 2;               // MFMA k-steps over the head dim
-    constexpr int NDB = (HD + 31) / 32;      // 32-wide blocks of the head dim
-    constexpr int KS = HD + 1;               // K row stride in LDS (odd: no bank conflicts)
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
+    constexpr int NS = HD / 2;               // S^T k-steps (lanes 32-63 take dims NS..HD-1)
+    constexpr int NDB = (HD + 31) / 32;      // O^T row blocks; block db row i is dim NDB*i+db
+    constexpr int KS = HD + 4;               // K row stride: 16-byte aligned rows
+    constexpr int OS = HD + 1;               // output staging stride: odd, conflict-free
     constexpr int F4 = 32 * HD / 4;          // float4s per K or V tile
     constexpr int PER = (F4 + 255) / 256;    // float4s per thread per tile
     // Two K stages [32][KS] and two V stages [32][HD]; at the end the same
-    // memory holds the 4 waves' outputs as [128][KS], which is the larger size.
+    // memory holds the 4 waves' outputs as [128][OS].
     constexpr int STAGES = 2 * 32 * KS + 2 * 32 * HD;
-    constexpr int OUT = 128 * KS;
+    constexpr int OUT = 128 * OS;
     __shared__ __attribute__((aligned(16))) float smem[STAGES > OUT ? STAGES : OUT];
     auto Ks = [&](int buf) { return smem + buf * 32 * KS; };
     auto Vs = [&](int buf) { return smem + 64 * KS + buf * 32 * HD; };
@@ -78,25 +79,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
     float qr[NS];
     {
         const int qi = min(q0 + lq, T - 1);
-        const float4 *src = reinterpret_cast<const float4 *>(Q + (int64_t)qi * p.sqt + lh * NS);
+        const float *src = Q + (int64_t)qi * p.sqt + lh * NS;
         if (NS % 4 == 0) {
 #pragma unroll
             for (int s = 0; s < NS / 4; ++s) {
-                const float4 v = src[s];
+                const float4 v = reinterpret_cast<const float4 *>(src)[s];
                 qr[4 * s + 0] = v.x;
                 qr[4 * s + 1] = v.y;
                 qr[4 * s + 2] = v.z;
                 qr[4 * s + 3] = v.w;
             }
         } else {
-            const float *s1 = Q + (int64_t)qi * p.sqt + lh * NS;
 #pragma unroll
-            for (int s = 0; s < NS; ++s) qr[s] = s1[s];
+            for (int s = 0; s < NS; ++s) qr[s] = src[s];
         }
     }
 
     float4 kreg[PER], vreg[PER];
-    auto load_tile = [&](int kt) {
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int f = tid + i * 256;
@@ -113,7 +113,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
             vreg[i] = vv;
         }
     };
-    auto store_tile = [&](int buf) {
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int f = tid + i * 256;
@@ -124,7 +124,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
                 kd[1] = kreg[i].y;
                 kd[2] = kreg[i].z;
                 kd[3] = kreg[i].w;
-                *reinterpret_cast<float4 *>(Vs(buf) + j * HD + c) = vreg[i];
+                float *vd = Vs(buf) + j * HD + c;
+                vd[0] = vreg[i].x;
+                vd[1] = vreg[i].y;
+                vd[2] = vreg[i].z;
+                vd[3] = vreg[i].w;
             }
         }
     };
@@ -134,6 +138,11 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    // Softmax state in log2 units: scores are scaled by scale * log2(e) and
+    // exponentials are exp2. m_run is raised only when some lane's max grows
+    // by more than 8 (then every exponential stays <= 2^8); O and l share the
+    // same stale max, so O / l is unchanged.
+    const float sc = p.scale * 1.4426950408889634f;
     float m_run = -INFINITY, l_run = 0.0f;
     const int qi = q0 + lq;
 
@@ -146,50 +155,80 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
         if (kt < my_tiles) {
             const float *Kb = Ks(cur);
             const float *Vb = Vs(cur);
-            floatx16 sacc;
+            // S^T = K . Q^T: two independent accumulator chains, summed.
+            floatx16 sacc, sacc1;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) sacc[r] = 0.0f;
+            for (int r = 0; r < 16; ++r) {
+                sacc[r] = 0.0f;
+                sacc1[r] = 0.0f;
+            }
+            const float *krow = Kb + lq * KS + lh * NS;
+            if (NS % 4 == 0) {
 #pragma unroll
-            for (int s = 0; s < NS; ++s)
-                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(Kb[lq * KS + lh * NS + s], qr[s], sacc,
-                                                            0, 0, 0);
-            // Scale, mask, online softmax for query qi (shared by lanes l, l^32).
+                for (int t = 0; t < NS / 4; ++t) {
+                    const float4 kv = reinterpret_cast<const float4 *>(krow)[t];
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, qr[4 * t + 0], sacc, 0, 0, 0);
+                    sacc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, qr[4 * t + 1], sacc1, 0, 0, 0);
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, qr[4 * t + 2], sacc, 0, 0, 0);
+                    sacc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, qr[4 * t + 3], sacc1, 0, 0, 0);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < NS; ++s)
+                    sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(krow[s], qr[s], sacc, 0, 0, 0);
+            }
             const int k0 = kt * 32;
             float pv[16];
             float mloc = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const float sv = sacc[r] * p.scale;
+                const float sv = (sacc[r] + sacc1[r]) * sc;
                 pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
                 mloc = fmaxf(mloc, pv[r]);
             }
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            const float m_new = fmaxf(m_run, mloc);
-            const float alpha = expf(m_run - m_new);
+            const bool need = mloc > m_run + 8.0f;  // always true on the first tile
+            if (__any(need)) {
+                const float m_new = need ? mloc : m_run;
+                const float alpha = exp2f(m_run - m_new);
+                l_run *= alpha;
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+                m_run = m_new;
+            }
             float lsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                pv[r] = expf(pv[r] - m_new);
+                pv[r] = exp2f(pv[r] - m_run);
                 lsum += pv[r];
             }
             lsum += __shfl_xor(lsum, 32, 64);
-            l_run = l_run * alpha + lsum;
-            m_run = m_new;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-#pragma unroll
-                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-            // s outer, head-dim block inner: consecutive MFMAs are independent.
+            l_run += lsum;
+            // O^T += V^T . P^T; lane lq reads the NDB consecutive dims it feeds.
 #pragma unroll
             for (int s = 0; s < 16; ++s) {
                 const int key = 8 * (s >> 2) + 4 * lh + (s & 3);
-#pragma unroll
-                for (int db = 0; db < NDB; ++db) {
-                    const int dcol = db * 32 + lq;
-                    const float a = (HD >= 32 || dcol < HD) ? Vb[key * HD + (dcol < HD ? dcol : 0)] : 0.0f;
-                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, pv[s], o[db], 0, 0, 0);
+                const float *vrow = Vb + key * HD;
+                float a[NDB];
+                if (NDB == 4) {
+                    const float4 v4 = reinterpret_cast<const float4 *>(vrow)[lq];
+                    a[0] = v4.x;
+                    a[NDB > 1 ? 1 : 0] = v4.y;
+                    a[NDB > 2 ? 2 : 0] = v4.z;
+                    a[NDB > 3 ? 3 : 0] = v4.w;
+                } else if (NDB == 2) {
+                    const float2 v2 = reinterpret_cast<const float2 *>(vrow)[lq];
+                    a[0] = v2.x;
+                    a[NDB > 1 ? 1 : 0] = v2.y;
+                } else {
+                    a[0] = (HD >= 32 || lq < HD) ? vrow[HD >= 32 ? lq : (lq < HD ? lq : 0)] : 0.0f;
                 }
+#pragma unroll
+                for (int db = 0; db < NDB; ++db)
+                    o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[db], pv[s], o[db], 0, 0, 0);
             }
         }
         if (kt + 1 < ntiles) store_tile(cur ^ 1);
@@ -197,15 +236,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
     }
 
     // O^T -> LDS as [q][d], then coalesced row stores.
-    float *Os = smem + wave * 32 * KS;
+    float *Os = smem + wave * 32 * OS;
     if (my_tiles > 0) {
         const float inv = 1.0f / l_run;
 #pragma unroll
         for (int db = 0; db < NDB; ++db)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int d = db * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                if (d < HD) Os[lq * KS + d] = o[db][r] * inv;
+                const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int d = NDB * i + db;
+                if (d < HD) Os[lq * OS + d] = o[db][r] * inv;
             }
     }
     __syncthreads();
@@ -213,33 +253,32 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(AttnP p) {
         for (int idx = lane; idx < 32 * HD; idx += 64) {
             const int j = idx / HD, c = idx - j * HD;
             const int q = q0 + j;
-            if (q < T) p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = Os[j * KS + c];
+            if (q < T) p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = Os[j * OS + c];
         }
     }
 }
 
 // In-place RoPE (rope.rs:28-32) on heads of a strided layout: element
-// (b, h, t, p) at x[b*sb + h*sh + t*st + p], positions t = 0..T-1.
-__global__ __launch_bounds__(256) void rope_strided_kernel(float *__restrict__ x, int64_t sb,
-                                                           int64_t sh, int64_t st, int64_t nb,
-                                                           int64_t nh, int64_t t, int64_t hd,
-                                                           const float *__restrict__ cos_t,
-                                                           const float *__restrict__ sin_t) {
-    const int64_t half = hd / 2, total = nb * nh * t * half;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        int64_t r = i;
-        const int64_t c = r % half;
-        r /= half;
-        const int64_t pos = r % t;
-        r /= t;
-        const int64_t hh = r % nh;
-        const int64_t bb = r / nh;
-        float *row = x + bb * sb + hh * sh + pos * st;
-        const float x1 = row[c], x2 = row[c + half];
-        const float cs = cos_t[pos * half + c], sn = sin_t[pos * half + c];
-        row[c] = x1 * cs - x2 * sn;
-        row[c + half] = x2 * cs + x1 * sn;
+// (b, h, t, p) at x[b*sb + h*sh + t*st + p], positions t = 0..T-1. One
+// workgroup per (b, t) row; its threads walk the row's nh*HD/2 rotation pairs.
+template <int HD>
+__global__ __launch_bounds__(256) void rope_rows_kernel(float *__restrict__ x, int64_t sb,
+                                                        int64_t sh, int64_t st, int nh, int t,
+                                                        const float *__restrict__ cos_t,
+                                                        const float *__restrict__ sin_t) {
+    constexpr int HALF = HD / 2;
+    const int row = blockIdx.x;
+    const int bb = row / t, pos = row - bb * t;
+    float *base = x + bb * sb + pos * st;
+    const float *cr = cos_t + pos * HALF;
+    const float *sr = sin_t + pos * HALF;
+    for (int i = threadIdx.x; i < nh * HALF; i += 256) {
+        const int hh = i / HALF, c = i - hh * HALF;
+        float *r = base + hh * sh;
+        const float x1 = r[c], x2 = r[c + HALF];
+        const float cs = cr[c], sn = sr[c];
+        r[c] = x1 * cs - x2 * sn;
+        r[c + HALF] = x2 * cs + x1 * sn;
     }
 }
 
@@ -255,12 +294,17 @@ bool al16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0
 void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,
                          int64_t nh, int64_t t, int64_t hd, const float *cos_t,
                          const float *sin_t) {
-    const int64_t work = nb * nh * t * (hd / 2);
-    int64_t blocks = (work + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL(rope_strided_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx.stream, x,
-                       sb, sh, st, nb, nh, t, hd, cos_t, sin_t);
+    if (nb * t > 0x7fffffff) fail(MMH_ERR_SHAPE, "rope: too many rows");
+    const dim3 grid((unsigned)(nb * t)), block(256);
+    const int nhi = (int)nh, ti = (int)t;
+    switch (hd) {
+        case 4: hipLaunchKernelGGL(rope_rows_kernel<4>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 8: hipLaunchKernelGGL(rope_rows_kernel<8>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 16: hipLaunchKernelGGL(rope_rows_kernel<16>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 32: hipLaunchKernelGGL(rope_rows_kernel<32>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 64: hipLaunchKernelGGL(rope_rows_kernel<64>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        default: hipLaunchKernelGGL(rope_rows_kernel<128>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+    }
     check_hip(hipGetLastError(), "rope launch");
 }
 
@@ -278,11 +322,18 @@ void attention(Context &ctx, const AttnDesc &d) {
     if (!al16(d.q) || !al16(d.k) || !al16(d.v))
         fail(MMH_ERR_ARGUMENT, "attention: q, k and v must be 16-byte aligned");
     if (d.cos_t) {
-        // q and k rows are rotated in place before the kernel reads them.
-        launch_rope_strided(ctx, const_cast<float *>(d.q), d.sqb, d.sqh, d.sqt, d.b, d.h, d.t, d.hd,
-                            d.cos_t, d.sin_t);
-        launch_rope_strided(ctx, const_cast<float *>(d.k), d.skb, d.skh, d.skt, d.b, d.hkv, d.t,
-                            d.hd, d.cos_t, d.sin_t);
+        // q and k rows are rotated in place before the kernel reads them; when
+        // the k heads directly follow the q heads in each row (the fused QKV
+        // layout), one launch covers both.
+        if (d.k == d.q + d.h * d.sqh && d.skb == d.sqb && d.skh == d.sqh && d.skt == d.sqt) {
+            launch_rope_strided(ctx, const_cast<float *>(d.q), d.sqb, d.sqh, d.sqt, d.b,
+                                d.h + d.hkv, d.t, d.hd, d.cos_t, d.sin_t);
+        } else {
+            launch_rope_strided(ctx, const_cast<float *>(d.q), d.sqb, d.sqh, d.sqt, d.b, d.h, d.t,
+                                d.hd, d.cos_t, d.sin_t);
+            launch_rope_strided(ctx, const_cast<float *>(d.k), d.skb, d.skh, d.skt, d.b, d.hkv,
+                                d.t, d.hd, d.cos_t, d.sin_t);
+        }
     }
     AttnP p{};
     p.q = d.q;

@@ -39,7 +39,7 @@ namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 128, BN = 128, BK = 32;
+constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int GROUP_M = 8;
 
 struct KParams {
@@ -85,11 +85,12 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                                               floatx16 (&acc)[2][2]) {
     const int tid = threadIdx.x;
     const int64_t M = p.m, N = p.n;
-    // A K-tile of each operand is 128 x 32 floats = 1024 float4; thread tid
-    // moves float4 idx = tid + 256*i, i < 4.
-    // Row-major-in-k operands (A for nn/nt, B for nt): row idx/8, k (idx%8)*4.
+    // A K-tile of each operand is 128 x BK floats = 32*BK float4; thread tid
+    // moves float4 idx = tid + 256*i, i < BK/8.
+    // Row-major-in-k operands (A for nn/nt, B for nt): row idx/(BK/4), k (idx%(BK/4))*4.
     // k-major operands (A for tn, B for nn/tn): k idx/32, column (idx%32)*4.
-    constexpr int NL = 4;
+    constexpr int NL = BK / 8;
+    constexpr int RQ = BK / 4;  // float4 per row of a row-major-in-k tile
     // Uniform bases (moved by the tile's k) and 32-bit per-thread offsets.
     const float *a_base = TA ? A + m0 : A + m0 * p.lda;
     const float *b_base = TB ? B + n0 * p.ldb : B + n0;
@@ -98,8 +99,8 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
         const int idx = tid + 256 * i;
-        ao[i] = TA ? (uint32_t)(idx >> 5) * lda + (idx & 31) * 4 : (uint32_t)(idx >> 3) * lda + (idx & 7) * 4;
-        bo[i] = TB ? (uint32_t)(idx >> 3) * ldb + (idx & 7) * 4 : (uint32_t)(idx >> 5) * ldb + (idx & 31) * 4;
+        ao[i] = TA ? (uint32_t)(idx >> 5) * lda + (idx & 31) * 4 : (uint32_t)(idx / RQ) * lda + (idx % RQ) * 4;
+        bo[i] = TB ? (uint32_t)(idx / RQ) * ldb + (idx % RQ) * 4 : (uint32_t)(idx >> 5) * ldb + (idx & 31) * 4;
     }
 
     float4 ra[NL], rb[NL];
@@ -107,7 +108,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     auto load_a_edge = [&](int idx, int64_t k0) __attribute__((always_inline)) -> float4 {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (!TA) {
-            const int64_t gm = m0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
+            const int64_t gm = m0 + idx / RQ, gk = k0 + (idx % RQ) * 4;
             if (gm < M) {
                 const float *src = A + gm * p.lda + gk;
                 if (gk + 0 < kend) v.x = src[0];
@@ -139,7 +140,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                 if (gn + 3 < N) w.w = src[3];
             }
         } else {
-            const int64_t gn = n0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
+            const int64_t gn = n0 + idx / RQ, gk = k0 + (idx % RQ) * 4;
             if (gn < N) {
                 const float *src = B + gn * p.ldb + gk;
                 if (gk + 0 < kend) w.x = src[0];
@@ -170,7 +171,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
         for (int i = 0; i < NL; ++i) {
             const int idx = tid + 256 * i;
             if (!TA) {
-                const int row = idx >> 3, kq = (idx & 7) * 4;
+                const int row = idx / RQ, kq = (idx % RQ) * 4;
                 As[buf][kq + 0][row] = ra[i].x;
                 As[buf][kq + 1][row] = ra[i].y;
                 As[buf][kq + 2][row] = ra[i].z;
@@ -189,7 +190,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                 dst[2] = rb[i].z;
                 dst[3] = rb[i].w;
             } else {
-                const int col = idx >> 3, kq = (idx & 7) * 4;
+                const int col = idx / RQ, kq = (idx % RQ) * 4;
                 Bs[buf][kq + 0][col] = rb[i].x;
                 Bs[buf][kq + 1][col] = rb[i].y;
                 Bs[buf][kq + 2][col] = rb[i].z;

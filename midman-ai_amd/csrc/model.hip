@@ -100,6 +100,22 @@ struct Model {
     int32_t *ids = nullptr, *tgt = nullptr;
     int64_t staged_n = 0;
     bool staged_targets = false;
+    // The staged forward + loss of one (batch, seq) as a HIP graph: launch-bound
+    // small presets replay ~30 kernels with one call. Valid while the
+    // activation buffer it was captured on is the current one.
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    int64_t graph_b = 0, graph_t = 0, warm_b = 0, warm_t = 0;
+    const void *graph_act = nullptr, *warm_act = nullptr;
+
+    void drop_graph() {
+        if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
+        if (graph) (void)hipGraphDestroy(graph);
+        graph_exec = nullptr;
+        graph = nullptr;
+        graph_b = graph_t = 0;
+        graph_act = nullptr;
+    }
 
     int64_t qkv_cols() const { return cfg.d + 2 * cfg.kv(); }
     const float *embed() const { return w; }
@@ -120,6 +136,7 @@ struct Model {
     void release() {
         ctx->select();
         (void)hipStreamSynchronize(ctx->stream);
+        drop_graph();
         for (void *p : {(void *)w, (void *)packed, (void *)cos_t, (void *)sin_t, (void *)act})
             if (p) (void)hipFree(p);
         w = packed = cos_t = sin_t = act = nullptr;
@@ -331,6 +348,40 @@ struct Model {
                   [&] { launch_cross_entropy(c, logits, tgt, n, V, row_loss, loss); });
     }
 
+    // First call for a shape: eager (every workspace reaches its size). Second:
+    // capture the same launches into a graph. Later calls replay the graph.
+    // The graph holds no memset or allocation: only kernel launches.
+    void run_staged(int64_t batch, int64_t seq) {
+        if (graph_exec && graph_b == batch && graph_t == seq && graph_act == act &&
+            staged_n == batch * seq && staged_targets) {
+            check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
+            return;
+        }
+        if (!(warm_b == batch && warm_t == seq && warm_act == act)) {
+            enqueue(batch, seq, true);
+            warm_b = batch;
+            warm_t = seq;
+            warm_act = act;
+            return;
+        }
+        drop_graph();
+        check_hip(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "capture");
+        try {
+            enqueue(batch, seq, true);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(ctx->stream, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        check_hip(hipStreamEndCapture(ctx->stream, &graph), "end capture");
+        check_hip(hipGraphInstantiate(&graph_exec, graph, nullptr, nullptr, 0), "instantiate");
+        graph_b = batch;
+        graph_t = seq;
+        graph_act = act;
+        check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
+    }
+
     void run(const int32_t *inputs, const int32_t *targets, int64_t batch, int64_t seq,
              float *logits_out, float *loss_out) {
         stage(inputs, loss_out ? targets : nullptr, batch, seq);
@@ -385,6 +436,7 @@ void release_models_of(mmh_handle ctx) {
             if (m && m->ctx_handle == ctx) dead.push_back(std::move(m));
     }
     for (auto &m : dead) {
+        m->drop_graph();
         for (void *p : {(void *)m->w, (void *)m->packed, (void *)m->cos_t, (void *)m->sin_t,
                         (void *)m->act})
             if (p) (void)hipFree(p);
@@ -547,7 +599,7 @@ int32_t mmh_model_stage(mmh_handle model_h, const int32_t *inputs_host,
 int32_t mmh_model_run_staged(mmh_handle model_h, int64_t batch, int64_t seq) {
     return guard([&] {
         Model &m = model(model_h);
-        m.enqueue(batch, seq, true);
+        m.run_staged(batch, seq);
         return MMH_OK;
     });
 }

@@ -142,6 +142,28 @@ def test_large_preset_full_size_invariants(ctx):
     m.close()
 
 
+@pytest.mark.parametrize("preset,batch,seq", [("smoke", 2, 32), ("tiny", 8, 256)])
+def test_staged_graph_replays_match_eager(ctx, preset, batch, seq):
+    # run_staged: call 1 eager, call 2 captures a HIP graph, later calls replay
+    # it. Every replay must equal the eager loss bit for bit, with eager work
+    # and synchronisation between replays, and must read re-staged tokens.
+    print(f"\n[graph] {preset} B{batch} T{seq}", flush=True)
+    m = mh.Model.new(ctx, mh.PRESETS[preset], 3)
+    x, y = m.lab_tokens(batch, seq)
+    x2, y2 = m.lab_tokens(batch, seq)
+    eager = m.loss(x, y, batch, seq)
+    eager2 = m.loss(x2, y2, batch, seq)
+    assert eager != eager2
+    for i in range(6):
+        xs, ys, want = (x, y, eager) if i % 2 == 0 else (x2, y2, eager2)
+        m.stage(xs, ys, batch, seq)
+        m.run_staged(batch, seq)
+        got = m.read_loss()
+        assert got == want, (i, got, want)
+        assert m.loss(xs, ys, batch, seq) == want  # eager work between replays
+    m.close()
+
+
 def test_model_errors(ctx):
     cfg = mh.PRESETS["smoke"]
     m = mh.Model.new(ctx, cfg, 1)
