@@ -445,6 +445,7 @@ void mmo_apply_rope(const float *x, int64_t bh, int64_t t, int64_t hd, const flo
 typedef struct {
     const float *q, *k, *v;
     float *out;
+    float *probs; /* [B,H,T,T] or NULL: the probabilities, 0 above the diagonal */
     int64_t h, hkv, t, hd;
 } attn_args;
 
@@ -493,6 +494,10 @@ static void attn_heads(void *ctx, int64_t lo, int64_t hi) {
             }
             const float inv = 1.0f / sum;
             for (int64_t j = 0; j < len; j++) row[j] *= inv;
+            if (g->probs) {
+                float *pr = g->probs + (bh * t + i) * t;
+                for (int64_t j = 0; j < t; j++) pr[j] = j < len ? row[j] : 0.0f;
+            }
             float *orow = o + i * hd;
             for (int64_t d = 0; d < hd; d++) orow[d] = 0.0f;
             for (int64_t j = 0; j < len; j++) {
@@ -508,7 +513,7 @@ static void attn_heads(void *ctx, int64_t lo, int64_t hi) {
 
 void mmo_causal_attention(const float *q, const float *k, const float *v, int64_t b, int64_t h,
                           int64_t hkv, int64_t t, int64_t hd, float *out, int32_t nthreads) {
-    attn_args g = {q, k, v, out, h, hkv, t, hd};
+    attn_args g = {q, k, v, out, NULL, h, hkv, t, hd};
     parallel_for(b * h, nthreads, attn_heads, &g);
 }
 
@@ -688,5 +693,594 @@ int32_t mmo_forward_loss(const mmo_config *c, const float *w, const int32_t *ids
     int32_t st = mmo_forward(c, w, ids, b, t, lg, nthreads);
     if (st == MMO_OK) st = mmo_cross_entropy(lg, targets, n, v, loss);
     free(own);
+    return st;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Backward: the autograd closures of the ops above, and the training step   */
+/* ------------------------------------------------------------------------ */
+/*
+ * Each closure is restated with the reference's per-element arithmetic. Where
+ * one tensor receives gradients from several consumers (the residual stream,
+ * x in both x*x and x*inv of a norm, the input of the q/k/v projections), the
+ * reference adds them in its graph-traversal order (autograd.rs:69-125,
+ * accumulate :44-56); here they are added in the fixed order each function
+ * states. A sum of a few such terms may differ from the reference's in the
+ * last bit; the golden gradient norms (1e-4 relative) absorb that.
+ */
+
+/* ops_reduce.rs:261-275: d = exp(z-max)/sum*scale, then d[t] -= scale, with
+ * scale = g/N. */
+int32_t mmo_cross_entropy_backward(const float *logits, const int32_t *targets, int64_t n,
+                                   int64_t v, float g, float *dlogits) {
+    if (n <= 0 || v <= 0) return MMO_ERR_SHAPE;
+    for (int64_t i = 0; i < n; i++)
+        if (targets[i] < 0 || targets[i] >= v) return MMO_ERR_INDEX;
+    const float scale = g / (float)n;
+    for (int64_t i = 0; i < n; i++) {
+        const float *row = logits + i * v;
+        float *drow = dlogits + i * v;
+        float mx = -INFINITY;
+        for (int64_t j = 0; j < v; j++) mx = fmaxf(mx, row[j]);
+        float sum = 0.0f;
+        for (int64_t j = 0; j < v; j++) sum += expf(row[j] - mx);
+        for (int64_t j = 0; j < v; j++) drow[j] = expf(row[j] - mx) / sum * scale;
+        drow[targets[i]] -= scale;
+    }
+    return MMO_OK;
+}
+
+/* ops_shape.rs:261-269: dtable[id] += g row, ids in order. Accumulates. */
+void mmo_embedding_backward(const int32_t *ids, int64_t n, const float *g, int64_t d,
+                            float *dtable) {
+    for (int64_t i = 0; i < n; i++) {
+        float *t = dtable + (int64_t)ids[i] * d;
+        const float *gr = g + i * d;
+        for (int64_t j = 0; j < d; j++) t[j] += gr[j];
+    }
+}
+
+/* norm.rs:36-38 backward, through y = (x*inv)*w (mul, ops_elementwise.rs:
+ * 123-198), inv = (mean(x*x) + eps)^-0.5 (powf :335-337, add_scalar :309-312,
+ * mean_axis = sum_axis then scale, ops_reduce.rs:34-92):
+ *   dy0 = dy*w; dw = sum over rows of dy*y0; dinv = sum_j dy0*x;
+ *   ds = dinv*(-0.5*a^-1.5)*(1/d); dx = (dy0*inv + ds*x) + ds*x.
+ * dx receives only the norm's share (the caller adds the residual branch);
+ * dw is overwritten. */
+void mmo_rms_norm_backward(const float *x, const float *w, const float *dy, int64_t rows,
+                           int64_t d, float eps, float *dx, float *dw) {
+    const float inv_len = 1.0f / (float)d;
+    for (int64_t j = 0; j < d; j++) dw[j] = 0.0f;
+    for (int64_t r = 0; r < rows; r++) {
+        const float *xr = x + r * d, *gr = dy + r * d;
+        float *o = dx + r * d;
+        float total = 0.0f;
+        for (int64_t j = 0; j < d; j++) {
+            const float sq = xr[j] * xr[j];
+            total += sq;
+        }
+        const float a = total * inv_len + eps;
+        const float inv = powf(a, -0.5f);
+        float dinv = 0.0f;
+        for (int64_t j = 0; j < d; j++) {
+            const float g0 = gr[j] * w[j];
+            const float prod = g0 * xr[j];
+            dinv += prod;
+            const float y0 = xr[j] * inv;
+            const float gw = gr[j] * y0;
+            dw[j] += gw;
+        }
+        const float da = dinv * (-0.5f * powf(a, -1.5f));
+        const float ds = da * inv_len;
+        for (int64_t j = 0; j < d; j++) {
+            const float g0 = gr[j] * w[j];
+            const float direct = g0 * inv;
+            const float t = ds * xr[j];
+            const float partial = direct + t;
+            o[j] = partial + t;
+        }
+    }
+}
+
+/* rope.rs:28-32 backward: the halves route through narrow/concat and the
+ * products give dx1 = dfirst*cos + dsecond*sin, dx2 = dsecond*cos - dfirst*sin
+ * (the sub's right operand receives -dfirst). */
+void mmo_rope_backward(const float *dy, int64_t bh, int64_t t, int64_t hd, const float *cos_t,
+                       const float *sin_t, float *dx) {
+    const int64_t half = hd / 2;
+    for (int64_t m = 0; m < bh; m++) {
+        for (int64_t pos = 0; pos < t; pos++) {
+            const float *gr = dy + (m * t + pos) * hd;
+            float *o = dx + (m * t + pos) * hd;
+            const float *cr = cos_t + pos * half, *sr = sin_t + pos * half;
+            for (int64_t i = 0; i < half; i++) {
+                const float df = gr[i], dsec = gr[i + half];
+                const float a = df * cr[i], b = dsec * sr[i];
+                const float c = dsec * cr[i], e = df * sr[i];
+                o[i] = a + b;
+                o[i + half] = c - e;
+            }
+        }
+    }
+}
+
+typedef struct {
+    const float *q, *k, *v, *dout;
+    float *dq, *dk_h, *dv_h; /* dk_h/dv_h per query head, [B,H,T,hd] */
+    int64_t h, hkv, t, hd;
+} attn_bwd_args;
+
+/* One (batch, head) per index. The forward's probabilities are rebuilt with
+ * the forward's own operations, then the closures run in reverse:
+ *   context = probs.v       (batched matmul backward, ops_matmul.rs:100-125):
+ *       dprobs = dctx.v^T, dv = probs^T.dctx (query rows ascending)
+ *   probs = softmax(scores) (ops_reduce.rs:144-175): ds = p*(g - sum g*p)
+ *   scores = raw*scale + mask: draw = ds*scale
+ *   raw = q.k^T:            dq = draw.k, dk = draw^T.q (query rows ascending)
+ * Entries above the diagonal carry p = 0, so their terms are +-0 and are
+ * skipped without changing a bit. */
+static void attn_bwd_heads(void *ctx, int64_t lo, int64_t hi) {
+    const attn_bwd_args *g = (const attn_bwd_args *)ctx;
+    const int64_t t = g->t, hd = g->hd, groups = g->h / g->hkv;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float *kt = (float *)malloc(sizeof(float) * (size_t)(hd * t));
+    float *row = (float *)malloc(sizeof(float) * (size_t)t);
+    float *dp = (float *)malloc(sizeof(float) * (size_t)t);
+    for (int64_t bh = lo; bh < hi; bh++) {
+        const int64_t b = bh / g->h, h = bh % g->h;
+        const int64_t kvh = h / groups;
+        const float *q = g->q + bh * t * hd;
+        const float *k = g->k + (b * g->hkv + kvh) * t * hd;
+        const float *v = g->v + (b * g->hkv + kvh) * t * hd;
+        const float *dout = g->dout + bh * t * hd;
+        float *dq = g->dq + bh * t * hd;
+        float *dk = g->dk_h + bh * t * hd, *dv = g->dv_h + bh * t * hd;
+        memset(dq, 0, sizeof(float) * (size_t)(t * hd));
+        memset(dk, 0, sizeof(float) * (size_t)(t * hd));
+        memset(dv, 0, sizeof(float) * (size_t)(t * hd));
+        for (int64_t j = 0; j < t; j++)
+            for (int64_t p = 0; p < hd; p++) kt[p * t + j] = k[j * hd + p];
+        for (int64_t i = 0; i < t; i++) {
+            const int64_t len = i + 1;
+            /* probabilities, exactly as the forward (attn_heads) */
+            for (int64_t j = 0; j < len; j++) row[j] = 0.0f;
+            for (int64_t p = 0; p < hd; p++) {
+                const float qv = q[i * hd + p];
+                const float *kr = kt + p * t;
+                for (int64_t j = 0; j < len; j++) row[j] += qv * kr[j];
+            }
+            float mx = -INFINITY;
+            for (int64_t j = 0; j < len; j++) {
+                row[j] = row[j] * scale + 0.0f;
+                mx = fmaxf(mx, row[j]);
+            }
+            float sum = 0.0f;
+            for (int64_t j = 0; j < len; j++) {
+                const float e = expf(row[j] - mx);
+                row[j] = e;
+                sum += e;
+            }
+            const float inv = 1.0f / sum;
+            for (int64_t j = 0; j < len; j++) row[j] *= inv;
+            /* dprobs = dctx . v^T (gemm_nt: p ascending over hd) */
+            const float *go = dout + i * hd;
+            for (int64_t j = 0; j < len; j++) dp[j] = 0.0f;
+            for (int64_t p = 0; p < hd; p++) {
+                const float gv = go[p];
+                for (int64_t j = 0; j < len; j++) {
+                    const float prod = gv * v[j * hd + p];
+                    dp[j] += prod;
+                }
+            }
+            /* dv += probs^T . dctx, row i's turn */
+            for (int64_t j = 0; j < len; j++) {
+                const float pj = row[j];
+                float *dvr = dv + j * hd;
+                for (int64_t p = 0; p < hd; p++) {
+                    const float prod = pj * go[p];
+                    dvr[p] += prod;
+                }
+            }
+            /* softmax backward, then the scale */
+            float dot = 0.0f;
+            for (int64_t j = 0; j < len; j++) {
+                const float prod = dp[j] * row[j];
+                dot += prod;
+            }
+            for (int64_t j = 0; j < len; j++) {
+                const float diff = dp[j] - dot;
+                const float ds = row[j] * diff;
+                dp[j] = ds * scale;
+            }
+            /* dq[i] = draw . k (gemm_nt over j ascending); dk += draw^T . q */
+            float *dqr = dq + i * hd;
+            for (int64_t j = 0; j < len; j++) {
+                const float dj = dp[j];
+                const float *kr = k + j * hd;
+                float *dkr = dk + j * hd;
+                for (int64_t p = 0; p < hd; p++) {
+                    const float a = dj * kr[p];
+                    dqr[p] += a;
+                    const float bq = q[i * hd + p] * dj;
+                    dkr[p] += bq;
+                }
+            }
+        }
+    }
+    free(kt);
+    free(row);
+    free(dp);
+}
+
+/* attention.rs:79-101 backward. dout [B,H,T,hd] -> dq [B,H,T,hd],
+ * dk/dv [B,Hkv,T,hd]; the copies of a shared key/value head are summed in
+ * head order (repeat_interleave backward, ops_shape.rs:209-219). */
+void mmo_causal_attention_backward(const float *q, const float *k, const float *v,
+                                   const float *dout, int64_t b, int64_t h, int64_t hkv,
+                                   int64_t t, int64_t hd, float *dq, float *dk, float *dv,
+                                   int32_t nthreads) {
+    const int64_t per = t * hd, groups = h / hkv;
+    float *dk_h = zalloc(b * h * per), *dv_h = zalloc(b * h * per);
+    attn_bwd_args g = {q, k, v, dout, dq, dk_h, dv_h, h, hkv, t, hd};
+    parallel_for(b * h, nthreads, attn_bwd_heads, &g);
+    memset(dk, 0, sizeof(float) * (size_t)(b * hkv * per));
+    memset(dv, 0, sizeof(float) * (size_t)(b * hkv * per));
+    for (int64_t bb = 0; bb < b; bb++)
+        for (int64_t kvh = 0; kvh < hkv; kvh++) {
+            float *dko = dk + (bb * hkv + kvh) * per, *dvo = dv + (bb * hkv + kvh) * per;
+            for (int64_t r = 0; r < groups; r++) {
+                const float *dks = dk_h + (bb * h + kvh * groups + r) * per;
+                const float *dvs = dv_h + (bb * h + kvh * groups + r) * per;
+                for (int64_t e = 0; e < per; e++) {
+                    dko[e] += dks[e];
+                    dvo[e] += dvs[e];
+                }
+            }
+        }
+    free(dk_h);
+    free(dv_h);
+}
+
+/* ops_elementwise.rs:239-241 */
+static inline float sigmoid_value(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+/* The h = silu(g) * u step of mlp.rs:20-24 backward: dsilu = dh*u, du = dh*silu(g)
+ * (mul), dg = dsilu * s*(1 + g*(1 - s)) (silu, ops_elementwise.rs:355-364). */
+void mmo_silu_mul_backward(const float *gate, const float *up, const float *dh, int64_t n,
+                           float *dgate, float *dup) {
+    for (int64_t i = 0; i < n; i++) {
+        const float x = gate[i];
+        const float sv = silu(x);
+        const float dsilu = dh[i] * up[i];
+        dup[i] = dh[i] * sv;
+        const float s = sigmoid_value(x);
+        const float one_minus = 1.0f - s;
+        const float inner = x * one_minus;
+        const float deriv = s * (1.0f + inner);
+        dgate[i] = dsilu * deriv;
+    }
+}
+
+/* Saved forward values of one block. */
+typedef struct {
+    float *x, *xn1, *q, *k, *v, *ctx, *hres, *xn2, *g, *u, *a;
+} block_cache;
+
+/* Parameter segments in reference order: offsets, sizes and ranks. */
+static int64_t param_segments(const mmo_config *c, int64_t *off, int64_t *size, int32_t *rank) {
+    const int64_t d = c->d_model, ff = c->d_ff, v = c->vocab_size,
+                  kv = c->n_kv_heads * (d / c->n_heads);
+    int64_t count = 0, at = 0;
+#define SEG(sz, rk)                 \
+    do {                            \
+        off[count] = at;            \
+        size[count] = (sz);         \
+        rank[count] = (rk);         \
+        at += (sz);                 \
+        count++;                    \
+    } while (0)
+    SEG(v * d, 2);
+    for (int64_t l = 0; l < c->n_layers; l++) {
+        SEG(d, 1);
+        SEG(d * d, 2);
+        SEG(d * kv, 2);
+        SEG(d * kv, 2);
+        SEG(d * d, 2);
+        SEG(d, 1);
+        SEG(d * ff, 2);
+        SEG(d * ff, 2);
+        SEG(ff * d, 2);
+    }
+    SEG(d, 1);
+    if (!c->tie_embeddings) SEG(d * v, 2);
+#undef SEG
+    return count;
+}
+
+int64_t mmo_param_segments(const mmo_config *c, int64_t *offsets, int64_t *sizes,
+                           int32_t *ranks) {
+    if (mmo_config_validate(c) != MMO_OK) return MMO_ERR_CONFIG;
+    return param_segments(c, offsets, sizes, ranks);
+}
+
+/* model.rs:174-183 and every closure beneath it: the loss, and the gradient of
+ * every parameter in the flat layout of w (overwritten). The forward is the
+ * same sequence of operations as mmo_forward, keeping what the backward reads.
+ * Gradient sums across branches (fixed order here):
+ *   residual stream: dx = d(out) + d(norm branch);
+ *   q/k/v input: dxn = dq.Wq^T + dk.Wk^T + dv.Wv^T, gate/up: dg.Wg^T + du.Wu^T;
+ *   tied table: d(head) + d(embedding). */
+int32_t mmo_forward_backward(const mmo_config *c, const float *w, const int32_t *ids,
+                             const int32_t *targets, int64_t b, int64_t t, float *loss,
+                             float *grads, int32_t nthreads) {
+    if (mmo_config_validate(c) != MMO_OK) return MMO_ERR_CONFIG;
+    if (b <= 0 || t <= 0 || t > c->max_seq_len) return MMO_ERR_ARGUMENT;
+    const int64_t d = c->d_model, v = c->vocab_size, n = b * t, ff = c->d_ff,
+                  nh = c->n_heads, hkv = c->n_kv_heads, hd = d / nh, kv = hkv * hd,
+                  L = c->n_layers;
+    for (int64_t i = 0; i < n; i++) {
+        if (ids[i] < 0 || ids[i] >= v) return MMO_ERR_INDEX;
+        if (targets[i] < 0 || targets[i] >= v) return MMO_ERR_INDEX;
+    }
+    const int64_t np = mmo_param_count(c), bp = block_param_count(c);
+    memset(grads, 0, sizeof(float) * (size_t)np);
+    float *cos_t = zalloc(c->max_seq_len * hd / 2), *sin_t = zalloc(c->max_seq_len * hd / 2);
+    mmo_rope_tables(hd, c->max_seq_len, c->rope_theta, cos_t, sin_t);
+
+    /* ---- forward, keeping each block's values ---- */
+    block_cache *bc = (block_cache *)calloc((size_t)L, sizeof(block_cache));
+    float *x = zalloc(n * d);
+    mmo_embedding(w, v, d, ids, n, x);
+    float *tmp_a = zalloc(n * d), *tmp_b = zalloc(n * kv), *tmp_c = zalloc(n * kv);
+    for (int64_t l = 0; l < L; l++) {
+        const float *bw = w + v * d + l * bp;
+        const float *attn_norm = bw, *wq = attn_norm + d, *wk = wq + d * d, *wv = wk + d * kv,
+                    *wo = wv + d * kv, *mlp_norm = wo + d * d, *wg = mlp_norm + d,
+                    *wu = wg + d * ff, *wd = wu + d * ff;
+        block_cache *s = &bc[l];
+        s->x = x;
+        s->xn1 = zalloc(n * d);
+        mmo_rms_norm(x, attn_norm, n, d, c->norm_eps, s->xn1);
+        memset(tmp_a, 0, sizeof(float) * (size_t)(n * d));
+        memset(tmp_b, 0, sizeof(float) * (size_t)(n * kv));
+        memset(tmp_c, 0, sizeof(float) * (size_t)(n * kv));
+        mmo_gemm_nn(s->xn1, wq, tmp_a, n, d, d, nthreads);
+        mmo_gemm_nn(s->xn1, wk, tmp_b, n, d, kv, nthreads);
+        mmo_gemm_nn(s->xn1, wv, tmp_c, n, d, kv, nthreads);
+        float *qh = zalloc(n * d), *kh = zalloc(n * kv);
+        s->q = zalloc(n * d);
+        s->k = zalloc(n * kv);
+        s->v = zalloc(n * kv);
+        split_heads(tmp_a, d, 0, b, t, nh, hd, qh);
+        split_heads(tmp_b, kv, 0, b, t, hkv, hd, kh);
+        split_heads(tmp_c, kv, 0, b, t, hkv, hd, s->v);
+        mmo_apply_rope(qh, b * nh, t, hd, cos_t, sin_t, s->q);
+        mmo_apply_rope(kh, b * hkv, t, hd, cos_t, sin_t, s->k);
+        mmo_causal_attention(s->q, s->k, s->v, b, nh, hkv, t, hd, qh, nthreads);
+        s->ctx = zalloc(n * d);
+        merge_heads(qh, b, t, nh, hd, s->ctx);
+        free(qh);
+        free(kh);
+        memset(tmp_a, 0, sizeof(float) * (size_t)(n * d));
+        mmo_gemm_nn(s->ctx, wo, tmp_a, n, d, d, nthreads);
+        s->hres = zalloc(n * d);
+        memcpy(s->hres, x, sizeof(float) * (size_t)(n * d));
+        add_inplace(s->hres, tmp_a, n * d);
+        s->xn2 = zalloc(n * d);
+        mmo_rms_norm(s->hres, mlp_norm, n, d, c->norm_eps, s->xn2);
+        s->g = zalloc(n * ff);
+        s->u = zalloc(n * ff);
+        s->a = zalloc(n * ff);
+        mmo_gemm_nn(s->xn2, wg, s->g, n, d, ff, nthreads);
+        mmo_gemm_nn(s->xn2, wu, s->u, n, d, ff, nthreads);
+        for (int64_t i = 0; i < n * ff; i++) s->a[i] = silu(s->g[i]) * s->u[i];
+        memset(tmp_a, 0, sizeof(float) * (size_t)(n * d));
+        mmo_gemm_nn(s->a, wd, tmp_a, n, ff, d, nthreads);
+        x = zalloc(n * d);
+        memcpy(x, s->hres, sizeof(float) * (size_t)(n * d));
+        add_inplace(x, tmp_a, n * d);
+    }
+    const float *final_norm = w + v * d + L * bp;
+    float *xf = x, *yf = zalloc(n * d), *logits = zalloc(n * v);
+    mmo_rms_norm(xf, final_norm, n, d, c->norm_eps, yf);
+    if (c->tie_embeddings)
+        mmo_gemm_nt(yf, w, logits, n, d, v, nthreads);
+    else
+        mmo_gemm_nn(yf, final_norm + d, logits, n, d, v, nthreads);
+    mmo_cross_entropy(logits, targets, n, v, loss);
+
+    /* ---- backward ---- */
+    float *dlogits = zalloc(n * v);
+    mmo_cross_entropy_backward(logits, targets, n, v, 1.0f, dlogits);
+    float *dy = zalloc(n * d);
+    float *gfinal = grads + v * d + L * bp;
+    if (c->tie_embeddings) {
+        /* logits = y . E^T with E^T materialized (model.rs:163): d(E^T) =
+         * y^T . dlogits, transposed back into dE. */
+        /* dy = gemm_nt(dlogits, E^T): the copy of (E^T)^T is E itself */
+        mmo_gemm_nn(dlogits, w, dy, n, v, d, nthreads);
+        float *det = zalloc(d * v);
+        mmo_gemm_tn(yf, dlogits, det, d, n, v, nthreads);
+        for (int64_t j = 0; j < d; j++)
+            for (int64_t r = 0; r < v; r++) grads[r * d + j] = det[j * v + r];
+        free(det);
+    } else {
+        const float *head = final_norm + d;
+        mmo_gemm_nt(dlogits, head, dy, n, v, d, nthreads);
+        mmo_gemm_tn(yf, dlogits, gfinal + d, d, n, v, nthreads);
+    }
+    free(dlogits);
+    float *dx = zalloc(n * d);
+    mmo_rms_norm_backward(xf, final_norm, dy, n, d, c->norm_eps, dx, gfinal);
+
+    float *dxn = zalloc(n * d), *dctx = zalloc(n * d), *dh = zalloc(n * ff),
+          *dg = zalloc(n * ff), *du = zalloc(n * ff), *dnorm = zalloc(n * d);
+    float *doh = zalloc(n * d), *dqh = zalloc(n * d), *dkh = zalloc(n * kv),
+          *dvh = zalloc(n * kv), *dqr = zalloc(n * d), *dkr = zalloc(n * kv),
+          *dqf = zalloc(n * d), *dkf = zalloc(n * kv), *dvf = zalloc(n * kv);
+    for (int64_t l = L - 1; l >= 0; l--) {
+        const float *bw = w + v * d + l * bp;
+        float *gw = grads + v * d + l * bp;
+        const float *attn_norm = bw, *wq = attn_norm + d, *wk = wq + d * d, *wv = wk + d * kv,
+                    *wo = wv + d * kv, *mlp_norm = wo + d * d, *wg = mlp_norm + d,
+                    *wu = wg + d * ff, *wd = wu + d * ff;
+        float *g_attn_norm = gw, *g_wq = g_attn_norm + d, *g_wk = g_wq + d * d,
+              *g_wv = g_wk + d * kv, *g_wo = g_wv + d * kv, *g_mlp_norm = g_wo + d * d,
+              *g_wg = g_mlp_norm + d, *g_wu = g_wg + d * ff, *g_wd = g_wu + d * ff;
+        block_cache *s = &bc[l];
+        /* y = hres + a.Wd: dx is d(y) */
+        mmo_matmul_backward(s->a, wd, dx, dh, g_wd, n, ff, d, nthreads);
+        mmo_silu_mul_backward(s->g, s->u, dh, n * ff, dg, du);
+        mmo_matmul_backward(s->xn2, wg, dg, dxn, g_wg, n, d, ff, nthreads);
+        mmo_matmul_backward(s->xn2, wu, du, dnorm, g_wu, n, d, ff, nthreads);
+        add_inplace(dxn, dnorm, n * d);
+        mmo_rms_norm_backward(s->hres, mlp_norm, dxn, n, d, c->norm_eps, dnorm, g_mlp_norm);
+        add_inplace(dx, dnorm, n * d); /* dx is now d(hres) */
+        /* hres = x + ctx.Wo */
+        mmo_matmul_backward(s->ctx, wo, dx, dctx, g_wo, n, d, d, nthreads);
+        split_heads(dctx, d, 0, b, t, nh, hd, doh);
+        mmo_causal_attention_backward(s->q, s->k, s->v, doh, b, nh, hkv, t, hd, dqh, dkh, dvh,
+                                      nthreads);
+        mmo_rope_backward(dqh, b * nh, t, hd, cos_t, sin_t, dqr);
+        mmo_rope_backward(dkh, b * hkv, t, hd, cos_t, sin_t, dkr);
+        merge_heads(dqr, b, t, nh, hd, dqf);
+        merge_heads(dkr, b, t, hkv, hd, dkf);
+        merge_heads(dvh, b, t, hkv, hd, dvf);
+        mmo_matmul_backward(s->xn1, wq, dqf, dxn, g_wq, n, d, d, nthreads);
+        mmo_matmul_backward(s->xn1, wk, dkf, dnorm, g_wk, n, d, kv, nthreads);
+        add_inplace(dxn, dnorm, n * d);
+        mmo_matmul_backward(s->xn1, wv, dvf, dnorm, g_wv, n, d, kv, nthreads);
+        add_inplace(dxn, dnorm, n * d);
+        mmo_rms_norm_backward(s->x, attn_norm, dxn, n, d, c->norm_eps, dnorm, g_attn_norm);
+        add_inplace(dx, dnorm, n * d); /* dx is now d(x) of this block */
+    }
+    mmo_embedding_backward(ids, n, dx, d, grads);
+
+    for (int64_t l = 0; l < L; l++) {
+        block_cache *s = &bc[l];
+        free(s->x); free(s->xn1); free(s->q); free(s->k); free(s->v); free(s->ctx);
+        free(s->hres); free(s->xn2); free(s->g); free(s->u); free(s->a);
+    }
+    free(bc);
+    free(xf); free(yf); free(logits); free(dy); free(dx); free(dxn); free(dctx); free(dh);
+    free(dg); free(du); free(dnorm); free(doh); free(dqh); free(dkh); free(dvh); free(dqr);
+    free(dkr); free(dqf); free(dkf); free(dvf); free(tmp_a); free(tmp_b); free(tmp_c);
+    free(cos_t); free(sin_t);
+    return MMO_OK;
+}
+
+/* clip.rs:30-33: sqrt of the f64 sum of squares, in parameter order. */
+float mmo_global_norm(const float *g, int64_t n) {
+    double sum = 0.0;
+    for (int64_t i = 0; i < n; i++) sum += (double)g[i] * (double)g[i];
+    return (float)sqrt(sum);
+}
+
+/* clip.rs:42-60: returns the norm before clipping; scales by
+ * max/(norm + 1e-6) when norm > max. A non-finite norm is an error and
+ * nothing changes. */
+int32_t mmo_clip_global_norm(float *g, int64_t n, float max_norm, float *norm_out) {
+    if (!(isfinite(max_norm) && max_norm > 0.0f)) return MMO_ERR_ARGUMENT;
+    const float norm = mmo_global_norm(g, n);
+    *norm_out = norm;
+    if (!isfinite(norm)) return MMO_ERR_ARGUMENT;
+    if (norm > max_norm) {
+        const float factor = max_norm / (norm + 1e-6f);
+        for (int64_t i = 0; i < n; i++) g[i] *= factor;
+    }
+    return MMO_OK;
+}
+
+/* schedule.rs:54-66 */
+float mmo_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup, uint64_t total,
+                           uint64_t step) {
+    const double mx = (double)max_lr, mn = (double)min_lr;
+    if (step < warmup) return (float)(mx * (double)(step + 1) / (double)warmup);
+    if (step >= total) return min_lr;
+    const double progress = (double)(step - warmup) / (double)(total - warmup);
+    return (float)(mn + 0.5 * (mx - mn) * (1.0 + cos(3.14159265358979323846 * progress)));
+}
+
+/* adamw.rs:180-214 for one parameter at optimizer step t (counting from 1):
+ * bias terms in f64 (:185-187), then per element in f32, left to right. */
+void mmo_adamw_update(float *w, const float *g, float *m, float *v, int64_t n, int32_t decays,
+                      uint64_t t, float lr, float beta1, float beta2, float eps,
+                      float weight_decay) {
+    const double tt = (double)t;
+    const float bias1 = (float)(1.0 - pow((double)beta1, tt));
+    const float bias2_sqrt = (float)sqrt(1.0 - pow((double)beta2, tt));
+    const float step_size = lr / bias1;
+    const float decay = decays ? 1.0f - lr * weight_decay : 1.0f;
+    for (int64_t i = 0; i < n; i++) {
+        const float grad = g[i];
+        w[i] *= decay;
+        m[i] = beta1 * m[i] + (1.0f - beta1) * grad;
+        v[i] = beta2 * v[i] + (1.0f - beta2) * grad * grad;
+        w[i] -= step_size * m[i] / (sqrtf(v[i]) / bias2_sqrt + eps);
+    }
+}
+
+/* AdamW::step over the flat parameter list (rank >= 2 parameters decay).
+ * *steps is the optimizer's step count (incremented). */
+int32_t mmo_adamw_step(const mmo_config *c, float *w, const float *g, float *m, float *v,
+                       float lr, float beta1, float beta2, float eps, float weight_decay,
+                       uint64_t *steps) {
+    if (!(isfinite(lr) && lr >= 0.0f)) return MMO_ERR_ARGUMENT;
+    const int64_t np = mmo_param_count(c);
+    for (int64_t i = 0; i < np; i++)
+        if (!isfinite(g[i])) return MMO_ERR_ARGUMENT;
+    if (9 * c->n_layers + 3 > 4096) return MMO_ERR_CONFIG;
+    int64_t off[4096], size[4096];
+    int32_t rank[4096];
+    const int64_t segs = param_segments(c, off, size, rank);
+    *steps += 1;
+    for (int64_t s = 0; s < segs; s++)
+        mmo_adamw_update(w + off[s], g + off[s], m + off[s], v + off[s], size[s], rank[s] >= 2,
+                         *steps, lr, beta1, beta2, eps, weight_decay);
+    return MMO_OK;
+}
+
+/* Lab::new (lab.rs:159-214) and Lab::step_once (lab.rs:263-283): weights and
+ * tokens from one Rng(seed), then `steps` training steps, each
+ * lr = schedule(step), loss + gradients, norm = clip(grads), AdamW(lr).
+ * hyper = {max_lr, min_lr, warmup_steps, total_steps, weight_decay,
+ * clip_norm, beta1, beta2} (lab.rs:29-46), eps 1e-8 (lab.rs:192).
+ * weights may be NULL; otherwise it receives the final weights. */
+int32_t mmo_lab_train(const mmo_config *c, const double *hyper, uint64_t seed, int64_t batch,
+                      int64_t seq, int64_t steps, float *losses, float *grad_norms, float *lrs,
+                      float *weights, int32_t nthreads) {
+    if (mmo_config_validate(c) != MMO_OK) return MMO_ERR_CONFIG;
+    const int64_t np = mmo_param_count(c), n = batch * seq;
+    float *w = zalloc(np), *g = zalloc(np), *m = zalloc(np), *vv = zalloc(np);
+    int32_t *inputs = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+    int32_t *targets = (int32_t *)malloc(sizeof(int32_t) * (size_t)n);
+    mmo_rng r;
+    mmo_rng_seed(&r, seed);
+    mmo_init_weights(c, 0.02f, &r, w, np);
+    mmo_lab_tokens(&r, c->vocab_size, batch, seq, inputs, targets);
+    const float max_lr = (float)hyper[0], min_lr = (float)hyper[1];
+    const uint64_t warmup = (uint64_t)hyper[2], total = (uint64_t)hyper[3];
+    const float wd = (float)hyper[4], clip = (float)hyper[5], b1 = (float)hyper[6],
+                b2 = (float)hyper[7];
+    uint64_t opt_steps = 0;
+    int32_t st = MMO_OK;
+    for (int64_t s = 0; s < steps && st == MMO_OK; s++) {
+        const float lr = mmo_warmup_cosine_lr(max_lr, min_lr, warmup, total, (uint64_t)s);
+        float loss = 0.0f, norm = 0.0f;
+        st = mmo_forward_backward(c, w, inputs, targets, batch, seq, &loss, g, nthreads);
+        if (st != MMO_OK) break;
+        if (!isfinite(loss)) {
+            st = MMO_ERR_ARGUMENT;
+            break;
+        }
+        st = mmo_clip_global_norm(g, np, clip, &norm);
+        if (st != MMO_OK) break;
+        st = mmo_adamw_step(c, w, g, m, vv, lr, b1, b2, 1e-8f, wd, &opt_steps);
+        if (losses) losses[s] = loss;
+        if (grad_norms) grad_norms[s] = norm;
+        if (lrs) lrs[s] = lr;
+    }
+    if (weights) memcpy(weights, w, sizeof(float) * (size_t)np);
+    free(w); free(g); free(m); free(vv); free(inputs); free(targets);
     return st;
 }

@@ -34,6 +34,15 @@
  *                     attends to itself (:296-303), GQA = copied heads
  *   swiglu         -> known value mlp.rs:90-98
  *   cross_entropy  -> ln 2 and ln 2 / 2 KATs ops_reduce.rs:363-377
+ *   forward_backward (every backward closure together) -> golden gradient
+ *                     norm 1.0999628 of the Lab config at seed 2024
+ *                     (engine.test.mjs:26); per-op backward -> central
+ *                     finite differences in float64 of the forward op
+ *   clip + AdamW + schedule + backward over five steps -> golden losses
+ *                     and gradient norms of steps 1..4 (engine.test.mjs:25-26);
+ *                     AdamW alone -> its three-step table (adamw.rs:234-259);
+ *                     schedule -> lr[0] = max/15, lr[14] = max
+ *                     (engine.test.mjs:123-131) and schedule.rs tests
  */
 #ifndef MM_ORACLE_H
 #define MM_ORACLE_H
@@ -145,6 +154,56 @@ int32_t mmo_forward(const mmo_config *c, const float *w, const int32_t *ids, int
 int32_t mmo_forward_loss(const mmo_config *c, const float *w, const int32_t *ids,
                          const int32_t *targets, int64_t b, int64_t t, float *logits,
                          float *loss, int32_t nthreads);
+
+/* ---- Backward (autograd closures) and the training step ---- */
+/* ops_reduce.rs:261-275; g is the loss gradient (1 for loss.backward()). */
+int32_t mmo_cross_entropy_backward(const float *logits, const int32_t *targets, int64_t n,
+                                   int64_t v, float g, float *dlogits);
+/* ops_shape.rs:261-269: dtable[id] += g row, in id order (accumulates). */
+void mmo_embedding_backward(const int32_t *ids, int64_t n, const float *g, int64_t d,
+                            float *dtable);
+/* norm.rs:36-38 backward: dx = the norm's share of d(x) (overwritten),
+ * dw = sum over rows (overwritten). */
+void mmo_rms_norm_backward(const float *x, const float *w, const float *dy, int64_t rows,
+                           int64_t d, float eps, float *dx, float *dw);
+/* rope.rs:28-32 backward (rotation by -angle). */
+void mmo_rope_backward(const float *dy, int64_t bh, int64_t t, int64_t hd, const float *cos_t,
+                       const float *sin_t, float *dx);
+/* attention.rs:79-101 backward: dout [B,H,T,hd] -> dq [B,H,T,hd],
+ * dk/dv [B,Hkv,T,hd] (overwritten). */
+void mmo_causal_attention_backward(const float *q, const float *k, const float *v,
+                                   const float *dout, int64_t b, int64_t h, int64_t hkv,
+                                   int64_t t, int64_t hd, float *dq, float *dk, float *dv,
+                                   int32_t nthreads);
+/* h = silu(g)*u backward (mlp.rs:20-24, ops_elementwise.rs:355-364). */
+void mmo_silu_mul_backward(const float *gate, const float *up, const float *dh, int64_t n,
+                           float *dgate, float *dup);
+/* Offsets, sizes and ranks of the parameters in the flat layout; returns the
+ * count (at most 9*L + 3). */
+int64_t mmo_param_segments(const mmo_config *c, int64_t *offsets, int64_t *sizes,
+                           int32_t *ranks);
+/* Loss and the gradient of every parameter, flat layout (model.rs:174-183 +
+ * loss.backward()). */
+int32_t mmo_forward_backward(const mmo_config *c, const float *w, const int32_t *ids,
+                             const int32_t *targets, int64_t b, int64_t t, float *loss,
+                             float *grads, int32_t nthreads);
+float mmo_global_norm(const float *g, int64_t n);                       /* clip.rs:30-33 */
+int32_t mmo_clip_global_norm(float *g, int64_t n, float max_norm, float *norm_out); /* :42-60 */
+float mmo_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup, uint64_t total,
+                           uint64_t step);                              /* schedule.rs:54-66 */
+/* adamw.rs:180-214 for one parameter at step t (from 1); decays = rank >= 2. */
+void mmo_adamw_update(float *w, const float *g, float *m, float *v, int64_t n, int32_t decays,
+                      uint64_t t, float lr, float beta1, float beta2, float eps,
+                      float weight_decay);
+/* AdamW::step over the flat list (rank >= 2 decays); *steps increments. */
+int32_t mmo_adamw_step(const mmo_config *c, float *w, const float *g, float *m, float *v,
+                       float lr, float beta1, float beta2, float eps, float weight_decay,
+                       uint64_t *steps);
+/* Lab::new + Lab::step (lab.rs:159-283). hyper = {max_lr, min_lr, warmup,
+ * total, weight_decay, clip_norm, beta1, beta2}. Outputs per step may be NULL. */
+int32_t mmo_lab_train(const mmo_config *c, const double *hyper, uint64_t seed, int64_t batch,
+                      int64_t seq, int64_t steps, float *losses, float *grad_norms, float *lrs,
+                      float *weights, int32_t nthreads);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,7 @@ _REF_PATH = os.path.join(_HERE, "_ref", "libmmb_ref.so")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
 _i64 = ctypes.c_int64
 _i32 = ctypes.c_int32
 
@@ -99,6 +100,29 @@ def lib():
             "mmo_forward": (_i32, [C, _f32p, _i32p, _i64, _i64, _f32p, _i32]),
             "mmo_forward_loss": (_i32, [C, _f32p, _i32p, _i32p, _i64, _i64, _f32p, _f32p,
                                         _i32]),
+            "mmo_cross_entropy_backward": (_i32, [_f32p, _i32p, _i64, _i64, ctypes.c_float,
+                                                  _f32p]),
+            "mmo_embedding_backward": (None, [_i32p, _i64, _f32p, _i64, _f32p]),
+            "mmo_rms_norm_backward": (None, [_f32p, _f32p, _f32p, _i64, _i64, ctypes.c_float,
+                                             _f32p, _f32p]),
+            "mmo_rope_backward": (None, [_f32p, _i64, _i64, _i64, _f32p, _f32p, _f32p]),
+            "mmo_causal_attention_backward": (None, [_f32p] * 4 + [_i64] * 5 + [_f32p] * 3
+                                              + [_i32]),
+            "mmo_silu_mul_backward": (None, [_f32p, _f32p, _f32p, _i64, _f32p, _f32p]),
+            "mmo_param_segments": (_i64, [C, _i64p, _i64p, _i32p]),
+            "mmo_forward_backward": (_i32, [C, _f32p, _i32p, _i32p, _i64, _i64, _f32p, _f32p,
+                                            _i32]),
+            "mmo_global_norm": (ctypes.c_float, [_f32p, _i64]),
+            "mmo_clip_global_norm": (_i32, [_f32p, _i64, ctypes.c_float, _f32p]),
+            "mmo_warmup_cosine_lr": (ctypes.c_float, [ctypes.c_float, ctypes.c_float,
+                                                      ctypes.c_uint64, ctypes.c_uint64,
+                                                      ctypes.c_uint64]),
+            "mmo_adamw_step": (_i32, [C, _f32p, _f32p, _f32p, _f32p] + [ctypes.c_float] * 5
+                               + [ctypes.POINTER(ctypes.c_uint64)]),
+            "mmo_adamw_update": (None, [_f32p] * 4 + [_i64, _i32, ctypes.c_uint64]
+                                 + [ctypes.c_float] * 5),
+            "mmo_lab_train": (_i32, [C, ctypes.POINTER(ctypes.c_double), ctypes.c_uint64,
+                                     _i64, _i64, _i64, _f32p, _f32p, _f32p, _f32p, _i32]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -359,6 +383,127 @@ def forward_loss(c, w, ids, targets, batch, seq, want_logits=True, threads=None)
     return loss.value, logits
 
 
+# ---- backward and training step ---------------------------------------------
+
+def cross_entropy_backward(logits, targets, g=1.0):
+    logits, targets = f32(logits), i32(targets)
+    n, v = logits.shape
+    out = np.empty_like(logits)
+    st = lib().mmo_cross_entropy_backward(fp(logits), ip(targets), n, v, g, fp(out))
+    if st != OK:
+        raise IndexError(f"cross_entropy_backward status {st}")
+    return out
+
+
+def embedding_backward(ids, g, vocab):
+    """dtable [V,d] from the gradient rows g [N,d] (rows added in id order)."""
+    ids, g = i32(ids), f32(g)
+    d = g.shape[-1]
+    out = np.zeros((vocab, d), np.float32)
+    lib().mmo_embedding_backward(ip(ids), ids.size, fp(g), d, fp(out))
+    return out
+
+
+def rms_norm_backward(x, w, dy, eps):
+    """(dx share of the norm, dw)."""
+    x, w, dy = f32(x), f32(w), f32(dy)
+    d = x.shape[-1]
+    dx = np.empty_like(x)
+    dw = np.empty(d, np.float32)
+    lib().mmo_rms_norm_backward(fp(x), fp(w), fp(dy), x.size // d, d, eps, fp(dx), fp(dw))
+    return dx, dw
+
+
+def rope_backward(dy, cos, sin):
+    dy = f32(dy)
+    hd = dy.shape[-1]
+    t = dy.shape[-2]
+    out = np.empty_like(dy)
+    lib().mmo_rope_backward(fp(dy), dy.size // (t * hd), t, hd, fp(f32(cos)), fp(f32(sin)),
+                            fp(out))
+    return out
+
+
+def causal_attention_backward(q, k, v, dout, threads=None):
+    q, k, v, dout = f32(q), f32(k), f32(v), f32(dout)
+    B, H, T, hd = q.shape
+    hkv = k.shape[1]
+    dq, dk, dv = np.empty_like(q), np.empty_like(k), np.empty_like(v)
+    lib().mmo_causal_attention_backward(fp(q), fp(k), fp(v), fp(dout), B, H, hkv, T, hd,
+                                        fp(dq), fp(dk), fp(dv), threads or default_threads())
+    return dq, dk, dv
+
+
+def silu_mul_backward(gate, up, dh):
+    gate, up, dh = f32(gate), f32(up), f32(dh)
+    dg, du = np.empty_like(gate), np.empty_like(up)
+    lib().mmo_silu_mul_backward(fp(gate), fp(up), fp(dh), gate.size, fp(dg), fp(du))
+    return dg, du
+
+
+def param_segments(c):
+    """[(offset, size, rank)] of the flat parameter layout."""
+    off = np.zeros(9 * c.n_layers + 3, np.int64)
+    size = np.zeros_like(off)
+    rank = np.zeros(off.size, np.int32)
+    n = lib().mmo_param_segments(ctypes.byref(c), off.ctypes.data_as(_i64p),
+                                 size.ctypes.data_as(_i64p), ip(rank))
+    assert n > 0, n
+    return [(int(off[i]), int(size[i]), int(rank[i])) for i in range(n)]
+
+
+def forward_backward(c, w, ids, targets, batch, seq, threads=None):
+    """(loss, grads) with grads in the flat layout of w."""
+    ids, targets = i32(ids), i32(targets)
+    grads = np.empty(param_count(c), np.float32)
+    loss = ctypes.c_float()
+    st = lib().mmo_forward_backward(ctypes.byref(c), fp(w), ip(ids), ip(targets), batch, seq,
+                                    ctypes.byref(loss), fp(grads),
+                                    threads or default_threads())
+    if st != OK:
+        raise ValueError(f"forward_backward status {st}")
+    return loss.value, grads
+
+
+def global_norm(g):
+    g = f32(g)
+    return lib().mmo_global_norm(fp(g), g.size)
+
+
+def warmup_cosine_lr(max_lr, min_lr, warmup, total, step):
+    return lib().mmo_warmup_cosine_lr(max_lr, min_lr, warmup, total, step)
+
+
+def adamw_step(c, w, g, m, v, lr, beta1, beta2, eps, weight_decay, steps):
+    """Updates w, m, v in place; returns the new step count."""
+    cnt = ctypes.c_uint64(steps)
+    st = lib().mmo_adamw_step(ctypes.byref(c), fp(w), fp(f32(g)), fp(m), fp(v), lr, beta1,
+                              beta2, eps, weight_decay, ctypes.byref(cnt))
+    if st != OK:
+        raise ValueError(f"adamw status {st}")
+    return cnt.value
+
+
+def adamw_update(w, g, m, v, decays, t, lr, beta1, beta2, eps, weight_decay):
+    """One parameter's AdamW update at step t (from 1), in place."""
+    lib().mmo_adamw_update(fp(w), fp(f32(g)), fp(m), fp(v), w.size, int(decays), t, lr, beta1,
+                           beta2, eps, weight_decay)
+
+
+def lab_train(c, hyper, seed, batch, seq, steps, want_weights=False, threads=None):
+    """(losses, grad_norms, lrs, final weights or None) of Lab::step."""
+    h = (ctypes.c_double * 8)(*[float(x) for x in hyper])
+    losses = np.zeros(steps, np.float32)
+    norms = np.zeros(steps, np.float32)
+    lrs = np.zeros(steps, np.float32)
+    w = np.empty(param_count(c), np.float32) if want_weights else None
+    st = lib().mmo_lab_train(ctypes.byref(c), h, seed, batch, seq, steps, fp(losses),
+                             fp(norms), fp(lrs), fp(w), threads or default_threads())
+    if st != OK:
+        raise ValueError(f"lab_train status {st}")
+    return losses, norms, lrs, w
+
+
 # ---- the reference's own C twins (oracle/_ref) -----------------------------
 
 def ref_lib():
@@ -372,7 +517,9 @@ def ref_lib():
     L.mmb_softmax_rows.argtypes = [_f32p, _f32p, sz, sz]
     L.mmb_silu.argtypes = [_f32p, _f32p, sz]
     L.mmb_rms_norm.argtypes = [_f32p, _f32p, _f32p, sz, sz, ctypes.c_float]
+    L.mmb_adamw_update.argtypes = [_f32p, _f32p, _f32p, _f32p, sz, ctypes.c_int] + \
+        [ctypes.c_float] * 5
     for n in ("mmb_matmul_ikj", "mmb_matmul_ijk", "mmb_softmax_rows", "mmb_silu",
-              "mmb_rms_norm"):
+              "mmb_rms_norm", "mmb_adamw_update"):
         getattr(L, n).restype = None
     return L
