@@ -131,6 +131,29 @@ int32_t mmh_apply_rope(mmh_handle ctx, const float *x, int64_t bh, int64_t t, in
 int32_t mmh_causal_attention(mmh_handle ctx, const float *q, const float *k, const float *v,
                              int64_t b, int64_t h, int64_t hkv, int64_t t, int64_t hd,
                              float *out);
+/* Backward closures of the layer seam (autograd.rs:69-125 through the ops each
+ * layer is composed of). Outputs are overwritten.
+ * rms_norm (norm.rs:36-38 via ops_elementwise.rs:123-198,287,309,335 and
+ * ops_reduce.rs:34-92): dx = d(loss)/dx, dw summed over rows. */
+int32_t mmh_rms_norm_backward(mmh_handle ctx, const float *x, const float *w, const float *dy,
+                              int64_t rows, int64_t d, float eps, float *dx, float *dw);
+/* apply_rope (rope.rs:28-32): dx1 = dy1*cos + dy2*sin, dx2 = dy2*cos - dy1*sin.
+ * Bit-exact. dx may equal dy. */
+int32_t mmh_apply_rope_backward(mmh_handle ctx, const float *dy, int64_t bh, int64_t t,
+                                int64_t hd, const float *cos_dev, const float *sin_dev,
+                                float *dx);
+/* causal_attention (attention.rs:79-101 with ops_matmul.rs:100-125,
+ * ops_reduce.rs:144-175, ops_shape.rs:209-219): dq [B,H,T,hd], dk/dv
+ * [B,Hkv,T,hd] from dout [B,H,T,hd]; the copies of a kv head are summed. */
+int32_t mmh_causal_attention_backward(mmh_handle ctx, const float *q, const float *k,
+                                      const float *v, const float *dout, int64_t b, int64_t h,
+                                      int64_t hkv, int64_t t, int64_t hd, float *dq, float *dk,
+                                      float *dv);
+/* Tensor::cross_entropy backward (ops_reduce.rs:261-275) for loss gradient 1:
+ * dlogits = (softmax - onehot) / N (may equal logits); loss_host may be NULL. */
+int32_t mmh_cross_entropy_backward(mmh_handle ctx, const float *logits,
+                                   const int32_t *targets_host, int64_t n, int64_t vocab,
+                                   float *dlogits, float *loss_host);
 /* attention.rs:146-170: x [B,T,d] -> out [B,T,d]; weights [d,d],[d,kv],[d,kv],[d,d]. */
 int32_t mmh_attention_forward(mmh_handle ctx, const float *x, const float *wq, const float *wk,
                               const float *wv, const float *wo, const float *cos_dev,
@@ -212,6 +235,47 @@ int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
  * MMH_PROF_CLASSES entries. */
 int32_t mmh_model_profile(mmh_handle model, int64_t batch, int64_t seq, float *class_ms,
                           int32_t *class_launches);
+
+/* ---- Training: backward, global-norm clip, AdamW, schedule ----------------
+ * model.loss(..).backward() + gather_gradients (model.rs:174-183,
+ * autograd.rs:69-125, clip.rs:17-27): forward + loss + the gradient of every
+ * parameter, kept on the device in the reference parameter order. loss_host
+ * may be NULL. Tolerance against the reference: each parameter's gradient
+ * max|diff| <= 2e-3 * max|grad| of that parameter, the global norm <= 1e-4
+ * relative. */
+int32_t mmh_model_backward(mmh_handle model, const int32_t *inputs_host,
+                           const int32_t *targets_host, int64_t batch, int64_t seq,
+                           float *loss_host);
+/* The gradients of the last backward or training step, reference order. */
+int32_t mmh_model_download_grads(mmh_handle model, float *out_host, int64_t n);
+/* global_norm of those gradients (clip.rs:30-33): f64 sum of squares. */
+int32_t mmh_model_grad_norm(mmh_handle model, float *norm_host);
+/* AdamW::new(beta1, beta2, eps, weight_decay) (adamw.rs:48-66) together with
+ * the clip limit of Lab/Trainer (lab.rs:185-190, clip.rs:42-47). Replaces any
+ * earlier optimizer: moments and the step count start from zero. */
+int32_t mmh_model_set_optimizer(mmh_handle model, float beta1, float beta2, float eps,
+                                float weight_decay, float clip_norm);
+/* Lab::step_once (lab.rs:263-283) / Trainer::update (trainer.rs:185-205) at
+ * learning rate lr: loss, backward, clip_global_norm (clip.rs:42-60) and
+ * AdamW::step (adamw.rs:180-214), all on the device. loss_host and
+ * grad_norm_host (the norm before clipping) may be NULL. When the loss or the
+ * gradient norm is not finite, returns MMH_STOPPED with the reference's
+ * message and changes nothing (weights, moments, step count). */
+int32_t mmh_model_train_step(mmh_handle model, const int32_t *inputs_host,
+                             const int32_t *targets_host, int64_t batch, int64_t seq, float lr,
+                             float *loss_host, float *grad_norm_host);
+/* The same split for callers that keep one batch on the device (Lab trains
+ * on a fixed task): stage_train validates and uploads ids and targets and
+ * builds the embedding-backward index; train_staged runs one step on them. */
+int32_t mmh_model_stage_train(mmh_handle model, const int32_t *inputs_host,
+                              const int32_t *targets_host, int64_t batch, int64_t seq);
+int32_t mmh_model_train_staged(mmh_handle model, int64_t batch, int64_t seq, float lr,
+                               float *loss_host, float *grad_norm_host);
+/* AdamW::step_count (adamw.rs:69-71). */
+int32_t mmh_model_optimizer_steps(mmh_handle model, uint64_t *out);
+/* WarmupCosine::new + lr(step) (schedule.rs:25-66), f64 inside, f32 out. */
+int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
+                             uint64_t total_steps, uint64_t step, float *lr_out);
 
 #ifdef __cplusplus
 }

@@ -38,6 +38,7 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 struct AttnP {
     const float *q, *k, *v;
     float *out;
+    float *lse;
     int64_t sqb, sqh, sqt, skb, skh, skt, svb, svh, svt, sob, soh, sot;
     int h, hkv, t, nqb;
     float scale;
@@ -248,6 +249,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
                 if (d < HD) Os[lq * OS + d] = o[db][r] * inv;
             }
     }
+    if (p.lse && my_tiles > 0 && lh == 0 && qi < T)
+        p.lse[((int64_t)b * p.h + head) * T + qi] = m_run + log2f(l_run);
     __syncthreads();
     if (my_tiles > 0) {
         for (int idx = lane; idx < 32 * HD; idx += 64) {
@@ -261,7 +264,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
 // In-place RoPE (rope.rs:28-32) on heads of a strided layout: element
 // (b, h, t, p) at x[b*sb + h*sh + t*st + p], positions t = 0..T-1. One
 // workgroup per (b, t) row; its threads walk the row's nh*HD/2 rotation pairs.
-template <int HD>
+// INV rotates by -angle: (x1, x2) -> (x1*c + x2*s, x2*c - x1*s), which is the
+// RoPE backward dx1 = dfirst*cos + dsecond*sin, dx2 = dsecond*cos - dfirst*sin.
+template <int HD, bool INV>
 __global__ __launch_bounds__(256) void rope_rows_kernel(float *__restrict__ x, int64_t sb,
                                                         int64_t sh, int64_t st, int nh, int t,
                                                         const float *__restrict__ cos_t,
@@ -277,8 +282,13 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(float *__restrict__ x, i
         float *r = base + hh * sh;
         const float x1 = r[c], x2 = r[c + HALF];
         const float cs = cr[c], sn = sr[c];
-        r[c] = x1 * cs - x2 * sn;
-        r[c + HALF] = x2 * cs + x1 * sn;
+        if (INV) {
+            r[c] = x1 * cs + x2 * sn;
+            r[c + HALF] = x2 * cs - x1 * sn;
+        } else {
+            r[c] = x1 * cs - x2 * sn;
+            r[c + HALF] = x2 * cs + x1 * sn;
+        }
     }
 }
 
@@ -291,20 +301,31 @@ bool al16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0
 
 }  // namespace
 
+template <bool INV>
+void launch_rope_rows(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int nhi,
+                      int ti, int64_t hd, const float *cos_t, const float *sin_t, dim3 grid) {
+    const dim3 block(256);
+    switch (hd) {
+        case 4: hipLaunchKernelGGL((rope_rows_kernel<4, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 8: hipLaunchKernelGGL((rope_rows_kernel<8, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 16: hipLaunchKernelGGL((rope_rows_kernel<16, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 32: hipLaunchKernelGGL((rope_rows_kernel<32, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 64: hipLaunchKernelGGL((rope_rows_kernel<64, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        default: hipLaunchKernelGGL((rope_rows_kernel<128, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+    }
+}
+
 void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,
                          int64_t nh, int64_t t, int64_t hd, const float *cos_t,
-                         const float *sin_t) {
+                         const float *sin_t, bool inverse) {
     if (nb * t > 0x7fffffff) fail(MMH_ERR_SHAPE, "rope: too many rows");
-    const dim3 grid((unsigned)(nb * t)), block(256);
-    const int nhi = (int)nh, ti = (int)t;
-    switch (hd) {
-        case 4: hipLaunchKernelGGL(rope_rows_kernel<4>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 8: hipLaunchKernelGGL(rope_rows_kernel<8>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 16: hipLaunchKernelGGL(rope_rows_kernel<16>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 32: hipLaunchKernelGGL(rope_rows_kernel<32>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 64: hipLaunchKernelGGL(rope_rows_kernel<64>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        default: hipLaunchKernelGGL(rope_rows_kernel<128>, grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-    }
+    if (hd != 4 && hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
+        fail(MMH_ERR_SHAPE, "rope: head_dim must be 4, 8, 16, 32, 64 or 128");
+    const dim3 grid((unsigned)(nb * t));
+    if (inverse)
+        launch_rope_rows<true>(ctx, x, sb, sh, st, (int)nh, (int)t, hd, cos_t, sin_t, grid);
+    else
+        launch_rope_rows<false>(ctx, x, sb, sh, st, (int)nh, (int)t, hd, cos_t, sin_t, grid);
     check_hip(hipGetLastError(), "rope launch");
 }
 
@@ -340,6 +361,7 @@ void attention(Context &ctx, const AttnDesc &d) {
     p.k = d.k;
     p.v = d.v;
     p.out = d.out;
+    p.lse = d.lse;
     p.sqb = d.sqb; p.sqh = d.sqh; p.sqt = d.sqt;
     p.skb = d.skb; p.skh = d.skh; p.skt = d.skt;
     p.svb = d.svb; p.svh = d.svh; p.svt = d.svt;

@@ -1,0 +1,505 @@
+// Backward of the fused causal attention on CDNA4 matrix cores (fp32 MFMA
+// 32x32x2). It replaces the reference's chain of closures for
+// probs.v, softmax, scale + mask and q.k^T (ops_matmul.rs:100-125,
+// ops_reduce.rs:144-175, ops_elementwise.rs:301-306, repeat_interleave
+// backward ops_shape.rs:209-219) with two kernels that rebuild the
+// probabilities from the forward's saved log-sum-exp and never hold a [T,T]
+// tensor:
+//
+//   dq kernel  (one workgroup = 4 waves x 32 queries of one (batch, head)):
+//       D     = rowsum(dO * O)                         (also written for dkv)
+//       S^T   = K . Q^T,  P^T = exp2(S^T*scale*log2e - lse2)
+//       dP^T  = V . dO^T, dS^T = P^T * (dP^T - D)
+//       dQ^T += K^T . dS^T                             (dS^T straight from the
+//                                                      accumulators)
+//   dkv kernel (one workgroup = 4 waves x 32 keys of one (batch, kv head)):
+//       for every query head of the group and every query tile at or after
+//       the keys: S = Q . K^T, P, dP = dO . V^T, dS as above,
+//       dV^T += dO^T . P and dK^T += Q^T . dS
+//
+// Every per-row quantity lives in the lane that owns the row, as in the
+// forward kernel: with the MFMA layout (lane l: column l%32; register r: row
+// 8*(r/4) + 4*(l/32) + r%4), a product whose B operand is an accumulator
+// block is summed over the accumulator's rows in that permuted order, which
+// the A operand follows. Summing the group's heads inside one workgroup (in
+// head order) makes dK and dV deterministic without atomics. The gradient of
+// the scaled scores is dS*scale (attention.rs:83), applied to dQ and dK at
+// the end. Entries above the diagonal have P = 0 and contribute nothing.
+#include "mmh_internal.h"
+
+namespace mmh {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+struct BwdP {
+    const float *q, *k, *v, *o, *dout, *lse;
+    float *dq, *dk, *dv, *dvec;
+    int64_t sqb, sqh, sqt, skb, skh, skt, svb, svh, svt, sob, soh, sot;
+    int h, hkv, t, nqb, nkb;
+    float scale;
+};
+
+__device__ __forceinline__ floatx16 mfma(float a, float b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// A lane's operand run: NS consecutive floats from src (16-byte aligned when NS % 4 == 0).
+template <int NS>
+__device__ __forceinline__ void load_run(float (&r)[NS], const float *src) {
+    if constexpr (NS % 4 == 0) {
+#pragma unroll
+        for (int s = 0; s < NS / 4; ++s) {
+            const float4 v = reinterpret_cast<const float4 *>(src)[s];
+            r[4 * s + 0] = v.x;
+            r[4 * s + 1] = v.y;
+            r[4 * s + 2] = v.z;
+            r[4 * s + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) r[s] = src[s];
+    }
+}
+
+// Operands of the "row-shared" products (B from accumulators): lane lq takes
+// dims NDB*lq .. NDB*lq + NDB-1 of one LDS row; block db row i is dim NDB*i+db.
+template <int HD, int NDB>
+__device__ __forceinline__ void read_dims(float (&a)[NDB], const float *row, int lq) {
+    if constexpr (NDB == 4) {
+        const float4 v = reinterpret_cast<const float4 *>(row)[lq];
+        a[0] = v.x;
+        a[1] = v.y;
+        a[2] = v.z;
+        a[3] = v.w;
+    } else if constexpr (NDB == 2) {
+        const float2 v = reinterpret_cast<const float2 *>(row)[lq];
+        a[0] = v.x;
+        a[1] = v.y;
+    } else if constexpr (HD >= 32) {
+        a[0] = row[lq];
+    } else {
+        a[0] = lq < HD ? row[lq] : 0.0f;
+    }
+}
+
+// Two dot-product chains over a lane's run: acc0/acc1 += X[row lq] . Y^T where
+// the LDS row xrow holds the A operand and y (registers) the B operand.
+template <int NS>
+__device__ __forceinline__ void dot_chains(const float *xrow, const float (&y)[NS], floatx16 &acc0,
+                                           floatx16 &acc1) {
+    if constexpr (NS % 4 == 0) {
+#pragma unroll
+        for (int t = 0; t < NS / 4; ++t) {
+            const float4 xv = reinterpret_cast<const float4 *>(xrow)[t];
+            acc0 = mfma(xv.x, y[4 * t + 0], acc0);
+            acc1 = mfma(xv.y, y[4 * t + 1], acc1);
+            acc0 = mfma(xv.z, y[4 * t + 2], acc0);
+            acc1 = mfma(xv.w, y[4 * t + 3], acc1);
+        }
+    } else {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) acc0 = mfma(xrow[s], y[s], acc0);
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(BwdP p) {
+    constexpr int NS = HD / 2, NDB = (HD + 31) / 32, KS = HD + 4, OS = HD + 1;
+    constexpr int F4 = 32 * HD / 4, PER = (F4 + 255) / 256;
+    constexpr int STAGES = 4 * 32 * KS;  // K and V tiles, two stages each
+    constexpr int OUT = 128 * OS;
+    __shared__ __attribute__((aligned(16))) float smem[STAGES > OUT ? STAGES : OUT];
+    auto Ks = [&](int buf) { return smem + buf * 32 * KS; };
+    auto Vs = [&](int buf) { return smem + (2 + buf) * 32 * KS; };
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int head = blockIdx.x, b = blockIdx.y;
+    const int qblk = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
+    const int kvh = head / (p.h / p.hkv);
+    const int T = p.t;
+    const int q_first = qblk * 128;
+    const int q_last = min(q_first + 127, T - 1);
+    const int ntiles = q_last / 32 + 1;
+    const int q0 = q_first + wave * 32;
+    const int my_tiles = q0 < T ? q0 / 32 + 1 : 0;
+    const int qi = q0 + lq;
+    const int qc = min(qi, T - 1);
+
+    const float *Q = p.q + b * p.sqb + head * p.sqh;
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+    const float *O = p.o + b * p.sob + head * p.soh;
+    const float *dO = p.dout + b * p.sob + head * p.soh;
+    const int64_t rows = ((int64_t)b * p.h + head) * T;
+
+    float qr[NS], gr[NS];
+    load_run<NS>(qr, Q + (int64_t)qc * p.sqt + lh * NS);
+    load_run<NS>(gr, dO + (int64_t)qc * p.sot + lh * NS);
+    float dsum = 0.0f;
+    {
+        const float *orow = O + (int64_t)qc * p.sot + lh * NS;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dsum += gr[s] * orow[s];
+    }
+    dsum += __shfl_xor(dsum, 32, 64);
+    const float Dq = dsum;
+    const float L2 = p.lse[rows + qc];
+    if (lh == 0 && qi < T) p.dvec[rows + qi] = Dq;
+
+    float4 kreg[PER], vreg[PER];
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * 256;
+            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
+            if (f < F4) {
+                const int j = (4 * f) / HD, c = (4 * f) % HD;
+                const int key = kt * 32 + j;
+                if (key < T) {
+                    kv = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + c);
+                    vv = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + c);
+                }
+            }
+            kreg[i] = kv;
+            vreg[i] = vv;
+        }
+    };
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * 256;
+            if (f < F4) {
+                const int j = (4 * f) / HD, c = (4 * f) % HD;
+                float *kd = Ks(buf) + j * KS + c;
+                kd[0] = kreg[i].x;
+                kd[1] = kreg[i].y;
+                kd[2] = kreg[i].z;
+                kd[3] = kreg[i].w;
+                float *vd = Vs(buf) + j * KS + c;
+                vd[0] = vreg[i].x;
+                vd[1] = vreg[i].y;
+                vd[2] = vreg[i].z;
+                vd[3] = vreg[i].w;
+            }
+        }
+    };
+
+    floatx16 dq[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dq[db][r] = 0.0f;
+    const float sc = p.scale * 1.4426950408889634f;
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < ntiles) load_tile(kt + 1);
+        if (kt < my_tiles) {
+            const float *Kb = Ks(cur);
+            const float *Vb = Vs(cur);
+            floatx16 s0, s1, g0, g1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s0[r] = 0.0f;
+                s1[r] = 0.0f;
+                g0[r] = 0.0f;
+                g1[r] = 0.0f;
+            }
+            dot_chains<NS>(Kb + lq * KS + lh * NS, qr, s0, s1);
+            dot_chains<NS>(Vb + lq * KS + lh * NS, gr, g0, g1);
+            const int k0 = kt * 32;
+            float ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const float sv = (s0[r] + s1[r]) * sc;
+                const float pr = (key <= qi && key < T) ? exp2f(sv - L2) : 0.0f;
+                ds[r] = pr * ((g0[r] + g1[r]) - Dq);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int key = 8 * (s >> 2) + 4 * lh + (s & 3);
+                float a[NDB];
+                read_dims<HD, NDB>(a, Kb + key * KS, lq);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) dq[db] = mfma(a[db], ds[s], dq[db]);
+            }
+        }
+        if (kt + 1 < ntiles) store_tile(cur ^ 1);
+        __syncthreads();
+    }
+
+    float *Os = smem + wave * 32 * OS;
+    if (my_tiles > 0) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int d = NDB * i + db;
+                if (d < HD) Os[lq * OS + d] = dq[db][r] * p.scale;
+            }
+    }
+    __syncthreads();
+    if (my_tiles > 0) {
+        for (int idx = lane; idx < 32 * HD; idx += 64) {
+            const int j = idx / HD, c = idx - j * HD;
+            const int q = q0 + j;
+            if (q < T) p.dq[b * p.sqb + head * p.sqh + (int64_t)q * p.sqt + c] = Os[j * OS + c];
+        }
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
+    constexpr int NS = HD / 2, NDB = (HD + 31) / 32, KS = HD + 4, OS = HD + 1;
+    constexpr int F4 = 32 * HD / 4, PER = (F4 + 255) / 256;
+    constexpr int TILE = 2 * 32 * KS + 64;  // Q [32][KS], dO [32][KS], lse2[32], D[32]
+    constexpr int STAGES = 2 * TILE;
+    constexpr int OUT = 128 * OS;
+    __shared__ __attribute__((aligned(16))) float smem[STAGES > OUT ? STAGES : OUT];
+    auto Qs = [&](int buf) { return smem + buf * TILE; };
+    auto Gs = [&](int buf) { return smem + buf * TILE + 32 * KS; };
+    auto Ls = [&](int buf) { return smem + buf * TILE + 64 * KS; };
+    auto Ds = [&](int buf) { return smem + buf * TILE + 64 * KS + 32; };
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const int kblk = blockIdx.z;  // block 0 sees the most queries and starts first
+    const int T = p.t;
+    const int groups = p.h / p.hkv;
+    const int k_first = kblk * 128;
+    const int k0 = k_first + wave * 32;  // this wave's first key
+    const int kj = k0 + lq;
+    const int kc = min(kj, T - 1);
+    const int qt_first = k_first / 32;
+    const int nqt = (T + 31) / 32;
+    const int per_head = nqt - qt_first;
+    const int total = groups * per_head;
+    const int my_first = k0 / 32;  // query tiles before this one are all above the keys
+
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+    float kr[NS], vr[NS];
+    load_run<NS>(kr, K + (int64_t)kc * p.skt + lh * NS);
+    load_run<NS>(vr, V + (int64_t)kc * p.svt + lh * NS);
+
+    float4 qreg[PER], greg[PER];
+    float lreg = 0.0f;
+    auto load_tile = [&](int it) __attribute__((always_inline)) {
+        const int g = it / per_head;
+        const int qt = qt_first + (it - g * per_head);
+        const int head = kvh * groups + g;
+        const float *Qh = p.q + b * p.sqb + head * p.sqh;
+        const float *Gh = p.dout + b * p.sob + head * p.soh;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * 256;
+            float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), gv = qv;
+            if (f < F4) {
+                const int j = (4 * f) / HD, c = (4 * f) % HD;
+                const int q = qt * 32 + j;
+                if (q < T) {
+                    qv = *reinterpret_cast<const float4 *>(Qh + (int64_t)q * p.sqt + c);
+                    gv = *reinterpret_cast<const float4 *>(Gh + (int64_t)q * p.sot + c);
+                }
+            }
+            qreg[i] = qv;
+            greg[i] = gv;
+        }
+        if (tid < 64) {
+            const int q = qt * 32 + (tid & 31);
+            const int64_t at = ((int64_t)b * p.h + head) * T + q;
+            lreg = q < T ? (tid < 32 ? p.lse[at] : p.dvec[at]) : 0.0f;
+        }
+    };
+    auto store_tile = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int f = tid + i * 256;
+            if (f < F4) {
+                const int j = (4 * f) / HD, c = (4 * f) % HD;
+                float *qd = Qs(buf) + j * KS + c;
+                qd[0] = qreg[i].x;
+                qd[1] = qreg[i].y;
+                qd[2] = qreg[i].z;
+                qd[3] = qreg[i].w;
+                float *gd = Gs(buf) + j * KS + c;
+                gd[0] = greg[i].x;
+                gd[1] = greg[i].y;
+                gd[2] = greg[i].z;
+                gd[3] = greg[i].w;
+            }
+        }
+        if (tid < 32)
+            Ls(buf)[tid] = lreg;
+        else if (tid < 64)
+            Ds(buf)[tid - 32] = lreg;
+    };
+
+    floatx16 dk[NDB], dv[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            dk[db][r] = 0.0f;
+            dv[db][r] = 0.0f;
+        }
+    const float sc = p.scale * 1.4426950408889634f;
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int it = 0; it < total; ++it) {
+        const int cur = it & 1;
+        if (it + 1 < total) load_tile(it + 1);
+        const int g = it / per_head;
+        const int qt = qt_first + (it - g * per_head);
+        if (qt >= my_first && k0 < T) {
+            const float *Qb = Qs(cur);
+            const float *Gb = Gs(cur);
+            const float *Lb = Ls(cur);
+            const float *Db = Ds(cur);
+            floatx16 s0, s1, g0, g1;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                s0[r] = 0.0f;
+                s1[r] = 0.0f;
+                g0[r] = 0.0f;
+                g1[r] = 0.0f;
+            }
+            dot_chains<NS>(Qb + lq * KS + lh * NS, kr, s0, s1);
+            dot_chains<NS>(Gb + lq * KS + lh * NS, vr, g0, g1);
+            float pv[16], ds[16];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int q = qt * 32 + row;
+                const float sv = (s0[r] + s1[r]) * sc;
+                const float pr = (kj <= q && q < T && kj < T) ? exp2f(sv - Lb[row]) : 0.0f;
+                pv[r] = pr;
+                ds[r] = pr * ((g0[r] + g1[r]) - Db[row]);
+            }
+#pragma unroll
+            for (int s = 0; s < 16; ++s) {
+                const int row = 8 * (s >> 2) + 4 * lh + (s & 3);
+                float ag[NDB], aq[NDB];
+                read_dims<HD, NDB>(ag, Gb + row * KS, lq);
+                read_dims<HD, NDB>(aq, Qb + row * KS, lq);
+#pragma unroll
+                for (int db = 0; db < NDB; ++db) {
+                    dv[db] = mfma(ag[db], pv[s], dv[db]);
+                    dk[db] = mfma(aq[db], ds[s], dk[db]);
+                }
+            }
+        }
+        if (it + 1 < total) store_tile(cur ^ 1);
+        __syncthreads();
+    }
+
+    // dK = scale * dK^T and dV = dV^T, each through LDS as [key][d], then rows.
+    float *Os = smem + wave * 32 * OS;
+    for (int which = 0; which < 2; ++which) {
+        if (k0 < T) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const int d = NDB * i + db;
+                    if (d < HD) Os[lq * OS + d] = which == 0 ? dk[db][r] * p.scale : dv[db][r];
+                }
+        }
+        __syncthreads();
+        if (k0 < T) {
+            float *dst = which == 0 ? p.dk + b * p.skb + kvh * p.skh : p.dv + b * p.svb + kvh * p.svh;
+            const int64_t st = which == 0 ? p.skt : p.svt;
+            for (int idx = lane; idx < 32 * HD; idx += 64) {
+                const int j = idx / HD, c = idx - j * HD;
+                const int key = k0 + j;
+                if (key < T) dst[(int64_t)key * st + c] = Os[j * OS + c];
+            }
+        }
+        __syncthreads();
+    }
+}
+
+bool al16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
+
+}  // namespace
+
+void attention_backward(Context &ctx, const AttnBwdDesc &d) {
+    if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
+        fail(MMH_ERR_SHAPE, "attention backward: empty shape");
+    if (d.h % d.hkv != 0)
+        fail(MMH_ERR_SHAPE, "attention backward: n_heads is not a multiple of n_kv_heads");
+    if (d.b > 65535 || d.h > 65535 || d.t > 0x3fffffff)
+        fail(MMH_ERR_SHAPE, "attention backward: shape too large");
+    if (d.hd != 4 && d.hd != 8 && d.hd != 16 && d.hd != 32 && d.hd != 64 && d.hd != 128)
+        fail(MMH_ERR_SHAPE, "attention backward: head_dim must be 4, 8, 16, 32, 64 or 128");
+    const int64_t strides[] = {d.sqb, d.sqh, d.sqt, d.skb, d.skh, d.skt,
+                               d.svb, d.svh, d.svt, d.sob, d.soh, d.sot};
+    for (int64_t s : strides)
+        if (s % 4) fail(MMH_ERR_SHAPE, "attention backward: strides must be multiples of 4 floats");
+    const void *ptrs[] = {d.q, d.k, d.v, d.o, d.dout, d.dq, d.dk, d.dv};
+    for (const void *ptr : ptrs)
+        if (!al16(ptr)) fail(MMH_ERR_ARGUMENT, "attention backward: buffers must be 16-byte aligned");
+    BwdP p{};
+    p.q = d.q;
+    p.k = d.k;
+    p.v = d.v;
+    p.o = d.o;
+    p.dout = d.dout;
+    p.lse = d.lse;
+    p.dq = d.dq;
+    p.dk = d.dk;
+    p.dv = d.dv;
+    p.dvec = d.dvec;
+    p.sqb = d.sqb; p.sqh = d.sqh; p.sqt = d.sqt;
+    p.skb = d.skb; p.skh = d.skh; p.skt = d.skt;
+    p.svb = d.svb; p.svh = d.svh; p.svt = d.svt;
+    p.sob = d.sob; p.soh = d.soh; p.sot = d.sot;
+    p.h = (int)d.h;
+    p.hkv = (int)d.hkv;
+    p.t = (int)d.t;
+    p.nqb = (int)((d.t + 127) / 128);
+    p.nkb = p.nqb;
+    p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
+    const dim3 gq((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
+    const dim3 gk((unsigned)d.hkv, (unsigned)d.b, (unsigned)p.nkb);
+    const dim3 blk(256);
+#define MMH_BWD_CASE(HD)                                                                   \
+    case HD:                                                                               \
+        hipLaunchKernelGGL((attn_bwd_dq_kernel<HD>), gq, blk, 0, ctx.stream, p);           \
+        hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD>), gk, blk, 0, ctx.stream, p);          \
+        break;
+    switch (d.hd) {
+        MMH_BWD_CASE(4)
+        MMH_BWD_CASE(8)
+        MMH_BWD_CASE(16)
+        MMH_BWD_CASE(32)
+        MMH_BWD_CASE(64)
+        MMH_BWD_CASE(128)
+    }
+#undef MMH_BWD_CASE
+    check_hip(hipGetLastError(), "attention backward launch");
+    if (d.cos_t) {
+        if (d.dk == d.dq + d.h * d.sqh && d.skb == d.sqb && d.skh == d.sqh && d.skt == d.sqt) {
+            launch_rope_strided(ctx, d.dq, d.sqb, d.sqh, d.sqt, d.b, d.h + d.hkv, d.t, d.hd,
+                                d.cos_t, d.sin_t, true);
+        } else {
+            launch_rope_strided(ctx, d.dq, d.sqb, d.sqh, d.sqt, d.b, d.h, d.t, d.hd, d.cos_t,
+                                d.sin_t, true);
+            launch_rope_strided(ctx, d.dk, d.skb, d.skh, d.skt, d.b, d.hkv, d.t, d.hd, d.cos_t,
+                                d.sin_t, true);
+        }
+    }
+}
+
+}  // namespace mmh

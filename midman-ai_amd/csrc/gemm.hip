@@ -52,6 +52,9 @@ struct KParams {
     int64_t stride_a, stride_b, stride_c;
     int64_t k_per_split;
     int64_t swiglu_ff;
+    const float *resid;
+    float *aux;
+    int64_t ldaux;
     int tiles_m, tiles_n;
     int splits;
     int vec_a, vec_b, vec_c;
@@ -61,6 +64,17 @@ __device__ __forceinline__ float silu_f(float x) {
     // ops_elementwise.rs:239-241, :355-364: x * (1 / (1 + e^-x))
     const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
     return __fmul_rn(x, s);
+}
+
+// Backward of h = silu(g) * u (mul then silu, ops_elementwise.rs:287, :355-364):
+// dsilu = dh*u, du = dh*silu(g), dg = dsilu * s*(1 + g*(1 - s)).
+__device__ __forceinline__ float2 swiglu_bwd_f(float dh, float g, float u) {
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+    const float sv = __fmul_rn(g, s);
+    const float dsilu = __fmul_rn(dh, u);
+    const float du = __fmul_rn(dh, sv);
+    const float deriv = __fmul_rn(s, __fadd_rn(1.0f, __fmul_rn(g, __fsub_rn(1.0f, s))));
+    return make_float2(__fmul_rn(dsilu, deriv), du);
 }
 
 // Row strides (floats) of the k-major LDS stages: even, so the 8-byte operand
@@ -320,11 +334,40 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-                if (row < M && f < p.swiglu_ff)
+                if (row >= M) continue;
+                if (p.aux && col + 1 < N)
+                    *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) =
+                        make_float2(acc[i][0][r], acc[i][1][r]);
+                if (f < p.swiglu_ff)
                     C[row * p.ldc + f] = __fmul_rn(silu_f(acc[i][0][r]), acc[i][1][r]);
             }
         return;
     }
+    if (EPI == EPI_SWIGLU_BWD) {
+        // acc is dh[row][col, col+1]; their (g, u) pairs sit at aux columns
+        // 2*col .. 2*col+3 and the (dg, du) pairs go to the same columns of C.
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
+                if (row >= M) continue;
+                const float *gu = p.aux + row * p.ldaux + 2 * col;
+                float *dst = C + row * p.ldc + 2 * col;
+                if (col + 1 < N) {
+                    const float4 v = *reinterpret_cast<const float4 *>(gu);
+                    const float2 a = swiglu_bwd_f(acc[i][0][r], v.x, v.y);
+                    const float2 b2 = swiglu_bwd_f(acc[i][1][r], v.z, v.w);
+                    *reinterpret_cast<float4 *>(dst) = make_float4(a.x, a.y, b2.x, b2.y);
+                } else if (col < N) {
+                    const float2 a = swiglu_bwd_f(acc[i][0][r], gu[0], gu[1]);
+                    dst[0] = a.x;
+                    dst[1] = a.y;
+                }
+            }
+        return;
+    }
+    const float *R = p.resid ? p.resid + batch * p.stride_c : C;
     const bool pair = p.vec_c && col + 1 < N;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -333,17 +376,18 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
             const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
             if (row >= M) continue;
             float *dst = C + row * p.ldc + col;
+            const float *src = R + row * p.ldc + col;
             float v0 = acc[i][0][r], v1 = acc[i][1][r];
             if (pair) {
                 if (EPI == EPI_ACCUM) {
-                    const float2 o = *reinterpret_cast<const float2 *>(dst);
+                    const float2 o = *reinterpret_cast<const float2 *>(src);
                     v0 = __fadd_rn(o.x, v0);
                     v1 = __fadd_rn(o.y, v1);
                 }
                 *reinterpret_cast<float2 *>(dst) = make_float2(v0, v1);
             } else {
-                if (col < N) dst[0] = EPI == EPI_ACCUM ? __fadd_rn(dst[0], v0) : v0;
-                if (col + 1 < N) dst[1] = EPI == EPI_ACCUM ? __fadd_rn(dst[1], v1) : v1;
+                if (col < N) dst[0] = EPI == EPI_ACCUM ? __fadd_rn(src[0], v0) : v0;
+                if (col + 1 < N) dst[1] = EPI == EPI_ACCUM ? __fadd_rn(src[1], v1) : v1;
             }
         }
 }
@@ -351,7 +395,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
 // Sums split partials in split order, then applies the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial,
-                                                     float *__restrict__ c, int64_t m,
+                                                     float *c, const float *resid, int64_t m,
                                                      int64_t n, int64_t ldc, int splits) {
     const int64_t total = m * n;
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
@@ -361,7 +405,7 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ p
         const int64_t row = idx / n, col = idx - row * n;
         float *dst = c + row * ldc + col;
         if (EPI == EPI_ACCUM)
-            *dst = __fadd_rn(*dst, acc);
+            *dst = __fadd_rn((resid ? resid : c)[row * ldc + col], acc);
         else
             *dst = acc;
     }
@@ -400,6 +444,16 @@ void gemm(Context &ctx, const GemmDesc &d) {
     p.stride_b = d.stride_b;
     p.stride_c = d.stride_c;
     p.swiglu_ff = d.swiglu_ff;
+    p.resid = d.resid;
+    p.aux = d.aux;
+    p.ldaux = d.ldaux;
+    if (d.epi == EPI_SWIGLU_BWD || (d.epi == EPI_SWIGLU && d.aux)) {
+        if (!d.aux || d.ldaux < (d.epi == EPI_SWIGLU ? d.n : 2 * d.n) || d.ldaux % 4 ||
+            !aligned16(d.aux) ||
+            (d.epi == EPI_SWIGLU_BWD && (d.ldc % 4 || !aligned16(d.c))))
+            fail(MMH_ERR_ARGUMENT, "gemm: swiglu pairs need 16-byte aligned rows of >= 2n");
+        if (d.batch != 1) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogues take one matrix");
+    }
     p.tiles_m = (int)((d.m + BM - 1) / BM);
     p.tiles_n = (int)((d.n + BN - 1) / BN);
     // The interior path addresses a tile with 32-bit offsets (< 128 rows of ld).
@@ -416,12 +470,12 @@ void gemm(Context &ctx, const GemmDesc &d) {
     int splits = 1;
     if (d.force_splits > 0) {
         splits = d.force_splits;
-    } else if (d.batch == 1 && d.epi != EPI_SWIGLU) {
+    } else if (d.batch == 1 && d.epi != EPI_SWIGLU && d.epi != EPI_SWIGLU_BWD) {
         // Fill the chip: at least two tiles per CU, at least 8 K-steps per split.
         const int64_t target = 2 * (int64_t)(ctx.cu_count > 0 ? ctx.cu_count : 256);
         while (tiles * splits < target && splits < 16 && ktiles / (splits * 2) >= 8) splits *= 2;
     }
-    if (d.batch > 1 || d.epi == EPI_SWIGLU) splits = 1;
+    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD) splits = 1;
     const int64_t kt_per = (ktiles + splits - 1) / splits;
     p.k_per_split = kt_per * BK;
     splits = (int)((ktiles + kt_per - 1) / kt_per);
@@ -434,6 +488,9 @@ void gemm(Context &ctx, const GemmDesc &d) {
     if (epi == EPI_SWIGLU) {
         if (d.ta || d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogue needs the nn form");
         launch<false, false, EPI_SWIGLU>(ctx, p, grid);
+    } else if (epi == EPI_SWIGLU_BWD) {
+        if (d.ta || !d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu backward epilogue needs the nt form");
+        launch<false, true, EPI_SWIGLU_BWD>(ctx, p, grid);
     } else if (epi == EPI_ACCUM) {
         dispatch_t<EPI_ACCUM>(ctx, d.ta, d.tb, p, grid);
     } else {
@@ -445,10 +502,10 @@ void gemm(Context &ctx, const GemmDesc &d) {
         const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
         if (d.epi == EPI_ACCUM)
             hipLaunchKernelGGL(splitk_reduce<EPI_ACCUM>, dim3(blocks), dim3(256), 0, ctx.stream,
-                               p.partial, d.c, d.m, d.n, d.ldc, splits);
+                               p.partial, d.c, d.resid, d.m, d.n, d.ldc, splits);
         else
             hipLaunchKernelGGL(splitk_reduce<EPI_STORE>, dim3(blocks), dim3(256), 0, ctx.stream,
-                               p.partial, d.c, d.m, d.n, d.ldc, splits);
+                               p.partial, d.c, nullptr, d.m, d.n, d.ldc, splits);
         check_hip(hipGetLastError(), "split-k reduce launch");
     }
 }

@@ -62,7 +62,11 @@ void release_models_of(mmh_handle ctx);
 // ---- GEMM -----------------------------------------------------------------
 // C[m,n] = epi(op(A)[m,k] op(B)[k,n]). op(A)(i,p) = A[i*lda+p] (ta=false)
 // or A[p*lda+i] (ta=true); op(B)(p,j) = B[p*ldb+j] (tb=false) or B[j*ldb+p].
-enum Epilogue : int { EPI_STORE = 0, EPI_ACCUM = 1, EPI_SWIGLU = 2 };
+// EPI_STORE: C = acc. EPI_ACCUM: C = R + acc with R = resid, or C itself.
+// EPI_SWIGLU: columns (2f, 2f+1) are (gate f, up f); C[row][f] = silu(gate)*up,
+// and aux (when set) receives the raw pair. EPI_SWIGLU_BWD: acc is dh [M, ff];
+// with (g, u) = aux[row][2f, 2f+1], C[row][2f, 2f+1] = (dg, du) (C may be aux).
+enum Epilogue : int { EPI_STORE = 0, EPI_ACCUM = 1, EPI_SWIGLU = 2, EPI_SWIGLU_BWD = 3 };
 
 struct GemmDesc {
     const float *a = nullptr;
@@ -74,6 +78,9 @@ struct GemmDesc {
     bool ta = false, tb = false;
     int epi = EPI_STORE;
     int64_t swiglu_ff = 0;  // EPI_SWIGLU: output columns (<= n/2)
+    const float *resid = nullptr;  // EPI_ACCUM: residual source (ldc layout); null = C
+    float *aux = nullptr;          // EPI_SWIGLU(_BWD): interleaved gate/up pairs
+    int64_t ldaux = 0;
     int force_splits = 0;   // 0 = heuristic
 };
 
@@ -96,6 +103,38 @@ void launch_pack_cols(Context &ctx, const float *src, int64_t rows, int64_t cols
 void launch_pack_gate_up(Context &ctx, const float *wg, const float *wu, int64_t rows,
                          int64_t ff, int64_t ff_pad, float *dst);
 
+// ---- training step ----------------------------------------------------------
+// Loss (row terms + f64 mean) and, in place, dlogits = (softmax - onehot) * g/N.
+void launch_cross_entropy_fwd_bwd(Context &ctx, float *logits, const int32_t *targets_dev,
+                                  int64_t n, int64_t v, float g, float *row_loss,
+                                  float *loss_dev);
+// Floats of scratch launch_rms_norm_backward needs for (rows, d).
+int64_t rms_norm_backward_scratch(int64_t rows, int64_t d);
+// dx = [dx +] the norm's share of d(x); dw overwritten.
+void launch_rms_norm_backward(Context &ctx, const float *x, const float *w, const float *dy,
+                              int64_t rows, int64_t d, float eps, float *dx, bool accumulate,
+                              float *dw, float *scratch);
+// table[uniq[u]] = [table +] sum of g rows order[start[u] .. start[u+1]).
+void launch_embedding_backward(Context &ctx, const float *g, int64_t d, const int32_t *uniq,
+                               const int32_t *start, const int32_t *order, int64_t n_unique,
+                               float *table, bool accumulate);
+void launch_fill(Context &ctx, float *x, int64_t n, float v);
+void launch_unpack_cols(Context &ctx, const float *src, int64_t ld_src, int64_t col_off,
+                        int64_t rows, int64_t cols, float *dst);
+void launch_unpack_gate_up(Context &ctx, const float *src, int64_t rows, int64_t ff,
+                           int64_t ff_pad, float *wg, float *wu);
+int64_t global_norm_scratch_bytes();
+void launch_global_norm(Context &ctx, const float *g, int64_t n, double *scratch, float *norm);
+struct AdamArgs {
+    float lr, beta1, beta2, eps, weight_decay, clip_norm;
+    float step_size, bias2_sqrt;  // lr / (1 - beta1^t), sqrt(1 - beta2^t) (adamw.rs:185-188)
+};
+// ranges: [start, end) pairs of parameters that do not decay (rank 1).
+int64_t adamw_max_ranges_per_chunk(const int64_t *ranges_host, int nranges, int64_t n);
+void launch_adamw(Context &ctx, float *w, const float *g, float *m, float *v, int64_t n,
+                  const int64_t *ranges_dev, int nranges, int64_t max_per_chunk,
+                  const AdamArgs &a, const float *loss_dev, const float *norm_dev);
+
 // ---- attention --------------------------------------------------------------
 // Element (b,h,t,p) of q is q[b*sqb + h*sqh + t*sqt + p] (likewise k, v with
 // the kv head, and out with the query head).
@@ -108,7 +147,29 @@ struct AttnDesc {
     int64_t sob, soh, sot;
     int64_t b, h, hkv, t, hd;
     const float *cos_t = nullptr, *sin_t = nullptr;  // non-null: rotate q and k in-kernel
+    float *lse = nullptr;  // non-null: per-row log2-sum-exp2 of the scaled scores, [B,H,T]
 };
 void attention(Context &ctx, const AttnDesc &d);
+
+// Backward of attention() from its saved lse. q and k are the rows the
+// forward read (rotated in place when it had tables); o is its output and do
+// the output gradient, both with the out strides. dq/dk/dv take the q/k/v
+// strides and are overwritten; with tables set, dq and dk are rotated back
+// (RoPE backward) at the end. dvec is [B*H*T] scratch (rowsum(dO*O)).
+struct AttnBwdDesc {
+    const float *q, *k, *v, *o, *dout, *lse;
+    float *dq, *dk, *dv, *dvec;
+    int64_t sqb, sqh, sqt;
+    int64_t skb, skh, skt;
+    int64_t svb, svh, svt;
+    int64_t sob, soh, sot;
+    int64_t b, h, hkv, t, hd;
+    const float *cos_t = nullptr, *sin_t = nullptr;
+};
+void attention_backward(Context &ctx, const AttnBwdDesc &d);
+// In-place RoPE on strided heads; inverse rotates by -angle (the backward).
+void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,
+                         int64_t nh, int64_t t, int64_t hd, const float *cos_t,
+                         const float *sin_t, bool inverse = false);
 
 }  // namespace mmh

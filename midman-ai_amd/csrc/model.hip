@@ -14,7 +14,22 @@
 // exists) and the loss (row log-sum-exp + f64 mean).
 //
 // Weights keep the reference parameter order in one device buffer; the QKV
-// and gate/up matrices are additionally packed once at creation.
+// and gate/up matrices are additionally packed once at creation (and again
+// after every optimizer step).
+//
+// Training (Lab::step_once, lab.rs:263-283; Trainer::update, trainer.rs:185-205)
+// runs the same forward with every value the backward reads kept per layer
+// (block input, both norm outputs, rotated QKV, attention output and its
+// log-sum-exp, the post-attention residual, the gate/up pre-activations and
+// h), then per layer in reverse:
+//   GEMM dx . Wd^T with the SwiGLU-backward epilogue -> d(gate, up), in place
+//   GEMM h^T . dx -> dWd;  d(gate,up) . Wgu^T -> d(xn2);  xn2^T . d(gate,up) -> dWg, dWu
+//   RMSNorm backward (adds into dx, dw);  dx . Wo^T -> d(ctx);  ctx^T . dx -> dWo
+//   attention backward (dq, dk, dv, RoPE backward) -> d(qkv)
+//   d(qkv) . Wqkv^T -> d(xn1);  xn1^T . d(qkv) -> dWq, dWk, dWv;  RMSNorm backward
+// then the embedding scatter. The global norm (f64) and one clip + AdamW pass
+// over every parameter follow on the device; the host reads back only the
+// loss and the norm.
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -108,6 +123,28 @@ struct Model {
     int64_t graph_b = 0, graph_t = 0, warm_b = 0, warm_t = 0;
     const void *graph_act = nullptr, *warm_act = nullptr;
 
+    // ---- training state, allocated on the first training call ----
+    struct TrainBuf {
+        int64_t cap = 0;
+        float *mem = nullptr;
+        float *xs = nullptr, *xn1 = nullptr, *qkv = nullptr, *cb = nullptr, *lse = nullptr,
+              *hres = nullptr, *xn2 = nullptr, *gu = nullptr, *h = nullptr, *xnf = nullptr,
+              *dx = nullptr, *dy = nullptr, *dxn = nullptr, *dctx = nullptr, *dqkv = nullptr,
+              *dvec = nullptr, *wtmp = nullptr, *rms = nullptr, *norm = nullptr;
+        double *norm_scratch = nullptr;
+        int32_t *uniq = nullptr, *start = nullptr, *order = nullptr;
+        int64_t n_unique = 0;
+    } tr;
+    bool staged_index = false;  // the embedding-backward index matches the staged ids
+    float *grad = nullptr, *mom1 = nullptr, *mom2 = nullptr;
+    int64_t *ranges = nullptr;  // [start, end) of the parameters without weight decay
+    int nranges = 0;
+    int64_t ranges_worst = 0;
+    bool has_grad = false;
+    bool has_opt = false;
+    float beta1 = 0.9f, beta2 = 0.999f, adam_eps = 1e-8f, weight_decay = 0.0f, clip_norm = 1.0f;
+    uint64_t opt_steps = 0;
+
     void drop_graph() {
         if (graph_exec) (void)hipGraphExecDestroy(graph_exec);
         if (graph) (void)hipGraphDestroy(graph);
@@ -137,9 +174,13 @@ struct Model {
         ctx->select();
         (void)hipStreamSynchronize(ctx->stream);
         drop_graph();
-        for (void *p : {(void *)w, (void *)packed, (void *)cos_t, (void *)sin_t, (void *)act})
+        for (void *p : {(void *)w, (void *)packed, (void *)cos_t, (void *)sin_t, (void *)act,
+                        (void *)tr.mem, (void *)grad, (void *)mom1, (void *)mom2,
+                        (void *)ranges})
             if (p) (void)hipFree(p);
         w = packed = cos_t = sin_t = act = nullptr;
+        tr.mem = grad = mom1 = mom2 = nullptr;
+        ranges = nullptr;
     }
 
     void ensure(int64_t n) {
@@ -169,10 +210,9 @@ struct Model {
         staged_n = 0;
     }
 
-    void pack() {
+    // Copies Wq|Wk|Wv and the interleaved Wg/Wu from w into the packed buffer.
+    void repack() {
         const int64_t d = cfg.d, kv = cfg.kv(), ff = cfg.ff;
-        ff_pad = (ff + 31) / 32 * 32;
-        check_hip(hipMalloc(&packed, (size_t)(cfg.layers * packed_per_layer()) * 4), "packed alloc");
         for (int64_t l = 0; l < cfg.layers; ++l) {
             const float *wq = block(l) + d, *wk = wq + d * d, *wv = wk + d * kv;
             float *dst = const_cast<float *>(wqkv(l));
@@ -182,6 +222,12 @@ struct Model {
             const float *wg = mlp_norm(l) + d, *wu = wg + d * ff;
             launch_pack_gate_up(*ctx, wg, wu, d, ff, ff_pad, const_cast<float *>(wgu(l)));
         }
+    }
+
+    void pack() {
+        ff_pad = (cfg.ff + 31) / 32 * 32;
+        check_hip(hipMalloc(&packed, (size_t)(cfg.layers * packed_per_layer()) * 4), "packed alloc");
+        repack();
         const size_t tab = (size_t)(cfg.max_seq * (cfg.hd() / 2));
         std::vector<float> c(tab), s(tab);
         rope_tables_host(cfg.hd(), cfg.max_seq, cfg.theta, c.data(), s.data());
@@ -213,6 +259,7 @@ struct Model {
                       "targets upload");
         staged_n = n;
         staged_targets = targets != nullptr;
+        staged_index = false;
     }
 
     // Per-launch HIP events, summed per kernel class after the run.
@@ -396,6 +443,356 @@ struct Model {
                       "logits download");
         check_hip(hipStreamSynchronize(c.stream), "forward sync");
     }
+
+    // ---------------------------------------------------------------- training
+    int64_t lse_rows(int64_t n) const { return n * cfg.heads; }
+
+    // Saved activations and backward scratch for up to n rows. Per-layer
+    // slices are cap rows apart.
+    void ensure_train(int64_t n) {
+        if (n <= tr.cap) return;
+        if (tr.mem) {
+            check_hip(hipStreamSynchronize(ctx->stream), "sync");
+            check_hip(hipFree(tr.mem), "free training activations");
+            tr.mem = nullptr;
+            tr.cap = 0;
+        }
+        const int64_t d = cfg.d, L = cfg.layers, qc = qkv_cols(), ffp2 = 2 * ff_pad;
+        auto al = [](int64_t v) { return (v + 63) / 64 * 64; };
+        const int64_t wcols = std::max(qc, ffp2);
+        const int64_t sizes[] = {
+            al((L + 1) * n * d),            // xs
+            al(L * n * d),                  // xn1
+            al(L * n * qc),                 // qkv
+            al(L * n * d),                  // cb
+            al(L * lse_rows(n)),            // lse
+            al(L * n * d),                  // hres
+            al(L * n * d),                  // xn2
+            al(L * n * ffp2),               // gu
+            al(L * n * cfg.ff),             // h
+            al(n * d),                      // xnf
+            al(n * d),                      // dx
+            al(n * d),                      // dy
+            al(n * d),                      // dxn
+            al(n * d),                      // dctx
+            al(n * qc),                     // dqkv
+            al(lse_rows(n)),                // dvec
+            al(d * wcols),                  // wtmp
+            al(rms_norm_backward_scratch(n, d)),  // rms
+            64,                             // norm
+            al(global_norm_scratch_bytes() / 4),  // norm_scratch (doubles)
+            al(n), al(n + 1), al(n),        // uniq, start, order (int32)
+        };
+        int64_t total = 0;
+        for (int64_t s : sizes) total += s;
+        check_hip(hipMalloc(&tr.mem, (size_t)total * 4), "training activation alloc");
+        float *p = tr.mem;
+        float **slots[] = {&tr.xs,   &tr.xn1, &tr.qkv,  &tr.cb,   &tr.lse,  &tr.hres, &tr.xn2,
+                           &tr.gu,   &tr.h,   &tr.xnf,  &tr.dx,   &tr.dy,   &tr.dxn,  &tr.dctx,
+                           &tr.dqkv, &tr.dvec, &tr.wtmp, &tr.rms, &tr.norm};
+        int i = 0;
+        for (; i < 19; ++i) {
+            *slots[i] = p;
+            p += sizes[i];
+        }
+        tr.norm_scratch = reinterpret_cast<double *>(p);
+        p += sizes[i++];
+        tr.uniq = reinterpret_cast<int32_t *>(p);
+        p += sizes[i++];
+        tr.start = reinterpret_cast<int32_t *>(p);
+        p += sizes[i++];
+        tr.order = reinterpret_cast<int32_t *>(p);
+        tr.cap = n;
+        staged_index = false;
+    }
+
+    // Stages ids and targets (stage()) and the embedding-backward index: the
+    // distinct ids in ascending order, and for each the positions holding it
+    // in ascending order (a counting sort).
+    void stage_train(const int32_t *inputs, const int32_t *targets, int64_t batch, int64_t seq) {
+        if (!targets) fail(MMH_ERR_ARGUMENT, "training needs targets");
+        stage(inputs, targets, batch, seq);
+        const int64_t n = batch * seq;
+        ensure_train(n);
+        std::vector<int32_t> count((size_t)cfg.vocab + 1, 0);
+        for (int64_t i = 0; i < n; ++i) count[(size_t)inputs[i] + 1]++;
+        std::vector<int32_t> uniq, start, order((size_t)n);
+        uniq.reserve((size_t)n);
+        start.reserve((size_t)n + 1);
+        std::vector<int32_t> at((size_t)cfg.vocab, 0);
+        int32_t run = 0;
+        for (int64_t v = 0; v < cfg.vocab; ++v) {
+            const int32_t c = count[(size_t)v + 1];
+            if (c) {
+                uniq.push_back((int32_t)v);
+                start.push_back(run);
+            }
+            at[(size_t)v] = run;
+            run += c;
+        }
+        start.push_back(run);
+        for (int64_t i = 0; i < n; ++i) order[(size_t)at[(size_t)inputs[i]]++] = (int32_t)i;
+        tr.n_unique = (int64_t)uniq.size();
+        // The copies run on the stream before this function returns; the
+        // vectors are synchronised below so the host memory outlives them.
+        check_hip(hipMemcpyAsync(tr.uniq, uniq.data(), uniq.size() * 4, hipMemcpyHostToDevice,
+                                 ctx->stream), "index upload");
+        check_hip(hipMemcpyAsync(tr.start, start.data(), start.size() * 4, hipMemcpyHostToDevice,
+                                 ctx->stream), "index upload");
+        check_hip(hipMemcpyAsync(tr.order, order.data(), order.size() * 4, hipMemcpyHostToDevice,
+                                 ctx->stream), "index upload");
+        check_hip(hipStreamSynchronize(ctx->stream), "index upload sync");
+        staged_index = true;
+    }
+
+    float *grad_of(const float *param) { return grad + (param - w); }
+
+    GemmDesc desc(const float *a, bool ta, int64_t lda, const float *b, bool tb, int64_t ldb,
+                  float *c, int64_t ldc, int64_t m, int64_t k, int64_t n) const {
+        GemmDesc g;
+        g.a = a;
+        g.ta = ta;
+        g.lda = lda;
+        g.b = b;
+        g.tb = tb;
+        g.ldb = ldb;
+        g.c = c;
+        g.ldc = ldc;
+        g.m = m;
+        g.k = k;
+        g.n = n;
+        return g;
+    }
+
+    // Forward keeping what the backward reads, the loss, and dlogits in place.
+    void enqueue_train_forward(int64_t batch, int64_t seq) {
+        const int64_t n = batch * seq;
+        Context &c = *ctx;
+        const int64_t d = cfg.d, kv = cfg.kv(), hd = cfg.hd(), V = cfg.vocab, qc = qkv_cols();
+        const int64_t cap = tr.cap, ffp2 = 2 * ff_pad;
+        launch_embedding(c, embed(), d, ids, n, tr.xs);
+        for (int64_t l = 0; l < cfg.layers; ++l) {
+            float *x = tr.xs + l * cap * d, *xn1 = tr.xn1 + l * cap * d;
+            float *qkvl = tr.qkv + l * cap * qc, *cbl = tr.cb + l * cap * d;
+            float *hres = tr.hres + l * cap * d, *xn2 = tr.xn2 + l * cap * d;
+            float *gu = tr.gu + l * cap * ffp2, *hl = tr.h + l * cap * cfg.ff;
+            float *xnext = tr.xs + (l + 1) * cap * d;
+            launch_rms_norm(c, x, attn_norm(l), n, d, cfg.eps, xn1);
+            gemm(c, desc(xn1, false, d, wqkv(l), false, qc, qkvl, qc, n, d, qc));
+            AttnDesc a{};
+            a.q = qkvl;
+            a.k = qkvl + d;
+            a.v = qkvl + d + kv;
+            a.out = cbl;
+            a.sqb = a.skb = a.svb = seq * qc;
+            a.sqh = a.skh = a.svh = hd;
+            a.sqt = a.skt = a.svt = qc;
+            a.sob = seq * d;
+            a.soh = hd;
+            a.sot = d;
+            a.b = batch;
+            a.h = cfg.heads;
+            a.hkv = cfg.kv_heads;
+            a.t = seq;
+            a.hd = hd;
+            a.cos_t = cos_t;
+            a.sin_t = sin_t;
+            a.lse = tr.lse + l * lse_rows(cap);
+            attention(c, a);
+            GemmDesc o = desc(cbl, false, d, wo(l), false, d, hres, d, n, d, d);
+            o.epi = EPI_ACCUM;
+            o.resid = x;
+            gemm(c, o);
+            launch_rms_norm(c, hres, mlp_norm(l), n, d, cfg.eps, xn2);
+            GemmDesc gg = desc(xn2, false, d, wgu(l), false, ffp2, hl, cfg.ff, n, d, ffp2);
+            gg.epi = EPI_SWIGLU;
+            gg.swiglu_ff = cfg.ff;
+            gg.aux = gu;
+            gg.ldaux = ffp2;
+            gemm(c, gg);
+            GemmDesc dn = desc(hl, false, cfg.ff, wd(l), false, d, xnext, d, n, cfg.ff, d);
+            dn.epi = EPI_ACCUM;
+            dn.resid = hres;
+            gemm(c, dn);
+        }
+        launch_rms_norm(c, tr.xs + cfg.layers * cap * d, final_norm(), n, d, cfg.eps, tr.xnf);
+        if (cfg.tie)
+            gemm(c, desc(tr.xnf, false, d, embed(), true, d, logits, V, n, d, V));
+        else
+            gemm(c, desc(tr.xnf, false, d, lm_head(), false, V, logits, V, n, d, V));
+        launch_cross_entropy_fwd_bwd(c, logits, tgt, n, V, 1.0f, row_loss, loss);
+    }
+
+    // Every parameter gradient into grad (reference order), from dlogits.
+    void enqueue_backward(int64_t batch, int64_t seq) {
+        const int64_t n = batch * seq;
+        Context &c = *ctx;
+        const int64_t d = cfg.d, kv = cfg.kv(), hd = cfg.hd(), V = cfg.vocab, qc = qkv_cols();
+        const int64_t cap = tr.cap, ffp2 = 2 * ff_pad, ff = cfg.ff;
+        // head: logits = xnf . E^T (tied) or xnf . W_head
+        if (cfg.tie) {
+            gemm(c, desc(logits, false, V, embed(), false, d, tr.dy, d, n, V, d));
+            gemm(c, desc(logits, true, V, tr.xnf, false, d, grad, d, V, n, d));
+        } else {
+            gemm(c, desc(logits, false, V, lm_head(), true, V, tr.dy, d, n, V, d));
+            gemm(c, desc(tr.xnf, true, d, logits, false, V, grad_of(lm_head()), V, d, n, V));
+        }
+        launch_rms_norm_backward(c, tr.xs + cfg.layers * cap * d, final_norm(), tr.dy, n, d,
+                                 cfg.eps, tr.dx, false, grad_of(final_norm()), tr.rms);
+        for (int64_t l = cfg.layers - 1; l >= 0; --l) {
+            float *x = tr.xs + l * cap * d, *xn1 = tr.xn1 + l * cap * d;
+            float *qkvl = tr.qkv + l * cap * qc, *cbl = tr.cb + l * cap * d;
+            float *hres = tr.hres + l * cap * d, *xn2 = tr.xn2 + l * cap * d;
+            float *gu = tr.gu + l * cap * ffp2, *hl = tr.h + l * cap * ff;
+            const float *wq = block(l) + d, *wk = wq + d * d, *wv = wk + d * kv;
+            const float *wg = mlp_norm(l) + d, *wu = wg + d * ff;
+            // MLP: y = hres + h . Wd, h = silu(gate) * up
+            GemmDesc dh = desc(tr.dx, false, d, wd(l), true, d, gu, ffp2, n, d, ff);
+            dh.epi = EPI_SWIGLU_BWD;
+            dh.aux = gu;
+            dh.ldaux = ffp2;
+            gemm(c, dh);  // gu now holds (dgate, dup) pairs
+            gemm(c, desc(hl, true, ff, tr.dx, false, d, grad_of(wd(l)), d, ff, n, d));
+            gemm(c, desc(gu, false, ffp2, wgu(l), true, ffp2, tr.dxn, d, n, ffp2, d));
+            gemm(c, desc(xn2, true, d, gu, false, ffp2, tr.wtmp, ffp2, d, n, ffp2));
+            launch_unpack_gate_up(c, tr.wtmp, d, ff, ff_pad, grad_of(wg), grad_of(wu));
+            launch_rms_norm_backward(c, hres, mlp_norm(l), tr.dxn, n, d, cfg.eps, tr.dx, true,
+                                     grad_of(mlp_norm(l)), tr.rms);
+            // attention: hres = x + ctx . Wo
+            gemm(c, desc(tr.dx, false, d, wo(l), true, d, tr.dctx, d, n, d, d));
+            gemm(c, desc(cbl, true, d, tr.dx, false, d, grad_of(wo(l)), d, d, n, d));
+            AttnBwdDesc ab{};
+            ab.q = qkvl;
+            ab.k = qkvl + d;
+            ab.v = qkvl + d + kv;
+            ab.o = cbl;
+            ab.dout = tr.dctx;
+            ab.lse = tr.lse + l * lse_rows(cap);
+            ab.dq = tr.dqkv;
+            ab.dk = tr.dqkv + d;
+            ab.dv = tr.dqkv + d + kv;
+            ab.dvec = tr.dvec;
+            ab.sqb = ab.skb = ab.svb = seq * qc;
+            ab.sqh = ab.skh = ab.svh = hd;
+            ab.sqt = ab.skt = ab.svt = qc;
+            ab.sob = seq * d;
+            ab.soh = hd;
+            ab.sot = d;
+            ab.b = batch;
+            ab.h = cfg.heads;
+            ab.hkv = cfg.kv_heads;
+            ab.t = seq;
+            ab.hd = hd;
+            ab.cos_t = cos_t;
+            ab.sin_t = sin_t;
+            attention_backward(c, ab);
+            gemm(c, desc(tr.dqkv, false, qc, wqkv(l), true, qc, tr.dxn, d, n, qc, d));
+            gemm(c, desc(xn1, true, d, tr.dqkv, false, qc, tr.wtmp, qc, d, n, qc));
+            launch_unpack_cols(c, tr.wtmp, qc, 0, d, d, grad_of(wq));
+            launch_unpack_cols(c, tr.wtmp, qc, d, d, kv, grad_of(wk));
+            launch_unpack_cols(c, tr.wtmp, qc, d + kv, d, kv, grad_of(wv));
+            launch_rms_norm_backward(c, x, attn_norm(l), tr.dxn, n, d, cfg.eps, tr.dx, true,
+                                     grad_of(attn_norm(l)), tr.rms);
+        }
+        // embedding: the tied table already holds the head's share
+        if (!cfg.tie) launch_fill(c, grad, cfg.vocab * d, 0.0f);
+        launch_embedding_backward(c, tr.dx, d, tr.uniq, tr.start, tr.order, tr.n_unique, grad,
+                                  true);
+        (void)V;
+    }
+
+    void ensure_grad() {
+        if (!grad) check_hip(hipMalloc(&grad, (size_t)n_params * 4), "gradient alloc");
+    }
+
+    // Forward + loss + backward on the staged batch; gradients stay on the device.
+    void backward_staged(int64_t batch, int64_t seq) {
+        const int64_t n = batch * seq;
+        if (n != staged_n || !staged_targets || !staged_index || n > tr.cap)
+            fail(MMH_ERR_ARGUMENT, "no training batch staged for batch " + std::to_string(batch) +
+                                       " x seq " + std::to_string(seq));
+        ensure_grad();
+        enqueue_train_forward(batch, seq);
+        enqueue_backward(batch, seq);
+        launch_global_norm(*ctx, grad, n_params, tr.norm_scratch, tr.norm);
+        has_grad = true;
+    }
+
+    void ensure_optimizer_state() {
+        if (!has_opt) fail(MMH_ERR_ARGUMENT, "no optimizer set (mmh_model_set_optimizer)");
+        if (!mom1) {
+            check_hip(hipMalloc(&mom1, (size_t)n_params * 4), "moment alloc");
+            check_hip(hipMalloc(&mom2, (size_t)n_params * 4), "moment alloc");
+            launch_fill(*ctx, mom1, n_params, 0.0f);
+            launch_fill(*ctx, mom2, n_params, 0.0f);
+        }
+        if (!ranges) {
+            // rank-1 parameters: the two norms of every block and the final norm
+            std::vector<int64_t> r;
+            const int64_t d = cfg.d;
+            for (int64_t l = 0; l < cfg.layers; ++l) {
+                const int64_t a = attn_norm(l) - w, m = mlp_norm(l) - w;
+                r.insert(r.end(), {a, a + d, m, m + d});
+            }
+            const int64_t f = final_norm() - w;
+            r.insert(r.end(), {f, f + d});
+            nranges = (int)(r.size() / 2);
+            ranges_worst = adamw_max_ranges_per_chunk(r.data(), nranges, n_params);
+            check_hip(hipMalloc(&ranges, r.size() * 8), "range alloc");
+            check_hip(hipMemcpyAsync(ranges, r.data(), r.size() * 8, hipMemcpyHostToDevice,
+                                     ctx->stream), "range upload");
+            check_hip(hipStreamSynchronize(ctx->stream), "range upload sync");
+        }
+    }
+
+    // clip + AdamW at lr for optimizer step opt_steps + 1 (adamw.rs:180-188),
+    // gated on the device by the loss and norm being finite; then repack.
+    void enqueue_update(float lr) {
+        if (!(std::isfinite(lr) && lr >= 0.0f))
+            fail(MMH_ERR_ARGUMENT, "adamw: lr must be finite and not negative, got " +
+                                       std::to_string(lr));
+        ensure_optimizer_state();
+        const double t = (double)(opt_steps + 1);
+        AdamArgs a;
+        a.lr = lr;
+        a.beta1 = beta1;
+        a.beta2 = beta2;
+        a.eps = adam_eps;
+        a.weight_decay = weight_decay;
+        a.clip_norm = clip_norm;
+        const float bias1 = (float)(1.0 - std::pow((double)beta1, t));
+        a.bias2_sqrt = (float)std::sqrt(1.0 - std::pow((double)beta2, t));
+        a.step_size = lr / bias1;
+        launch_adamw(*ctx, w, grad, mom1, mom2, n_params, ranges, nranges, ranges_worst, a, loss,
+                     tr.norm);
+        repack();
+    }
+
+    // Reads the loss and the norm; true when both are finite.
+    bool read_step(float *loss_out, float *norm_out) {
+        float host[2];
+        check_hip(hipMemcpyAsync(&host[0], loss, 4, hipMemcpyDeviceToHost, ctx->stream),
+                  "loss download");
+        check_hip(hipMemcpyAsync(&host[1], tr.norm, 4, hipMemcpyDeviceToHost, ctx->stream),
+                  "norm download");
+        check_hip(hipStreamSynchronize(ctx->stream), "step sync");
+        if (loss_out) *loss_out = host[0];
+        if (norm_out) *norm_out = host[1];
+        return std::isfinite(host[0]) && std::isfinite(host[1]);
+    }
+
+    // Lab::step_once / Trainer::update on the staged batch. Returns false (and
+    // changes nothing) when the loss or the gradient norm is not finite.
+    bool train_staged(int64_t batch, int64_t seq, float lr, float *loss_out, float *norm_out) {
+        ensure_optimizer_state();
+        if (!(std::isfinite(lr) && lr >= 0.0f))
+            fail(MMH_ERR_ARGUMENT, "adamw: lr must be finite and not negative");
+        backward_staged(batch, seq);
+        enqueue_update(lr);
+        const bool ok = read_step(loss_out, norm_out);
+        if (ok) ++opt_steps;
+        return ok;
+    }
 };
 
 std::mutex g_models_mutex;
@@ -438,7 +835,8 @@ void release_models_of(mmh_handle ctx) {
     for (auto &m : dead) {
         m->drop_graph();
         for (void *p : {(void *)m->w, (void *)m->packed, (void *)m->cos_t, (void *)m->sin_t,
-                        (void *)m->act})
+                        (void *)m->act, (void *)m->tr.mem, (void *)m->grad, (void *)m->mom1,
+                        (void *)m->mom2, (void *)m->ranges})
             if (p) (void)hipFree(p);
     }
 }
@@ -643,6 +1041,142 @@ int32_t mmh_model_profile(mmh_handle model_h, int64_t batch, int64_t seq, float 
             check_hip(hipEventElapsedTime(&ms, mk.second.first, mk.second.second), "elapsed");
             class_ms[mk.first] += ms;
             class_launches[mk.first] += 1;
+        }
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_backward(mmh_handle model_h, const int32_t *inputs_host,
+                           const int32_t *targets_host, int64_t batch, int64_t seq,
+                           float *loss_host) {
+    return guard([&] {
+        Model &m = model(model_h);
+        m.stage_train(inputs_host, targets_host, batch, seq);
+        m.backward_staged(batch, seq);
+        m.read_step(loss_host, nullptr);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_download_grads(mmh_handle model_h, float *out_host, int64_t n) {
+    return guard([&] {
+        Model &m = model(model_h);
+        if (!out_host) fail(MMH_ERR_ARGUMENT, "out is a null pointer");
+        if (!m.has_grad) fail(MMH_ERR_ARGUMENT, "no gradients yet: run mmh_model_backward first");
+        if (n != m.n_params) fail(MMH_ERR_SHAPE, "gradients: wrong count");
+        check_hip(hipMemcpyAsync(out_host, m.grad, (size_t)n * 4, hipMemcpyDeviceToHost,
+                                 m.ctx->stream),
+                  "gradient download");
+        check_hip(hipStreamSynchronize(m.ctx->stream), "gradient download sync");
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_grad_norm(mmh_handle model_h, float *norm_host) {
+    return guard([&] {
+        Model &m = model(model_h);
+        if (!norm_host) fail(MMH_ERR_ARGUMENT, "norm is a null pointer");
+        if (!m.has_grad) fail(MMH_ERR_ARGUMENT, "no gradients yet: run mmh_model_backward first");
+        float host[2];
+        m.read_step(&host[0], &host[1]);
+        *norm_host = host[1];
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_set_optimizer(mmh_handle model_h, float beta1, float beta2, float eps,
+                                float weight_decay, float clip_norm) {
+    return guard([&] {
+        Model &m = model(model_h);
+        // adamw.rs:48-66 and lab.rs:185-190
+        if (!(beta1 >= 0.0f && beta1 < 1.0f))
+            fail(MMH_ERR_ARGUMENT, "adamw: beta1 must be in [0, 1), got " + std::to_string(beta1));
+        if (!(beta2 >= 0.0f && beta2 < 1.0f))
+            fail(MMH_ERR_ARGUMENT, "adamw: beta2 must be in [0, 1), got " + std::to_string(beta2));
+        if (!(std::isfinite(eps) && eps > 0.0f))
+            fail(MMH_ERR_ARGUMENT, "adamw: eps must be positive and finite");
+        if (!(std::isfinite(weight_decay) && weight_decay >= 0.0f))
+            fail(MMH_ERR_ARGUMENT, "adamw: weight_decay must be finite and not negative");
+        if (!(std::isfinite(clip_norm) && clip_norm > 0.0f))
+            fail(MMH_ERR_ARGUMENT, "clip_norm must be positive and finite");
+        m.beta1 = beta1;
+        m.beta2 = beta2;
+        m.adam_eps = eps;
+        m.weight_decay = weight_decay;
+        m.clip_norm = clip_norm;
+        m.has_opt = true;
+        m.opt_steps = 0;
+        if (m.mom1) {  // a new optimizer starts with no moments
+            launch_fill(*m.ctx, m.mom1, m.n_params, 0.0f);
+            launch_fill(*m.ctx, m.mom2, m.n_params, 0.0f);
+            check_hip(hipStreamSynchronize(m.ctx->stream), "optimizer reset sync");
+        }
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_stage_train(mmh_handle model_h, const int32_t *inputs_host,
+                              const int32_t *targets_host, int64_t batch, int64_t seq) {
+    return guard([&] {
+        model(model_h).stage_train(inputs_host, targets_host, batch, seq);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_train_staged(mmh_handle model_h, int64_t batch, int64_t seq, float lr,
+                               float *loss_host, float *grad_norm_host) {
+    return guard([&] {
+        Model &m = model(model_h);
+        float l = 0.0f, g = 0.0f;
+        const bool ok = m.train_staged(batch, seq, lr, &l, &g);
+        if (loss_host) *loss_host = l;
+        if (grad_norm_host) *grad_norm_host = g;
+        if (!ok) {  // lab.rs:268-271, clip.rs:48-50: nothing was changed
+            if (!std::isfinite(l))
+                fail(MMH_STOPPED, "the loss is " + std::to_string(l) + ", not a finite number");
+            fail(MMH_STOPPED, "clip: the gradient norm is not finite");
+        }
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_train_step(mmh_handle model_h, const int32_t *inputs_host,
+                             const int32_t *targets_host, int64_t batch, int64_t seq, float lr,
+                             float *loss_host, float *grad_norm_host) {
+    const int32_t st = mmh_model_stage_train(model_h, inputs_host, targets_host, batch, seq);
+    if (st != MMH_OK) return st;
+    return mmh_model_train_staged(model_h, batch, seq, lr, loss_host, grad_norm_host);
+}
+
+int32_t mmh_model_optimizer_steps(mmh_handle model_h, uint64_t *out) {
+    return guard([&] {
+        if (!out) fail(MMH_ERR_ARGUMENT, "out is a null pointer");
+        *out = model(model_h).opt_steps;
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
+                             uint64_t total_steps, uint64_t step, float *lr_out) {
+    return guard([&] {
+        if (!lr_out) fail(MMH_ERR_ARGUMENT, "lr is a null pointer");
+        // schedule.rs:25-48
+        if (!(std::isfinite(max_lr) && max_lr > 0.0f))
+            fail(MMH_ERR_ARGUMENT, "schedule: max_lr must be positive and finite");
+        if (!(std::isfinite(min_lr) && min_lr >= 0.0f && min_lr <= max_lr))
+            fail(MMH_ERR_ARGUMENT, "schedule: min_lr must be in [0, max_lr]");
+        if (warmup_steps >= total_steps)
+            fail(MMH_ERR_ARGUMENT, "schedule: warmup_steps must be below total_steps");
+        // schedule.rs:54-66
+        const double mx = (double)max_lr, mn = (double)min_lr;
+        if (step < warmup_steps) {
+            *lr_out = (float)(mx * (double)(step + 1) / (double)warmup_steps);
+        } else if (step >= total_steps) {
+            *lr_out = min_lr;
+        } else {
+            const double progress =
+                (double)(step - warmup_steps) / (double)(total_steps - warmup_steps);
+            *lr_out = (float)(mn + 0.5 * (mx - mn) * (1.0 + std::cos(M_PI * progress)));
         }
         return MMH_OK;
     });

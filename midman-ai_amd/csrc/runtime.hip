@@ -638,4 +638,149 @@ int32_t mmh_cross_entropy(mmh_handle ctx, const float *logits, const int32_t *ta
     });
 }
 
+// ---- op-level backward (the autograd closures of the layer seam) ----------
+
+int32_t mmh_rms_norm_backward(mmh_handle ctx, const float *x, const float *w, const float *dy,
+                              int64_t rows, int64_t d, float eps, float *dx, float *dw) {
+    return guard([&] {
+        Context &cx = context(ctx);
+        need(x, "x");
+        need(w, "w");
+        need(dy, "dy");
+        need(dx, "dx");
+        need(dw, "dw");
+        positive(rows, "rows");
+        positive(d, "d");
+        if (!(std::isfinite(eps) && eps > 0.0f))
+            fail(MMH_ERR_ARGUMENT, "rms_norm: eps must be positive and finite");
+        float *scratch = static_cast<float *>(
+            cx.workspace(2, (size_t)rms_norm_backward_scratch(rows, d) * 4 + 256));
+        launch_rms_norm_backward(cx, x, w, dy, rows, d, eps, dx, false, dw, scratch);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_apply_rope_backward(mmh_handle ctx, const float *dy, int64_t bh, int64_t t,
+                                int64_t hd, const float *cos_dev, const float *sin_dev,
+                                float *dx) {
+    return guard([&] {
+        Context &cx = context(ctx);
+        need(dy, "dy");
+        need(dx, "dx");
+        need(cos_dev, "cos");
+        need(sin_dev, "sin");
+        positive(bh, "bh");
+        positive(t, "time");
+        if (hd != 4 && hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
+            fail(MMH_ERR_SHAPE, "rope backward: head_dim must be 4, 8, 16, 32, 64 or 128");
+        if (dx != dy)
+            check_hip(hipMemcpyAsync(dx, dy, (size_t)(bh * t * hd) * 4, hipMemcpyDeviceToDevice,
+                                     cx.stream),
+                      "rope copy");
+        launch_rope_strided(cx, dx, 0, t * hd, hd, 1, bh, t, hd, cos_dev, sin_dev, true);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_causal_attention_backward(mmh_handle ctx, const float *q, const float *k,
+                                      const float *v, const float *dout, int64_t b, int64_t h,
+                                      int64_t hkv, int64_t t, int64_t hd, float *dq, float *dk,
+                                      float *dv) {
+    return guard([&] {
+        Context &cx = context(ctx);
+        need(q, "q");
+        need(k, "k");
+        need(v, "v");
+        need(dout, "dout");
+        need(dq, "dq");
+        need(dk, "dk");
+        need(dv, "dv");
+        positive(b, "batch");
+        positive(h, "n_heads");
+        positive(hkv, "n_kv_heads");
+        positive(t, "time");
+        positive(hd, "head_dim");
+        if (h % hkv) fail(MMH_ERR_SHAPE, "causal_attention: n_heads is not a multiple of n_kv_heads");
+        // forward output and log-sum-exp, then the backward
+        const int64_t rows = b * h * t;
+        const size_t o_floats = ((size_t)(rows * hd) + 63) / 64 * 64;
+        const size_t r_floats = ((size_t)rows + 63) / 64 * 64;
+        float *o = static_cast<float *>(cx.workspace(2, (o_floats + 2 * r_floats) * 4));
+        float *lse = o + o_floats, *dvec = lse + r_floats;
+        AttnDesc f{};
+        f.q = q;
+        f.k = k;
+        f.v = v;
+        f.out = o;
+        f.sqb = h * t * hd;
+        f.sqh = t * hd;
+        f.sqt = hd;
+        f.skb = hkv * t * hd;
+        f.skh = t * hd;
+        f.skt = hd;
+        f.svb = f.skb;
+        f.svh = f.skh;
+        f.svt = f.skt;
+        f.sob = f.sqb;
+        f.soh = f.sqh;
+        f.sot = f.sqt;
+        f.b = b;
+        f.h = h;
+        f.hkv = hkv;
+        f.t = t;
+        f.hd = hd;
+        f.lse = lse;
+        attention(cx, f);
+        AttnBwdDesc g{};
+        g.q = q;
+        g.k = k;
+        g.v = v;
+        g.o = o;
+        g.dout = dout;
+        g.lse = lse;
+        g.dq = dq;
+        g.dk = dk;
+        g.dv = dv;
+        g.dvec = dvec;
+        g.sqb = f.sqb; g.sqh = f.sqh; g.sqt = f.sqt;
+        g.skb = f.skb; g.skh = f.skh; g.skt = f.skt;
+        g.svb = f.svb; g.svh = f.svh; g.svt = f.svt;
+        g.sob = f.sob; g.soh = f.soh; g.sot = f.sot;
+        g.b = b;
+        g.h = h;
+        g.hkv = hkv;
+        g.t = t;
+        g.hd = hd;
+        attention_backward(cx, g);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_cross_entropy_backward(mmh_handle ctx, const float *logits,
+                                   const int32_t *targets_host, int64_t n, int64_t vocab,
+                                   float *dlogits, float *loss_host) {
+    return guard([&] {
+        Context &cx = context(ctx);
+        need(logits, "logits");
+        need(dlogits, "dlogits");
+        positive(n, "rows");
+        positive(vocab, "vocab");
+        check_ids(targets_host, n, vocab, "target class");
+        const int32_t *tg = cx.stage_ids(targets_host, n, 1);
+        float *rows = static_cast<float *>(cx.workspace(3, (size_t)(n + 64) * 4));
+        float *loss_dev = rows + ((n + 63) / 64) * 64;
+        if (dlogits != logits)
+            check_hip(hipMemcpyAsync(dlogits, logits, (size_t)(n * vocab) * 4,
+                                     hipMemcpyDeviceToDevice, cx.stream),
+                      "logits copy");
+        launch_cross_entropy_fwd_bwd(cx, dlogits, tg, n, vocab, 1.0f, rows, loss_dev);
+        if (loss_host) {
+            check_hip(hipMemcpyAsync(loss_host, loss_dev, 4, hipMemcpyDeviceToHost, cx.stream),
+                      "loss download");
+            check_hip(hipStreamSynchronize(cx.stream), "loss sync");
+        }
+        return MMH_OK;
+    });
+}
+
 }  // extern "C"

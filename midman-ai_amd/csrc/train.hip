@@ -1,0 +1,610 @@
+// Training-step kernels: the backward closures that are not GEMMs or
+// attention, the global gradient norm and the fused clip + AdamW update.
+//
+//   cross entropy forward + backward (ops_reduce.rs:236-275), one row per
+//     workgroup: the row's max and sum in one pass, then dlogits written in
+//     place over the logits.
+//   RMSNorm backward (norm.rs:36-38 through mul, mean_axis, add_scalar, powf):
+//     one wave per row with the row in registers; the weight gradient is summed
+//     per workgroup into a partial row, then over workgroups in a fixed order.
+//   embedding backward (ops_shape.rs:261-269): rows of the same id are added
+//     in position order from a host-built index (no atomics).
+//   unpacking of the fused QKV and interleaved gate/up weight gradients into
+//     the reference's parameter layout.
+//   global norm (clip.rs:30-33): f64 sum of squares, fixed reduction tree.
+//   clip + AdamW (clip.rs:42-60, adamw.rs:180-214): one pass over every
+//     parameter; nothing is written when the loss or the norm is not finite.
+// Element-wise arithmetic uses explicitly rounded intrinsics, so the update is
+// the reference's operation order with no contraction.
+#include "mmh_internal.h"
+
+namespace mmh {
+namespace {
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2) {
+    if (m2 == -INFINITY) return;
+    if (m == -INFINITY) {
+        m = m2;
+        s = s2;
+        return;
+    }
+    if (m2 > m) {
+        s = s * expf(m - m2) + s2;
+        m = m2;
+    } else {
+        s = s + s2 * expf(m2 - m);
+    }
+}
+
+// ---- cross entropy forward + backward ----------------------------------------
+// row_loss[row] = max + ln(sum) - z[t]; then z[j] <- exp(z[j] - max) / sum * scale,
+// minus scale at the target (ops_reduce.rs:263-272, scale = g / N).
+__global__ __launch_bounds__(256) void ce_fwd_bwd_kernel(float *__restrict__ logits,
+                                                         const int32_t *__restrict__ targets,
+                                                         int64_t v, float scale,
+                                                         float *__restrict__ row_loss, int vec) {
+    constexpr int CH = 4;
+    const int64_t row = blockIdx.x;
+    float *z = logits + row * v;
+    float4 *z4 = reinterpret_cast<float4 *>(z);
+    const int64_t v4 = vec ? v / 4 : 0;
+    float m = -INFINITY, s = 0.0f;
+    for (int64_t j0 = threadIdx.x; j0 < v4; j0 += 256 * CH) {
+        float4 a[CH];
+        float cm = -INFINITY;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) {
+            const int64_t j = j0 + 256 * c;
+            a[c] = j < v4 ? z4[j] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+            cm = fmaxf(cm, fmaxf(fmaxf(a[c].x, a[c].y), fmaxf(a[c].z, a[c].w)));
+        }
+        if (cm == -INFINITY) continue;
+        if (cm > m) {
+            s = s * expf(m - cm);
+            m = cm;
+        }
+        float cs = 0.0f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c)
+            cs += expf(a[c].x - m) + expf(a[c].y - m) + expf(a[c].z - m) + expf(a[c].w - m);
+        s += cs;
+    }
+    for (int64_t k = v4 * 4 + threadIdx.x; k < v; k += 256) {
+        const float x = z[k];
+        if (x > m) {
+            s = (m == -INFINITY) ? 0.0f : s * expf(m - x);
+            m = x;
+        }
+        s += expf(x - m);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
+        lse_merge(m, s, m2, s2);
+    }
+    __shared__ float sm[4], ss[4];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) {
+        sm[wave] = m;
+        ss[wave] = s;
+    }
+    __syncthreads();
+    float M = sm[0], S = ss[0];
+    for (int i = 1; i < 4; ++i) lse_merge(M, S, sm[i], ss[i]);
+    const int64_t t = targets[row];
+    if (threadIdx.x == 0) row_loss[row] = __fsub_rn(__fadd_rn(M, logf(S)), z[t]);
+    __syncthreads();  // z[t] is read before anything is overwritten
+    auto grad = [&](float x, int64_t j) {
+        const float d = __fmul_rn(__fdiv_rn(expf(__fsub_rn(x, M)), S), scale);
+        return j == t ? __fsub_rn(d, scale) : d;
+    };
+    for (int64_t j = threadIdx.x; j < v4; j += 256) {
+        float4 a = z4[j];
+        a.x = grad(a.x, 4 * j);
+        a.y = grad(a.y, 4 * j + 1);
+        a.z = grad(a.z, 4 * j + 2);
+        a.w = grad(a.w, 4 * j + 3);
+        z4[j] = a;
+    }
+    for (int64_t k = v4 * 4 + threadIdx.x; k < v; k += 256) z[k] = grad(z[k], k);
+}
+
+__global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__ row_loss,
+                                                       int64_t n, float *__restrict__ out) {
+    __shared__ double part[256];
+    double acc = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += 256) acc += (double)row_loss[i];
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if ((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[0] = (float)(part[0] / (double)n);
+}
+
+// ---- RMSNorm backward ----------------------------------------------------------
+// Per row (a = mean(x^2) + eps, inv = a^-1/2 as the forward computes it):
+//   dinv = sum_j (dy_j w_j) x_j, ds = dinv * (-0.5 * a^-3/2) * (1/d),
+//   share_j = ((dy_j w_j) inv + ds x_j) + ds x_j,  dx_j = [dx_j +] share_j,
+//   dw_j += dy_j (x_j inv).
+// Workgroup = 4 waves x RPW rows; each lane keeps the column partials of the
+// float4 columns it owns (lane + 64 i), the 4 waves' partials are summed in
+// LDS in wave order and written as one partial row per workgroup.
+constexpr int RMS_RPW = 2;  // rows per wave
+
+template <int NV>
+__global__ __launch_bounds__(256) void rms_bwd_rows_kernel(const float *__restrict__ x,
+                                                           const float *__restrict__ w,
+                                                           const float *__restrict__ dy,
+                                                           int64_t rows, int d, float eps,
+                                                           float *__restrict__ dx, int accumulate,
+                                                           float *__restrict__ partial) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int d4 = d >> 2;
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 pw[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) pw[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float inv_len = __fdiv_rn(1.0f, (float)d);
+    for (int rr = 0; rr < RMS_RPW; ++rr) {
+        const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * RMS_RPW + rr;
+        if (row >= rows) break;
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + row * d);
+        const float4 *g4 = reinterpret_cast<const float4 *>(dy + row * d);
+        float4 xv[NV], gv[NV];
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = lane + 64 * i;
+            xv[i] = j < d4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            gv[i] = j < d4 ? g4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        float ss = 0.0f, dinv = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = lane + 64 * i;
+            const float4 wv = j < d4 ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            ss = __fadd_rn(ss, __fmul_rn(xv[i].x, xv[i].x));
+            ss = __fadd_rn(ss, __fmul_rn(xv[i].y, xv[i].y));
+            ss = __fadd_rn(ss, __fmul_rn(xv[i].z, xv[i].z));
+            ss = __fadd_rn(ss, __fmul_rn(xv[i].w, xv[i].w));
+            // gv becomes dy*w from here on
+            gv[i].x = __fmul_rn(gv[i].x, wv.x);
+            gv[i].y = __fmul_rn(gv[i].y, wv.y);
+            gv[i].z = __fmul_rn(gv[i].z, wv.z);
+            gv[i].w = __fmul_rn(gv[i].w, wv.w);
+            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].x, xv[i].x));
+            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].y, xv[i].y));
+            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].z, xv[i].z));
+            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].w, xv[i].w));
+        }
+        ss = wave_sum(ss);
+        dinv = wave_sum(dinv);
+        const float a = __fadd_rn(__fmul_rn(ss, inv_len), eps);
+        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(a));
+        const float a32 = __fmul_rn(__fmul_rn(inv, inv), inv);  // a^-3/2
+        const float ds = __fmul_rn(__fmul_rn(dinv, __fmul_rn(-0.5f, a32)), inv_len);
+        float4 *o4 = reinterpret_cast<float4 *>(dx + row * d);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = lane + 64 * i;
+            if (j >= d4) continue;
+            const float4 gd = g4[j];  // dy again (cache) for the weight gradient
+            float4 sh;
+#define MMH_SHARE(c)                                                                   \
+    {                                                                                  \
+        const float t = __fmul_rn(ds, xv[i].c);                                        \
+        sh.c = __fadd_rn(__fadd_rn(__fmul_rn(gv[i].c, inv), t), t);                    \
+        pw[i].c = __fadd_rn(pw[i].c, __fmul_rn(gd.c, __fmul_rn(xv[i].c, inv)));        \
+    }
+            MMH_SHARE(x)
+            MMH_SHARE(y)
+            MMH_SHARE(z)
+            MMH_SHARE(w)
+#undef MMH_SHARE
+            if (accumulate) {
+                const float4 o = o4[j];
+                sh.x = __fadd_rn(o.x, sh.x);
+                sh.y = __fadd_rn(o.y, sh.y);
+                sh.z = __fadd_rn(o.z, sh.z);
+                sh.w = __fadd_rn(o.w, sh.w);
+            }
+            o4[j] = sh;
+        }
+    }
+    // Workgroup partial: waves 1..3 park theirs in LDS, wave 0 adds in order.
+    __shared__ float4 part[3][64 * NV];
+    if (wave > 0) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) part[wave - 1][lane + 64 * i] = pw[i];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float4 *out = reinterpret_cast<float4 *>(partial + (int64_t)blockIdx.x * d);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int j = lane + 64 * i;
+            if (j >= d4) continue;
+            float4 s = pw[i];
+            for (int wv = 0; wv < 3; ++wv) {
+                const float4 o = part[wv][j];
+                s.x = __fadd_rn(s.x, o.x);
+                s.y = __fadd_rn(s.y, o.y);
+                s.z = __fadd_rn(s.z, o.z);
+                s.w = __fadd_rn(s.w, o.w);
+            }
+            out[j] = s;
+        }
+    }
+}
+
+// Generic rows (any d): one wave per row, dx and the row's inv; the weight
+// gradient is formed afterwards by the column kernel below.
+__global__ __launch_bounds__(256) void rms_bwd_generic_kernel(const float *__restrict__ x,
+                                                              const float *__restrict__ w,
+                                                              const float *__restrict__ dy,
+                                                              int64_t rows, int64_t d, float eps,
+                                                              float *__restrict__ dx,
+                                                              int accumulate,
+                                                              float *__restrict__ inv_out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * d, *gr = dy + row * d;
+    float *o = dx + row * d;
+    float ss = 0.0f, dinv = 0.0f;
+    for (int64_t j = lane; j < d; j += 64) {
+        ss = __fadd_rn(ss, __fmul_rn(xr[j], xr[j]));
+        dinv = __fadd_rn(dinv, __fmul_rn(__fmul_rn(gr[j], w[j]), xr[j]));
+    }
+    ss = wave_sum(ss);
+    dinv = wave_sum(dinv);
+    const float inv_len = __fdiv_rn(1.0f, (float)d);
+    const float a = __fadd_rn(__fmul_rn(ss, inv_len), eps);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(a));
+    const float a32 = __fmul_rn(__fmul_rn(inv, inv), inv);
+    const float ds = __fmul_rn(__fmul_rn(dinv, __fmul_rn(-0.5f, a32)), inv_len);
+    for (int64_t j = lane; j < d; j += 64) {
+        const float t = __fmul_rn(ds, xr[j]);
+        float sh = __fadd_rn(__fadd_rn(__fmul_rn(__fmul_rn(gr[j], w[j]), inv), t), t);
+        if (accumulate) sh = __fadd_rn(o[j], sh);
+        o[j] = sh;
+    }
+    if (lane == 0) inv_out[row] = inv;
+}
+
+// partial[chunk][j] = sum over the chunk's rows (in order) of dy * (x * inv).
+__global__ __launch_bounds__(256) void rms_dw_cols_kernel(const float *__restrict__ x,
+                                                          const float *__restrict__ dy,
+                                                          const float *__restrict__ inv,
+                                                          int64_t rows, int64_t d,
+                                                          int64_t rows_per_chunk,
+                                                          float *__restrict__ partial) {
+    const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= d) return;
+    const int64_t r0 = (int64_t)blockIdx.y * rows_per_chunk;
+    const int64_t r1 = min(rows, r0 + rows_per_chunk);
+    float acc = 0.0f;
+    for (int64_t r = r0; r < r1; ++r)
+        acc = __fadd_rn(acc, __fmul_rn(dy[r * d + j], __fmul_rn(x[r * d + j], inv[r])));
+    partial[(int64_t)blockIdx.y * d + j] = acc;
+}
+
+// out[j] = sum over the partial rows: workgroup = 64 columns x 4 waves; wave w
+// sums rows w, w+4, w+8, ... (four independent loads in flight), then the four
+// wave sums are added in wave order. Fixed order for a given nrows.
+__global__ __launch_bounds__(256) void sum_rows_kernel(const float *__restrict__ partial,
+                                                       int64_t nrows, int64_t d,
+                                                       float *__restrict__ out) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t j = (int64_t)blockIdx.x * 64 + lane;
+    float acc = 0.0f;
+    if (j < d) {
+        int64_t r = wave;
+        for (; r + 12 < nrows; r += 16) {
+            const float a0 = partial[r * d + j], a1 = partial[(r + 4) * d + j];
+            const float a2 = partial[(r + 8) * d + j], a3 = partial[(r + 12) * d + j];
+            acc = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(acc, a0), a1), a2), a3);
+        }
+        for (; r < nrows; r += 4) acc = __fadd_rn(acc, partial[r * d + j]);
+    }
+    __shared__ float part[4][64];
+    part[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && j < d)
+        out[j] = __fadd_rn(__fadd_rn(__fadd_rn(part[0][lane], part[1][lane]), part[2][lane]),
+                           part[3][lane]);
+}
+
+// ---- embedding backward ----------------------------------------------------------
+// Workgroup u owns table row ids[u]: the gradient rows at positions
+// order[start[u] .. start[u+1]) are added in that (ascending) order from zero,
+// then added to the row's current value when accumulate is set.
+__global__ __launch_bounds__(256) void embedding_bwd_kernel(const float *__restrict__ g,
+                                                            int64_t d,
+                                                            const int32_t *__restrict__ uniq,
+                                                            const int32_t *__restrict__ start,
+                                                            const int32_t *__restrict__ order,
+                                                            float *__restrict__ table,
+                                                            int accumulate) {
+    const int u = blockIdx.x;
+    const int64_t row = uniq[u];
+    const int p0 = start[u], p1 = start[u + 1];
+    for (int64_t c = (int64_t)blockIdx.y * 256 + threadIdx.x; c < d; c += (int64_t)gridDim.y * 256) {
+        float acc = 0.0f;
+        for (int p = p0; p < p1; ++p) acc = __fadd_rn(acc, g[(int64_t)order[p] * d + c]);
+        float *dst = table + row * d + c;
+        *dst = accumulate ? __fadd_rn(*dst, acc) : acc;
+    }
+}
+
+__global__ __launch_bounds__(256) void fill_kernel(float *__restrict__ x, int64_t n, float v) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        x[i] = v;
+}
+
+// ---- weight-gradient unpacking ------------------------------------------------------
+__global__ __launch_bounds__(256) void unpack_cols_kernel(const float *__restrict__ src,
+                                                          int64_t ld_src, int64_t col_off,
+                                                          int64_t rows, int64_t cols,
+                                                          float *__restrict__ dst) {
+    const int64_t total = rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / cols, c = i - r * cols;
+        dst[i] = src[r * ld_src + col_off + c];
+    }
+}
+
+// src [rows, 2*ff_pad] interleaved (2f gate, 2f+1 up) -> wg, wu [rows, ff].
+__global__ __launch_bounds__(256) void unpack_gate_up_kernel(const float *__restrict__ src,
+                                                             int64_t rows, int64_t ff,
+                                                             int64_t ff_pad,
+                                                             float *__restrict__ wg,
+                                                             float *__restrict__ wu) {
+    const int64_t total = rows * ff;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t r = i / ff, f = i - r * ff;
+        const float2 v = *reinterpret_cast<const float2 *>(src + r * 2 * ff_pad + 2 * f);
+        wg[i] = v.x;
+        wu[i] = v.y;
+    }
+}
+
+// ---- global norm ---------------------------------------------------------------------
+constexpr int NORM_BLOCKS = 1024;
+
+// Block b sums the squares of elements b*256 + t, stepping by NORM_BLOCKS*256,
+// in f64; then a tree inside the block. Fixed order for a given n.
+__global__ __launch_bounds__(256) void sumsq_partial_kernel(const float *__restrict__ g,
+                                                            int64_t n,
+                                                            double *__restrict__ partial) {
+    __shared__ double part[256];
+    double acc = 0.0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (int64_t)NORM_BLOCKS * 256) {
+        const double v = (double)g[i];
+        acc += v * v;
+    }
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if ((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) partial[blockIdx.x] = part[0];
+}
+
+__global__ __launch_bounds__(256) void norm_final_kernel(const double *__restrict__ partial,
+                                                         float *__restrict__ norm) {
+    __shared__ double part[256];
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < NORM_BLOCKS; i += 256) acc += partial[i];
+    part[threadIdx.x] = acc;
+    __syncthreads();
+    for (int stride = 128; stride > 0; stride >>= 1) {
+        if ((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) norm[0] = (float)sqrt(part[0]);
+}
+
+// ---- clip + AdamW ----------------------------------------------------------------------
+// Workgroup chunk [c0, c1) of the flat parameter list; the rank-1 ranges
+// (no weight decay) that meet the chunk are gathered into LDS first.
+constexpr int ADAM_CHUNK = 8192;
+constexpr int ADAM_MAX_RANGES = 64;
+
+__global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ w,
+                                                    const float *__restrict__ g,
+                                                    float *__restrict__ m, float *__restrict__ v,
+                                                    int64_t n, const int64_t *__restrict__ ranges,
+                                                    int nranges, AdamArgs a,
+                                                    const float *__restrict__ loss,
+                                                    const float *__restrict__ norm) {
+    const float ln = loss[0], nv = norm[0];
+    if (!(isfinite(ln) && isfinite(nv))) return;  // a failed step changes nothing
+    const bool clip = nv > a.clip_norm;
+    const float factor = __fdiv_rn(a.clip_norm, __fadd_rn(nv, 1e-6f));  // clip.rs:52
+    const int64_t c0 = (int64_t)blockIdx.x * ADAM_CHUNK;
+    const int64_t c1 = min(n, c0 + ADAM_CHUNK);
+    __shared__ int64_t lo[ADAM_MAX_RANGES], hi[ADAM_MAX_RANGES];
+    __shared__ int cnt;
+    if (threadIdx.x == 0) {
+        int k = 0;
+        for (int r = 0; r < nranges; ++r) {
+            const int64_t s = ranges[2 * r], e = ranges[2 * r + 1];
+            if (s < c1 && e > c0 && k < ADAM_MAX_RANGES) {
+                lo[k] = s;
+                hi[k] = e;
+                ++k;
+            }
+        }
+        cnt = k;
+    }
+    __syncthreads();
+    const int k = cnt;
+    const float one_b1 = __fsub_rn(1.0f, a.beta1), one_b2 = __fsub_rn(1.0f, a.beta2);
+    const float decay = __fsub_rn(1.0f, __fmul_rn(a.lr, a.weight_decay));
+    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+        bool rank1 = false;
+        for (int r = 0; r < k; ++r) rank1 |= (i >= lo[r] && i < hi[r]);
+        float grad = g[i];
+        if (clip) grad = __fmul_rn(grad, factor);
+        float x = w[i];
+        if (!rank1) x = __fmul_rn(x, decay);
+        const float mi = __fadd_rn(__fmul_rn(a.beta1, m[i]), __fmul_rn(one_b1, grad));
+        const float vi =
+            __fadd_rn(__fmul_rn(a.beta2, v[i]), __fmul_rn(__fmul_rn(one_b2, grad), grad));
+        const float den = __fadd_rn(__fdiv_rn(__fsqrt_rn(vi), a.bias2_sqrt), a.eps);
+        x = __fsub_rn(x, __fdiv_rn(__fmul_rn(a.step_size, mi), den));
+        m[i] = mi;
+        v[i] = vi;
+        w[i] = x;
+    }
+}
+
+unsigned grid_for(int64_t work, int per_block = 256) {
+    int64_t b = (work + per_block - 1) / per_block;
+    if (b < 1) b = 1;
+    if (b > 65536) b = 65536;
+    return (unsigned)b;
+}
+
+bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+void launch_cross_entropy_fwd_bwd(Context &ctx, float *logits, const int32_t *targets_dev,
+                                  int64_t n, int64_t v, float g, float *row_loss,
+                                  float *loss_dev) {
+    if (n > 0x7fffffff) fail(MMH_ERR_SHAPE, "cross_entropy: too many rows");
+    const int vec = (v % 4 == 0) && al16(logits);
+    hipLaunchKernelGGL(ce_fwd_bwd_kernel, dim3((unsigned)n), dim3(256), 0, ctx.stream, logits,
+                       targets_dev, v, g / (float)n, row_loss, vec);
+    check_hip(hipGetLastError(), "cross_entropy backward launch");
+    hipLaunchKernelGGL(mean_f64_kernel, dim3(1), dim3(256), 0, ctx.stream, row_loss, n,
+                       loss_dev);
+    check_hip(hipGetLastError(), "loss mean launch");
+}
+
+int64_t rms_norm_backward_scratch(int64_t rows, int64_t d) {
+    // partial rows (fast path: one per workgroup of 4*RMS_RPW rows; generic: row
+    // chunks of 64) plus one inv per row.
+    const int64_t fast = (rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW);
+    const int64_t generic = (rows + 63) / 64;
+    return (fast > generic ? fast : generic) * d + rows;
+}
+
+void launch_rms_norm_backward(Context &ctx, const float *x, const float *w, const float *dy,
+                              int64_t rows, int64_t d, float eps, float *dx, bool accumulate,
+                              float *dw, float *scratch) {
+    const int vec = (d % 4 == 0) && d <= 4096 && al16(x) && al16(w) && al16(dy) && al16(dx) &&
+                    al16(scratch);
+    if (vec) {
+        const int64_t blocks = (rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW);
+        if (blocks > 0x7fffffff) fail(MMH_ERR_SHAPE, "rms_norm backward: too many rows");
+        const dim3 grid((unsigned)blocks), block(256);
+        const int dd = (int)d, acc = accumulate ? 1 : 0;
+        if (d <= 256)
+            hipLaunchKernelGGL(rms_bwd_rows_kernel<1>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
+        else if (d <= 512)
+            hipLaunchKernelGGL(rms_bwd_rows_kernel<2>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
+        else if (d <= 1024)
+            hipLaunchKernelGGL(rms_bwd_rows_kernel<4>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
+        else if (d <= 2048)
+            hipLaunchKernelGGL(rms_bwd_rows_kernel<8>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
+        else
+            hipLaunchKernelGGL(rms_bwd_rows_kernel<16>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
+        check_hip(hipGetLastError(), "rms_norm backward launch");
+        hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(256), 0, ctx.stream,
+                           scratch, blocks, d, dw);
+        check_hip(hipGetLastError(), "rms_norm dw launch");
+        return;
+    }
+    const int64_t chunks = (rows + 63) / 64;
+    float *inv = scratch + chunks * d;
+    hipLaunchKernelGGL(rms_bwd_generic_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       ctx.stream, x, w, dy, rows, d, eps, dx, accumulate ? 1 : 0, inv);
+    check_hip(hipGetLastError(), "rms_norm backward launch");
+    hipLaunchKernelGGL(rms_dw_cols_kernel, dim3(grid_for(d), (unsigned)chunks), dim3(256), 0,
+                       ctx.stream, x, dy, inv, rows, d, (int64_t)64, scratch);
+    check_hip(hipGetLastError(), "rms_norm dw launch");
+    hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(256), 0, ctx.stream, scratch,
+                       chunks, d, dw);
+    check_hip(hipGetLastError(), "rms_norm dw launch");
+}
+
+void launch_embedding_backward(Context &ctx, const float *g, int64_t d, const int32_t *uniq,
+                               const int32_t *start, const int32_t *order, int64_t n_unique,
+                               float *table, bool accumulate) {
+    if (n_unique <= 0) return;
+    if (n_unique > 0x7fffffff) fail(MMH_ERR_SHAPE, "embedding backward: too many ids");
+    const unsigned ycols = (unsigned)std::min<int64_t>((d + 255) / 256, 16);
+    hipLaunchKernelGGL(embedding_bwd_kernel, dim3((unsigned)n_unique, ycols), dim3(256), 0,
+                       ctx.stream, g, d, uniq, start, order, table, accumulate ? 1 : 0);
+    check_hip(hipGetLastError(), "embedding backward launch");
+}
+
+void launch_fill(Context &ctx, float *x, int64_t n, float v) {
+    hipLaunchKernelGGL(fill_kernel, dim3(grid_for(n)), dim3(256), 0, ctx.stream, x, n, v);
+    check_hip(hipGetLastError(), "fill launch");
+}
+
+void launch_unpack_cols(Context &ctx, const float *src, int64_t ld_src, int64_t col_off,
+                        int64_t rows, int64_t cols, float *dst) {
+    hipLaunchKernelGGL(unpack_cols_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, ctx.stream,
+                       src, ld_src, col_off, rows, cols, dst);
+    check_hip(hipGetLastError(), "unpack launch");
+}
+
+void launch_unpack_gate_up(Context &ctx, const float *src, int64_t rows, int64_t ff,
+                           int64_t ff_pad, float *wg, float *wu) {
+    hipLaunchKernelGGL(unpack_gate_up_kernel, dim3(grid_for(rows * ff)), dim3(256), 0,
+                       ctx.stream, src, rows, ff, ff_pad, wg, wu);
+    check_hip(hipGetLastError(), "unpack launch");
+}
+
+int64_t global_norm_scratch_bytes() { return (int64_t)NORM_BLOCKS * 8; }
+
+void launch_global_norm(Context &ctx, const float *g, int64_t n, double *scratch, float *norm) {
+    hipLaunchKernelGGL(sumsq_partial_kernel, dim3(NORM_BLOCKS), dim3(256), 0, ctx.stream, g, n,
+                       scratch);
+    check_hip(hipGetLastError(), "norm launch");
+    hipLaunchKernelGGL(norm_final_kernel, dim3(1), dim3(256), 0, ctx.stream, scratch, norm);
+    check_hip(hipGetLastError(), "norm launch");
+}
+
+int64_t adamw_max_ranges_per_chunk(const int64_t *ranges_host, int nranges, int64_t n) {
+    int64_t worst = 0;
+    for (int64_t c0 = 0; c0 < n; c0 += ADAM_CHUNK) {
+        const int64_t c1 = std::min<int64_t>(n, c0 + ADAM_CHUNK);
+        int64_t k = 0;
+        for (int r = 0; r < nranges; ++r)
+            if (ranges_host[2 * r] < c1 && ranges_host[2 * r + 1] > c0) ++k;
+        worst = std::max(worst, k);
+    }
+    return worst;
+}
+
+void launch_adamw(Context &ctx, float *w, const float *g, float *m, float *v, int64_t n,
+                  const int64_t *ranges_dev, int nranges, int64_t max_per_chunk,
+                  const AdamArgs &a, const float *loss_dev, const float *norm_dev) {
+    if (max_per_chunk > ADAM_MAX_RANGES)
+        fail(MMH_ERR_ARGUMENT, "adamw: too many undecayed parameters in one chunk");
+    const int64_t blocks = (n + ADAM_CHUNK - 1) / ADAM_CHUNK;
+    if (blocks > 0x7fffffff) fail(MMH_ERR_SHAPE, "adamw: too many parameters");
+    hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx.stream, w, g, m,
+                       v, n, ranges_dev, nranges, a, loss_dev, norm_dev);
+    check_hip(hipGetLastError(), "adamw launch");
+}
+
+}  // namespace mmh

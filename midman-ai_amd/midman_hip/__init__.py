@@ -116,6 +116,20 @@ _SIGNATURES = {
     "mmh_model_run_staged": [_h, _i64, _i64],
     "mmh_model_read_loss": [_h, _f32p],
     "mmh_model_profile": [_h, _i64, _i64, _f32p, _i32p],
+    "mmh_rms_norm_backward": [_h, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp],
+    "mmh_apply_rope_backward": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
+    "mmh_causal_attention_backward": [_h, _vp, _vp, _vp, _vp] + [_i64] * 5 + [_vp] * 3,
+    "mmh_cross_entropy_backward": [_h, _vp, _i32p, _i64, _i64, _vp, _f32p],
+    "mmh_model_backward": [_h, _i32p, _i32p, _i64, _i64, _f32p],
+    "mmh_model_download_grads": [_h, _f32p, _i64],
+    "mmh_model_grad_norm": [_h, _f32p],
+    "mmh_model_set_optimizer": [_h] + [ctypes.c_float] * 5,
+    "mmh_model_train_step": [_h, _i32p, _i32p, _i64, _i64, ctypes.c_float, _f32p, _f32p],
+    "mmh_model_stage_train": [_h, _i32p, _i32p, _i64, _i64],
+    "mmh_model_train_staged": [_h, _i64, _i64, ctypes.c_float, _f32p, _f32p],
+    "mmh_model_optimizer_steps": [_h, ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_warmup_cosine_lr": [ctypes.c_float, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64,
+                             ctypes.c_uint64, _f32p],
 }
 
 PROFILE_CLASSES = ("embedding", "rms_norm", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down",
@@ -166,6 +180,20 @@ def randn(shape, std: float, seed: int) -> np.ndarray:
     out = np.empty(shape, np.float32)
     check(lib().mmh_randn(seed, std, out.ctypes.data_as(_f32p), out.size))
     return out
+
+
+def warmup_cosine_lr(max_lr: float, min_lr: float, warmup_steps: int, total_steps: int,
+                     step: int) -> float:
+    """WarmupCosine::new(..).lr(step) (schedule.rs:25-66)."""
+    out = ctypes.c_float()
+    check(lib().mmh_warmup_cosine_lr(max_lr, min_lr, warmup_steps, total_steps, step,
+                                     ctypes.byref(out)))
+    return out.value
+
+
+class Stopped(MidmanError):
+    """A training step that did not run because the loss or the gradient norm
+    was not finite (lab.rs:268-271, clip.rs:48-50); nothing was changed."""
 
 
 def _fp(a: np.ndarray):
@@ -400,6 +428,59 @@ def cross_entropy(ctx: Context, logits: DeviceArray, targets: np.ndarray) -> flo
     return loss.value
 
 
+# ---- backward closures of the layer seam ---------------------------------------------
+
+def rms_norm_backward(ctx: Context, x: DeviceArray, w: DeviceArray, dy: DeviceArray, eps: float):
+    """rms_norm's backward (norm.rs:36-38): (dx, dw)."""
+    d = x.shape[-1]
+    if w.shape != (d,) or dy.shape != x.shape:
+        raise ShapeError(ERR_SHAPE, "rms_norm backward: x, w, dy do not fit")
+    dx = ctx.empty(x.shape)
+    dw = ctx.empty((d,))
+    check(lib().mmh_rms_norm_backward(ctx.handle, x.ptr, w.ptr, dy.ptr, x.size // d, d, eps,
+                                      dx.ptr, dw.ptr))
+    return dx, dw
+
+
+def apply_rope_backward(ctx: Context, dy: DeviceArray, tables: RotaryTables,
+                        out: DeviceArray = None):
+    """apply_rope's backward (rope.rs:28-32): rotation by -angle."""
+    t, hd = dy.shape[-2], dy.shape[-1]
+    if t > tables.max_seq_len:
+        raise ShapeError(ERR_SHAPE, "rope: sequence longer than the tables")
+    out = out or ctx.empty(dy.shape)
+    check(lib().mmh_apply_rope_backward(ctx.handle, dy.ptr, dy.size // (t * hd), t, hd,
+                                        tables.cos.ptr, tables.sin.ptr, out.ptr))
+    return out
+
+
+def causal_attention_backward(ctx: Context, q: DeviceArray, k: DeviceArray, v: DeviceArray,
+                              dout: DeviceArray):
+    """causal_attention's backward (attention.rs:79-101): (dq, dk, dv)."""
+    if len(q.shape) != 4 or len(k.shape) != 4 or k.shape != v.shape or dout.shape != q.shape:
+        raise ShapeError(ERR_SHAPE, "causal_attention backward: shapes do not fit")
+    B, H, T, hd = q.shape
+    dq, dk, dv = ctx.empty(q.shape), ctx.empty(k.shape), ctx.empty(v.shape)
+    check(lib().mmh_causal_attention_backward(ctx.handle, q.ptr, k.ptr, v.ptr, dout.ptr, B, H,
+                                              k.shape[1], T, hd, dq.ptr, dk.ptr, dv.ptr))
+    return dq, dk, dv
+
+
+def cross_entropy_backward(ctx: Context, logits: DeviceArray, targets: np.ndarray):
+    """Tensor::cross_entropy backward (ops_reduce.rs:261-275): (loss, dlogits)."""
+    if len(logits.shape) != 2:
+        raise ShapeError(ERR_SHAPE, "cross_entropy: logits must have shape [N, V]")
+    n, v = logits.shape
+    targets = np.ascontiguousarray(targets, dtype=np.int32)
+    if targets.size != n:
+        raise ShapeError(ERR_SHAPE, f"cross_entropy: {n} logit rows but {targets.size} targets")
+    out = ctx.empty(logits.shape)
+    loss = ctypes.c_float()
+    check(lib().mmh_cross_entropy_backward(ctx.handle, logits.ptr, _ip(targets), n, v, out.ptr,
+                                           ctypes.byref(loss)))
+    return loss.value, out
+
+
 # ---- the model: midman-model/src/model.rs ------------------------------------------
 
 CONFIG_FIELDS = ("vocab_size", "d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff",
@@ -516,7 +597,115 @@ class Model:
         check(lib().mmh_model_profile(self.handle, batch, seq, ms, cnt))
         return {name: (ms[i], cnt[i]) for i, name in enumerate(PROFILE_CLASSES)}
 
+    # ---- training ---------------------------------------------------------
+    def backward(self, inputs, targets, batch: int, seq: int) -> float:
+        """loss.backward() (model.rs:174-183): returns the loss; the gradients
+        stay on the device (grads(), grad_norm())."""
+        x, y = self._pair(inputs, targets, batch, seq)
+        loss = ctypes.c_float()
+        check(lib().mmh_model_backward(self.handle, _ip(x), _ip(y), batch, seq,
+                                       ctypes.byref(loss)))
+        return loss.value
+
+    def grads(self) -> np.ndarray:
+        """Gradients of the last backward / step, in the reference parameter order."""
+        n = self.num_parameters()
+        out = np.empty(n, np.float32)
+        check(lib().mmh_model_download_grads(self.handle, _fp(out), n))
+        return out
+
+    def grad_norm(self) -> float:
+        out = ctypes.c_float()
+        check(lib().mmh_model_grad_norm(self.handle, ctypes.byref(out)))
+        return out.value
+
+    def set_optimizer(self, beta1: float, beta2: float, eps: float, weight_decay: float,
+                      clip_norm: float):
+        """AdamW::new(beta1, beta2, eps, weight_decay) plus the clip limit."""
+        check(lib().mmh_model_set_optimizer(self.handle, beta1, beta2, eps, weight_decay,
+                                            clip_norm))
+
+    def train_step(self, inputs, targets, batch: int, seq: int, lr: float):
+        """Lab::step_once / Trainer::update: (loss, grad_norm before clipping).
+        Raises Stopped, changing nothing, on a non-finite loss or norm."""
+        x, y = self._pair(inputs, targets, batch, seq)
+        loss, norm = ctypes.c_float(), ctypes.c_float()
+        st = lib().mmh_model_train_step(self.handle, _ip(x), _ip(y), batch, seq, lr,
+                                        ctypes.byref(loss), ctypes.byref(norm))
+        if st == STOPPED:
+            raise Stopped(st, last_error())
+        check(st)
+        return loss.value, norm.value
+
+    def stage_train(self, inputs, targets, batch: int, seq: int):
+        x, y = self._pair(inputs, targets, batch, seq)
+        check(lib().mmh_model_stage_train(self.handle, _ip(x), _ip(y), batch, seq))
+
+    def train_staged(self, batch: int, seq: int, lr: float):
+        loss, norm = ctypes.c_float(), ctypes.c_float()
+        st = lib().mmh_model_train_staged(self.handle, batch, seq, lr, ctypes.byref(loss),
+                                          ctypes.byref(norm))
+        if st == STOPPED:
+            raise Stopped(st, last_error())
+        check(st)
+        return loss.value, norm.value
+
+    def optimizer_steps(self) -> int:
+        out = ctypes.c_uint64()
+        check(lib().mmh_model_optimizer_steps(self.handle, ctypes.byref(out)))
+        return out.value
+
     def close(self):
         if self.handle:
             check(lib().mmh_model_destroy(self.handle))
             self.handle = 0
+
+
+class Lab:
+    """midman-api's Lab (lab.rs:150-310) on the device: the model from
+    Rng(seed), the fixed memorization task from the same Rng, and training
+    steps with WarmupCosine + global-norm clip + AdamW.
+
+    hyper = (max_lr, min_lr, warmup_steps, total_steps, weight_decay,
+    clip_norm, beta1, beta2) (lab.rs:29-46); eps is 1e-8 (lab.rs:192)."""
+
+    def __init__(self, ctx: Context, config, hyper, seed: int, batch: int, seq: int):
+        self.config, self.batch, self.seq = list(config), batch, seq
+        h = [float(x) for x in hyper]
+        self.max_lr, self.min_lr = h[0], h[1]
+        self.warmup, self.total = int(h[2]), int(h[3])
+        warmup_cosine_lr(self.max_lr, self.min_lr, self.warmup, self.total, 0)  # validates
+        self.model = Model.new(ctx, config, seed)
+        self.inputs, self.targets = self.model.lab_tokens(batch, seq)
+        self.model.set_optimizer(h[6], h[7], 1e-8, h[4], h[5])
+        self.model.stage_train(self.inputs, self.targets, batch, seq)
+        self.steps = 0
+
+    def step(self, steps: int):
+        """Lab::step (lab.rs:241-258): (losses, grad_norms, lrs, stopped message or None)."""
+        losses, norms, lrs = [], [], []
+        stopped = None
+        for _ in range(steps):
+            lr = warmup_cosine_lr(self.max_lr, self.min_lr, self.warmup, self.total, self.steps)
+            try:
+                loss, norm = self.model.train_staged(self.batch, self.seq, lr)
+            except Stopped as e:
+                stopped = e.message
+                break
+            self.steps += 1
+            losses.append(loss)
+            norms.append(norm)
+            lrs.append(lr)
+        return losses, norms, lrs, stopped
+
+    def eval(self):
+        """Lab::eval (lab.rs:290-310): (loss, accuracy, predictions)."""
+        logits = self.model.forward(self.inputs, self.batch, self.seq)
+        loss = self.model.loss(self.inputs, self.targets, self.batch, self.seq)
+        pred = logits.reshape(-1, logits.shape[-1]).argmax(-1).astype(np.int32)
+        acc = float((pred == self.targets).mean())
+        self.model.stage_train(self.inputs, self.targets, self.batch, self.seq)
+        return loss, acc, pred
+
+    def close(self):
+        self.model.close()
