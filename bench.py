@@ -5,7 +5,8 @@ Headline (`value`): forward + cross-entropy loss tokens/s of the reference's
 `large` preset (1,009,338,368 parameters) at batch 4 x seq 1024, seeded
 reference init, uniform token ids, all in f32, with the weights and the token
 ids resident in HBM when the timed region starts. One step = one forward +
-loss over the batch (mmh_model_run_staged). Also reported: the tiny preset
+loss over the batch (mmh_model_run_staged). Also reported: the large-preset
+training step (forward + loss + backward + clip + AdamW), the tiny preset
 (B8 T256), the BASELINE GEMM sweep (M=2048, K,N in {256,1024,4096}, forward
 C=A.B and backward dA=dC.B^T, dB=A^T.dC), a per-kernel-class breakdown from
 HIP events, the roofline of the dominant kernel (the fp32 MFMA GEMM) and the
@@ -32,6 +33,13 @@ import numpy as np  # noqa: E402
 METRIC = "forward+loss tokens/sec (tiny, large presets) + GEMM fp32 TFLOPS % of MFMA peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3  # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0
+# HBM bytes per GEMM launch of one large forward (the roofline kernel), from two
+# rocprofv3 passes over this same bench (--pmc FETCH_SIZE, then --pmc
+# WRITE_SIZE, --steps 1 --warmup 0 --train-steps 0 --copy-probe), each scaled by
+# what the counter reads for the add kernel's known traffic (FETCH x 2.0,
+# WRITE x 1.0): (43,181,710 + 4,935,760) KiB over 81 launches. The counters
+# cannot be read from inside this process; see profiles/large_forward_hbm_traffic.md.
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 608.3e6
 
 
 def log(msg):
@@ -67,7 +75,26 @@ def model_bytes(cfg, B, T):
     }
 
 
-def time_model(mh, ctx, preset, B, T, steps, warmup):
+def time_train(mh, m, B, T, steps, warmup):
+    """Training steps on the model's own weights (Lab::step_once /
+    Trainer::update on the device): forward + loss + backward + f64 global
+    norm + clip + AdamW + repack, ids staged once. Wall clock per step,
+    including the per-step read of the loss and the norm."""
+    m.set_optimizer(0.9, 0.95, 1e-8, 0.1, 1.0)
+    x, y = m.lab_tokens(B, T)
+    m.stage_train(x, y, B, T)
+    for _ in range(warmup):
+        m.train_staged(B, T, 1e-4)
+    rec = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        rec.append(m.train_staged(B, T, 1e-4))
+    ms = (time.perf_counter() - t0) * 1000 / steps
+    return {"ms_per_step": ms, "tokens_per_s": B * T / (ms / 1000),
+            "first_loss": rec[0][0], "last_loss": rec[-1][0], "grad_norm": rec[-1][1]}
+
+
+def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0):
     cfg = mh.PRESETS[preset]
     t0 = time.time()
     m = mh.Model.new(ctx, cfg, 0)
@@ -90,9 +117,11 @@ def time_model(mh, ctx, preset, B, T, steps, warmup):
         m.loss(x, y, B, T)
     host_ms = (time.perf_counter() - t1) * 1000 / max(1, steps // 2)
     prof = m.profile(B, T)
+    train = time_train(mh, m, B, T, train_steps, 2) if train_steps else None
     m.close()
     return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
-            "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg}
+            "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg,
+            "train": train}
 
 
 def gemm_sweep(mh, ctx, reps=10):
@@ -185,6 +214,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-tiny", action="store_true")
+    ap.add_argument("--train-steps", type=int, default=5,
+                    help="large-preset training steps to time after the forward (0: none)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one add kernel over 2^26 floats (read 512 MiB, write "
                          "256 MiB) to calibrate HBM byte counters")
@@ -208,9 +239,13 @@ def main():
             b.free()
         log("copy probe: add over 2^26 floats done")
 
-    large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup)
+    large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup, a.train_steps)
     log(f"large: {large['ms_per_step']:.2f} ms/step, {large['tokens_per_s']:.0f} tok/s, "
         f"loss {large['loss']:.5f}")
+    if large["train"]:
+        tr = large["train"]
+        log(f"large train step: {tr['ms_per_step']:.1f} ms, {tr['tokens_per_s']:.0f} tok/s, "
+            f"loss {tr['first_loss']:.4f} -> {tr['last_loss']:.4f}")
     tiny = None
     if not a.no_tiny:
         tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5))
@@ -269,7 +304,9 @@ def main():
                    "flops_per_step": total_flops},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                      "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                     "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
+                     "traffic_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE passes, scaled x2.0/x1.0",
                      "kernel": "gemm_f32_mfma (all GEMM launches of one large forward)",
                      "launches": gemm_launches, "avg_launch_ms": round(gemm_ms / gemm_launches, 4)},
         "cpu_baseline": cpu,
@@ -278,6 +315,15 @@ def main():
             "pcie_inclusive_tokens_per_s": round(large["pcie_inclusive_tokens_per_s"], 1),
             "large_loss": large["loss"],
             "kernel_classes": breakdown,
+            "train_step": None if not large["train"] else {
+                "workload": "large preset training step B4 T1024: forward + loss + backward "
+                            "+ global norm + clip + AdamW",
+                "ms_per_step": round(large["train"]["ms_per_step"], 2),
+                "tokens_per_s": round(large["train"]["tokens_per_s"], 1),
+                "model_tflops": round(3 * total_flops / (large["train"]["ms_per_step"] / 1000)
+                                      / 1e12, 2),
+                "loss_first_last": [large["train"]["first_loss"], large["train"]["last_loss"]],
+                "grad_norm": large["train"]["grad_norm"]},
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),

@@ -1,7 +1,7 @@
 /*
  * midman_hip.h -- C ABI of libmidman_hip.so, the MI355X (gfx950) implementation
- * of midman-ai's decoder forward + cross-entropy loss and the autograd matmul
- * backward.
+ * of midman-ai's decoder forward + cross-entropy loss, the autograd matmul
+ * backward, the full decoder backward and the clip + AdamW training step.
  *
  * Conventions follow the reference's own C ABI (crates/midman-api/src/ffi.rs:5-32):
  *   - Handles, not pointers, for library objects (contexts, models). A stale or
