@@ -17,10 +17,11 @@
 // and B[k=l/32][j=l%32]; accumulator register r of lane l holds
 // D[i = 8*(r/4) + 4*(l/32) + r%4][j = l%32].
 //
-// K advances 32 at a time through two LDS stages, software-pipelined: while
-// the 64 MFMAs per wave of tile t run, tile t+1 waits in registers and tile
-// t+2's global loads are issued as soon as tile t+1 is in LDS. One barrier per
-// tile. Interior tiles take a path with no
+// K advances 16 at a time through two LDS stages, software-pipelined: at the
+// top of iteration t, tile t+1 moves from registers into the free stage and
+// tile t+2's global loads are issued; then the 32 MFMAs per wave of tile t run
+// while those loads are in flight. One barrier per tile. Interior tiles take a
+// path with no
 // load predicates and 32-bit offsets from uniform base pointers; edge tiles
 // zero-fill outside [M, N, K).
 //
@@ -41,6 +42,10 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int GROUP_M = 8;
+// Raw buffer descriptor: byte range (interior tiles stay below 2^31 bytes from
+// their base, checked on the host) and the gfx9-family dword-3 flags.
+constexpr int kBufferRange = 0x7fffffff;
+constexpr int kBufferFlags = 0x00020000;
 
 struct KParams {
     const float *a;
@@ -105,7 +110,9 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     // k-major operands (A for tn, B for nn/tn): k idx/32, column (idx%32)*4.
     constexpr int NL = BK / 8;
     constexpr int RQ = BK / 4;  // float4 per row of a row-major-in-k tile
-    // Uniform bases (moved by the tile's k) and 32-bit per-thread offsets.
+    // Uniform bases (moved by the tile's k) and loop-invariant 32-bit byte
+    // offsets per thread, so each load is one SGPR base + VGPR offset
+    // instruction with no per-iteration address registers.
     const float *a_base = TA ? A + m0 : A + m0 * p.lda;
     const float *b_base = TB ? B + n0 * p.ldb : B + n0;
     const uint32_t lda = (uint32_t)p.lda, ldb = (uint32_t)p.ldb;
@@ -113,8 +120,10 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
         const int idx = tid + 256 * i;
-        ao[i] = TA ? (uint32_t)(idx >> 5) * lda + (idx & 31) * 4 : (uint32_t)(idx / RQ) * lda + (idx % RQ) * 4;
-        bo[i] = TB ? (uint32_t)(idx / RQ) * ldb + (idx % RQ) * 4 : (uint32_t)(idx >> 5) * ldb + (idx & 31) * 4;
+        ao[i] = 4u * (TA ? (uint32_t)(idx >> 5) * lda + (idx & 31) * 4
+                         : (uint32_t)(idx / RQ) * lda + (idx % RQ) * 4);
+        bo[i] = 4u * (TB ? (uint32_t)(idx / RQ) * ldb + (idx % RQ) * 4
+                         : (uint32_t)(idx >> 5) * ldb + (idx & 31) * 4);
     }
 
     float4 ra[NL], rb[NL];
@@ -167,12 +176,20 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     };
     auto load = [&](int64_t k0) __attribute__((always_inline)) {
         if (FAST) {
+            // Buffer loads: the tile's base in a scalar descriptor, the
+            // per-thread byte offset in one loop-invariant VGPR.
             const float *ak = TA ? a_base + k0 * p.lda : a_base + k0;
             const float *bk = TB ? b_base + k0 : b_base + k0 * p.ldb;
+            const __amdgpu_buffer_rsrc_t rsa = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(ak), (short)0, kBufferRange, kBufferFlags);
+            const __amdgpu_buffer_rsrc_t rsb = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(bk), (short)0, kBufferRange, kBufferFlags);
 #pragma unroll
-            for (int i = 0; i < NL; ++i) ra[i] = *reinterpret_cast<const float4 *>(ak + ao[i]);
+            for (int i = 0; i < NL; ++i)
+                ra[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsa, ao[i], 0, 0));
 #pragma unroll
-            for (int i = 0; i < NL; ++i) rb[i] = *reinterpret_cast<const float4 *>(bk + bo[i]);
+            for (int i = 0; i < NL; ++i)
+                rb[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsb, bo[i], 0, 0));
         } else {
 #pragma unroll
             for (int i = 0; i < NL; ++i) ra[i] = load_a_edge(tid + 256 * i, k0);
@@ -239,10 +256,10 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     };
 
     // Pipeline: stage t%2 holds tile t and the registers hold tile t+1 when
-    // iteration t starts. The MFMAs of tile t run; tile t+1 then goes into the
-    // other stage (last read in iteration t-1, before its barrier), the global
-    // loads of tile t+2 are issued, and one barrier ends the iteration; those
-    // loads land while tile t+1 is being multiplied.
+    // iteration t starts. Tile t+1 first goes into the other stage (last read
+    // in iteration t-1, before its barrier), the global loads of tile t+2 are
+    // issued into the freed registers, and then the MFMAs of tile t run: the
+    // loads have a whole tile of MFMAs to land. One barrier per iteration.
     const int nk = (int)((kend - kbeg + BK - 1) / BK);
     if (nk > 0) {
         load(kbeg);
@@ -252,9 +269,9 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     __syncthreads();
     for (int it = 0; it < nk; ++it) {
         const int cur = it & 1;
-        compute(cur);
         if (it + 1 < nk) store(cur ^ 1);
         if (it + 2 < nk) load(kbeg + (int64_t)(it + 2) * BK);
+        compute(cur);
         __syncthreads();
     }
 }
@@ -456,8 +473,8 @@ void gemm(Context &ctx, const GemmDesc &d) {
     }
     p.tiles_m = (int)((d.m + BM - 1) / BM);
     p.tiles_n = (int)((d.n + BN - 1) / BN);
-    // The interior path addresses a tile with 32-bit offsets (< 128 rows of ld).
-    const int64_t off_limit = int64_t(1) << 31;
+    // The interior path addresses a tile with byte offsets below 2^31 (128 rows of ld).
+    const int64_t off_limit = int64_t(1) << 29;
     p.vec_a = (d.lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(d.a) &&
               d.lda * BM < off_limit;
     p.vec_b = (d.ldb % 4 == 0) && (d.batch == 1 || d.stride_b % 4 == 0) && aligned16(d.b) &&
