@@ -94,7 +94,34 @@ def time_train(mh, m, B, T, steps, warmup):
             "first_loss": rec[0][0], "last_loss": rec[-1][0], "grad_norm": rec[-1][1]}
 
 
-def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0):
+def time_checkpoint(mh, m):
+    """save_parameters / load_parameters of the model's weights between HBM and a
+    safetensors file in the system temp directory (page cache warm after the
+    save), streamed through pinned staging. None when the disk has no room."""
+    import shutil
+    import tempfile
+
+    nbytes = 4 * m.num_parameters()
+    tmp = tempfile.gettempdir()
+    if shutil.disk_usage(tmp).free < 2 * nbytes + (1 << 30):
+        return None
+    path = os.path.join(tmp, f"mmh_bench_{os.getpid()}.safetensors")
+    try:
+        t0 = time.perf_counter()
+        m.save_checkpoint(path, {"step": "0"})
+        t_save = time.perf_counter() - t0
+        size = os.path.getsize(path)
+        t0 = time.perf_counter()
+        m.load_checkpoint(path)
+        t_load = time.perf_counter() - t0
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    return {"file_bytes": size, "save_s": round(t_save, 3), "load_s": round(t_load, 3),
+            "save_gbs": round(size / t_save / 1e9, 2), "load_gbs": round(size / t_load / 1e9, 2)}
+
+
+def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=False):
     cfg = mh.PRESETS[preset]
     t0 = time.time()
     m = mh.Model.new(ctx, cfg, 0)
@@ -117,11 +144,17 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0):
         m.loss(x, y, B, T)
     host_ms = (time.perf_counter() - t1) * 1000 / max(1, steps // 2)
     prof = m.profile(B, T)
+    ckpt = None
+    if checkpoint:
+        try:
+            ckpt = time_checkpoint(mh, m)
+        except (OSError, mh.MidmanError) as e:
+            log(f"checkpoint timing skipped: {e}")
     train = time_train(mh, m, B, T, train_steps, 2) if train_steps else None
     m.close()
     return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
             "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg,
-            "train": train}
+            "train": train, "checkpoint": ckpt}
 
 
 def gemm_sweep(mh, ctx, reps=10):
@@ -214,6 +247,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-tiny", action="store_true")
+    ap.add_argument("--no-checkpoint", action="store_true",
+                    help="skip timing the large model's safetensors save/load")
     ap.add_argument("--train-steps", type=int, default=5,
                     help="large-preset training steps to time after the forward (0: none)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -239,7 +274,12 @@ def main():
             b.free()
         log("copy probe: add over 2^26 floats done")
 
-    large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup, a.train_steps)
+    large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup, a.train_steps,
+                       checkpoint=not a.no_checkpoint)
+    if large["checkpoint"]:
+        ck = large["checkpoint"]
+        log(f"large checkpoint: save {ck['save_s']} s ({ck['save_gbs']} GB/s), "
+            f"load {ck['load_s']} s ({ck['load_gbs']} GB/s)")
     log(f"large: {large['ms_per_step']:.2f} ms/step, {large['tokens_per_s']:.0f} tok/s, "
         f"loss {large['loss']:.5f}")
     if large["train"]:
@@ -315,6 +355,7 @@ def main():
             "pcie_inclusive_tokens_per_s": round(large["pcie_inclusive_tokens_per_s"], 1),
             "large_loss": large["loss"],
             "kernel_classes": breakdown,
+            "checkpoint": large["checkpoint"],
             "train_step": None if not large["train"] else {
                 "workload": "large preset training step B4 T1024: forward + loss + backward "
                             "+ global norm + clip + AdamW",

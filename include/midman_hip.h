@@ -277,6 +277,53 @@ int32_t mmh_model_optimizer_steps(mmh_handle model, uint64_t *out);
 int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
                              uint64_t total_steps, uint64_t step, float *lr_out);
 
+/* ---- Checkpoints: midman-checkpoint (safetensors.rs, params.rs) -----------
+ * TensorFile (safetensors.rs:68-330): named F32 tensors + string metadata,
+ * read with the reference's validation (8-byte length, <= 100 MB header of
+ * restricted JSON, F32 only, offsets tiling the data exactly) and written
+ * byte-identically (tensors sorted by name, __metadata__ first with sorted
+ * keys, serde_json string escapes, header space-padded to a multiple of 8).
+ * Host-only: no device is needed. Names and strings are (pointer, length). */
+int32_t mmh_tensorfile_create(mmh_handle *out);                       /* TensorFile::new */
+int32_t mmh_tensorfile_parse(const uint8_t *bytes, uint64_t len, mmh_handle *out); /* from_bytes */
+/* TensorFile::push: copies the values; the name must be new and not __metadata__. */
+int32_t mmh_tensorfile_push(mmh_handle tf, const char *name, uint32_t name_len,
+                            const uint64_t *shape, int32_t rank, const float *data, uint64_t n);
+int32_t mmh_tensorfile_set_metadata(mmh_handle tf, const char *key, uint32_t key_len,
+                                    const char *value, uint32_t value_len);
+int32_t mmh_tensorfile_count(mmh_handle tf, int64_t *n_tensors, int64_t *n_metadata);
+/* Tensor i (insertion order, or file order for a parsed file). */
+int32_t mmh_tensorfile_tensor(mmh_handle tf, int64_t i, char *name, uint32_t name_cap,
+                              uint32_t *name_len, int32_t *rank, uint64_t *shape,
+                              int32_t shape_cap, uint64_t *numel);
+int32_t mmh_tensorfile_read(mmh_handle tf, int64_t i, float *out, uint64_t n);
+/* Metadata entry i in key order. */
+int32_t mmh_tensorfile_metadata(mmh_handle tf, int64_t i, char *key, uint32_t key_cap,
+                                uint32_t *key_len, char *value, uint32_t value_cap,
+                                uint32_t *value_len);
+/* TensorFile::to_bytes; out may be NULL to learn *len. */
+int32_t mmh_tensorfile_serialize(mmh_handle tf, uint8_t *out, uint64_t cap, uint64_t *len);
+int32_t mmh_tensorfile_destroy(mmh_handle tf);
+
+/* save_parameters (params.rs:36-80, safetensors.rs:220-250) from the device:
+ * one tensor per parameter under the reference's names (embed_tokens.weight,
+ * blocks.{i}.attn_norm.weight, blocks.{i}.attn.{q,k,v,o}_proj.weight,
+ * blocks.{i}.mlp_norm.weight, blocks.{i}.mlp.{gate,up,down}_proj.weight,
+ * final_norm.weight, lm_head.weight), metadata format = "midman-checkpoint",
+ * checkpoint_version = "1" plus the caller's pairs (those two keys are
+ * reserved). The bytes stream device -> pinned staging -> <path>.tmp, which is
+ * flushed and renamed over path. The file is byte-identical to the reference
+ * writer's for the same weights. */
+int32_t mmh_model_save_checkpoint(mmh_handle model, const char *path, const char *const *keys,
+                                  const char *const *values, int64_t n_metadata);
+/* check_header + load_parameters (params.rs:82-210) straight into HBM: strict
+ * (every parameter with its shape, nothing else, format and version checked)
+ * and all or nothing (the old weights stay unless the whole file was read). */
+int32_t mmh_model_load_checkpoint(mmh_handle model, const char *path);
+/* A model built from a checkpoint file (config as mmh_model_create). */
+int32_t mmh_model_create_from_checkpoint(mmh_handle ctx, const double config[10],
+                                         const char *path, mmh_handle *out_model);
+
 #ifdef __cplusplus
 }
 #endif

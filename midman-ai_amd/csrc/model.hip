@@ -34,6 +34,7 @@
 #include <cstring>
 #include <mutex>
 
+#include "mmh_checkpoint.h"
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -1178,6 +1179,85 @@ int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
                 (double)(step - warmup_steps) / (double)(total_steps - warmup_steps);
             *lr_out = (float)(mn + 0.5 * (mx - mn) * (1.0 + std::cos(M_PI * progress)));
         }
+        return MMH_OK;
+    });
+}
+
+// ---- checkpoints (midman-checkpoint params.rs) ----------------------------------
+
+namespace {
+
+std::vector<ParamSpec> specs_of(const Model &m) {
+    const Config &c = m.cfg;
+    return model_param_specs(c.vocab, c.d, c.layers, c.kv(), c.ff, c.tie);
+}
+
+// The new weights arrive in a separate buffer and replace the old ones only when
+// the whole file has been read (params.rs:126: nothing changes on failure).
+void load_into(Model &m, const std::string &path) {
+    float *fresh = nullptr;
+    check_hip(hipMalloc(&fresh, (size_t)m.n_params * 4), "checkpoint staging alloc");
+    try {
+        load_checkpoint(*m.ctx, specs_of(m), m.n_params, path, fresh, nullptr);
+    } catch (...) {
+        (void)hipFree(fresh);
+        throw;
+    }
+    check_hip(hipMemcpyAsync(m.w, fresh, (size_t)m.n_params * 4, hipMemcpyDeviceToDevice,
+                             m.ctx->stream),
+              "checkpoint swap");
+    check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint swap sync");
+    (void)hipFree(fresh);
+}
+
+}  // namespace
+
+int32_t mmh_model_save_checkpoint(mmh_handle model_h, const char *path, const char *const *keys,
+                                  const char *const *values, int64_t n_metadata) {
+    return guard([&] {
+        Model &m = model(model_h);
+        if (!path) fail(MMH_ERR_ARGUMENT, "path is a null pointer");
+        if (n_metadata < 0 || (n_metadata > 0 && (!keys || !values)))
+            fail(MMH_ERR_ARGUMENT, "metadata arrays are null");
+        std::map<std::string, std::string> meta;
+        for (int64_t i = 0; i < n_metadata; ++i) {
+            if (!keys[i] || !values[i]) fail(MMH_ERR_ARGUMENT, "a metadata string is null");
+            meta[keys[i]] = values[i];
+        }
+        m.ctx->select();
+        check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint sync");
+        save_checkpoint(*m.ctx, m.w, specs_of(m), meta, path);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_load_checkpoint(mmh_handle model_h, const char *path) {
+    return guard([&] {
+        Model &m = model(model_h);
+        if (!path) fail(MMH_ERR_ARGUMENT, "path is a null pointer");
+        m.ctx->select();
+        check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint sync");
+        load_into(m, path);
+        m.repack();
+        check_hip(hipStreamSynchronize(m.ctx->stream), "repack sync");
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_create_from_checkpoint(mmh_handle ctx, const double config[10],
+                                         const char *path, mmh_handle *out_model) {
+    return guard([&] {
+        if (!out_model) fail(MMH_ERR_ARGUMENT, "out_model is a null pointer");
+        if (!path) fail(MMH_ERR_ARGUMENT, "path is a null pointer");
+        auto m = new_model(ctx, config);
+        try {
+            load_checkpoint(*m->ctx, specs_of(*m), m->n_params, path, m->w, nullptr);
+        } catch (...) {
+            m->release();
+            throw;
+        }
+        m->pack();
+        *out_model = register_model(std::move(m));
         return MMH_OK;
     });
 }

@@ -120,6 +120,29 @@ _SIGNATURES = {
     "mmh_apply_rope_backward": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "mmh_causal_attention_backward": [_h, _vp, _vp, _vp, _vp] + [_i64] * 5 + [_vp] * 3,
     "mmh_cross_entropy_backward": [_h, _vp, _i32p, _i64, _i64, _vp, _f32p],
+    "mmh_tensorfile_create": [ctypes.POINTER(_h)],
+    "mmh_tensorfile_parse": [ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(_h)],
+    "mmh_tensorfile_push": [_h, ctypes.c_char_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64),
+                            ctypes.c_int32, _f32p, ctypes.c_uint64],
+    "mmh_tensorfile_set_metadata": [_h, ctypes.c_char_p, ctypes.c_uint32, ctypes.c_char_p,
+                                    ctypes.c_uint32],
+    "mmh_tensorfile_count": [_h, ctypes.POINTER(_i64), ctypes.POINTER(_i64)],
+    "mmh_tensorfile_tensor": [_h, _i64, ctypes.c_char_p, ctypes.c_uint32,
+                              ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_int32),
+                              ctypes.POINTER(ctypes.c_uint64), ctypes.c_int32,
+                              ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_tensorfile_read": [_h, _i64, _f32p, ctypes.c_uint64],
+    "mmh_tensorfile_metadata": [_h, _i64, ctypes.c_char_p, ctypes.c_uint32,
+                                ctypes.POINTER(ctypes.c_uint32), ctypes.c_char_p,
+                                ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32)],
+    "mmh_tensorfile_serialize": [_h, ctypes.c_char_p, ctypes.c_uint64,
+                                 ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_tensorfile_destroy": [_h],
+    "mmh_model_save_checkpoint": [_h, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p),
+                                  ctypes.POINTER(ctypes.c_char_p), _i64],
+    "mmh_model_load_checkpoint": [_h, ctypes.c_char_p],
+    "mmh_model_create_from_checkpoint": [_h, ctypes.POINTER(ctypes.c_double), ctypes.c_char_p,
+                                         ctypes.POINTER(_h)],
     "mmh_model_backward": [_h, _i32p, _i32p, _i64, _i64, _f32p],
     "mmh_model_download_grads": [_h, _f32p, _i64],
     "mmh_model_grad_norm": [_h, _f32p],
@@ -481,6 +504,113 @@ def cross_entropy_backward(ctx: Context, logits: DeviceArray, targets: np.ndarra
     return loss.value, out
 
 
+# ---- checkpoints: midman-checkpoint ----------------------------------------------------
+
+class TensorFile:
+    """midman-checkpoint's TensorFile (safetensors.rs:68-330) in the library:
+    named f32 tensors plus string metadata, parsed with the reference's checks
+    and serialized to the reference's exact bytes. Host-only."""
+
+    def __init__(self, handle: Optional[int] = None):
+        if handle is None:
+            h = _h()
+            check(lib().mmh_tensorfile_create(ctypes.byref(h)))
+            handle = h.value
+        self.handle = handle
+
+    @classmethod
+    def from_bytes(cls, data: bytes) -> "TensorFile":
+        h = _h()
+        check(lib().mmh_tensorfile_parse(data, len(data), ctypes.byref(h)))
+        return cls(h.value)
+
+    @classmethod
+    def load(cls, path: str) -> "TensorFile":
+        with open(path, "rb") as f:
+            return cls.from_bytes(f.read())
+
+    def push(self, name: str, shape, data):
+        nb = name.encode("utf-8")
+        shape = [int(s) for s in shape]
+        sh = (ctypes.c_uint64 * max(1, len(shape)))(*shape)
+        arr = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
+        check(lib().mmh_tensorfile_push(self.handle, nb, len(nb), sh, len(shape), _fp(arr),
+                                        arr.size))
+
+    def set_metadata(self, key: str, value: str):
+        kb, vb = key.encode("utf-8"), value.encode("utf-8")
+        check(lib().mmh_tensorfile_set_metadata(self.handle, kb, len(kb), vb, len(vb)))
+
+    def _counts(self):
+        nt, nm = _i64(), _i64()
+        check(lib().mmh_tensorfile_count(self.handle, ctypes.byref(nt), ctypes.byref(nm)))
+        return nt.value, nm.value
+
+    def tensors(self):
+        """[(name, shape, values)] in file (or insertion) order."""
+        out = []
+        for i in range(self._counts()[0]):
+            nl, rank, numel = ctypes.c_uint32(), ctypes.c_int32(), ctypes.c_uint64()
+            check(lib().mmh_tensorfile_tensor(self.handle, i, None, 0, ctypes.byref(nl), None,
+                                              None, 0, None))
+            name = ctypes.create_string_buffer(max(1, nl.value))
+            shape = (ctypes.c_uint64 * 16)()
+            check(lib().mmh_tensorfile_tensor(self.handle, i, name, nl.value, ctypes.byref(nl),
+                                              ctypes.byref(rank), shape, 16,
+                                              ctypes.byref(numel)))
+            vals = np.empty(numel.value, np.float32)
+            check(lib().mmh_tensorfile_read(self.handle, i, _fp(vals), numel.value))
+            out.append((name.raw[: nl.value].decode("utf-8"), [shape[k] for k in range(rank.value)],
+                        vals))
+        return out
+
+    def metadata(self) -> dict:
+        out = {}
+        for i in range(self._counts()[1]):
+            kl, vl = ctypes.c_uint32(), ctypes.c_uint32()
+            check(lib().mmh_tensorfile_metadata(self.handle, i, None, 0, ctypes.byref(kl), None,
+                                                0, ctypes.byref(vl)))
+            k = ctypes.create_string_buffer(max(1, kl.value))
+            v = ctypes.create_string_buffer(max(1, vl.value))
+            check(lib().mmh_tensorfile_metadata(self.handle, i, k, kl.value, ctypes.byref(kl), v,
+                                                vl.value, ctypes.byref(vl)))
+            out[k.raw[: kl.value].decode("utf-8")] = v.raw[: vl.value].decode("utf-8")
+        return out
+
+    def to_bytes(self) -> bytes:
+        n = ctypes.c_uint64()
+        check(lib().mmh_tensorfile_serialize(self.handle, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(1, n.value))
+        check(lib().mmh_tensorfile_serialize(self.handle, buf, n.value, ctypes.byref(n)))
+        return buf.raw[: n.value]
+
+    def close(self):
+        if self.handle:
+            check(lib().mmh_tensorfile_destroy(self.handle))
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+
+def parameter_names(config) -> list:
+    """The reference's parameter names in Module order (docs/midman-model.md:20)."""
+    L, tie = int(config[2]), bool(config[9])
+    names = ["embed_tokens.weight"]
+    for i in range(L):
+        b = f"blocks.{i}."
+        names += [b + "attn_norm.weight", b + "attn.q_proj.weight", b + "attn.k_proj.weight",
+                  b + "attn.v_proj.weight", b + "attn.o_proj.weight", b + "mlp_norm.weight",
+                  b + "mlp.gate_proj.weight", b + "mlp.up_proj.weight", b + "mlp.down_proj.weight"]
+    names.append("final_norm.weight")
+    if not tie:
+        names.append("lm_head.weight")
+    return names
+
+
 # ---- the model: midman-model/src/model.rs ------------------------------------------
 
 CONFIG_FIELDS = ("vocab_size", "d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff",
@@ -596,6 +726,25 @@ class Model:
         cnt = (ctypes.c_int32 * n)()
         check(lib().mmh_model_profile(self.handle, batch, seq, ms, cnt))
         return {name: (ms[i], cnt[i]) for i, name in enumerate(PROFILE_CLASSES)}
+
+    # ---- checkpoints -------------------------------------------------------
+    @classmethod
+    def from_checkpoint(cls, ctx: Context, config, path: str) -> "Model":
+        h = _h()
+        check(lib().mmh_model_create_from_checkpoint(ctx.handle, _config_array(config),
+                                                     path.encode(), ctypes.byref(h)))
+        return cls(ctx, h.value, config)
+
+    def save_checkpoint(self, path: str, metadata: Optional[dict] = None):
+        """save_parameters (params.rs:36-80) straight from HBM."""
+        items = sorted((metadata or {}).items())
+        keys = (ctypes.c_char_p * max(1, len(items)))(*[k.encode() for k, _ in items])
+        vals = (ctypes.c_char_p * max(1, len(items)))(*[v.encode() for _, v in items])
+        check(lib().mmh_model_save_checkpoint(self.handle, path.encode(), keys, vals, len(items)))
+
+    def load_checkpoint(self, path: str):
+        """load_parameters (params.rs:82-210) straight into HBM; all or nothing."""
+        check(lib().mmh_model_load_checkpoint(self.handle, path.encode()))
 
     # ---- training ---------------------------------------------------------
     def backward(self, inputs, targets, batch: int, seq: int) -> float:
