@@ -121,7 +121,64 @@ def time_checkpoint(mh, m):
             "save_gbs": round(size / t_save / 1e9, 2), "load_gbs": round(size / t_load / 1e9, 2)}
 
 
-def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=False):
+def time_data(mh, m, B, T, steps, shards=4, shard_tokens=1 << 22, eval_batches=8):
+    """Training and evaluation fed from token shards (Trainer::step /
+    Trainer::evaluate): synthetic uniform ids written as shard files in the
+    system temp directory, loaded back (read + SHA-256 + id checks), cut into
+    sequences of T and batched by the seeded batcher. None when the disk has
+    no room."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    vocab = int(m.config[0])
+    tmp = tempfile.gettempdir()
+    if shutil.disk_usage(tmp).free < shards * shard_tokens * 4 + (1 << 30):
+        return None
+    r = np.random.default_rng(0)
+    paths = [os.path.join(tmp, f"mmh_bench_{os.getpid()}_{n:05}.mmtokens") for n in range(shards)]
+    try:
+        for p in paths:
+            mh.TokenShard(vocab, vocab - 1, r.integers(0, vocab, shard_tokens)).save(p)
+        nbytes = sum(os.path.getsize(p) for p in paths)
+        t0 = time.perf_counter()
+        loaded = [mh.TokenShard.load(p) for p in paths]
+        t_load = time.perf_counter() - t0
+    finally:
+        for p in paths:
+            if os.path.exists(p):
+                os.remove(p)
+    data = mh.Sequences(loaded, T)
+    batcher = mh.Batcher(data, B, 1)
+    probe = mh.Batcher(data, B, 1)
+    t0 = time.perf_counter()
+    for _ in range(64):
+        probe.next_batch()
+    batch_us = (time.perf_counter() - t0) * 1e6 / 64
+    m.set_optimizer(0.9, 0.95, 1e-8, 0.1, 1.0)
+    m.train_next(batcher, 1e-4)  # warm-up: index buffers at this size
+    rec = []
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        rec.append(m.train_next(batcher, 1e-4))
+    train_ms = (time.perf_counter() - t0) * 1000 / steps
+    t0 = time.perf_counter()
+    loss, nb, ntok = m.evaluate(data, B, eval_batches)
+    t_eval = time.perf_counter() - t0
+    return {"shards": shards, "tokens": shards * shard_tokens, "sequences": len(data),
+            "file_bytes": nbytes, "load_s": round(t_load, 3),
+            "load_gbs": round(nbytes / t_load / 1e9, 3),
+            "batch_assembly_us": round(batch_us, 1),
+            "train_ms_per_step": round(train_ms, 2),
+            "train_tokens_per_s": round(B * T / (train_ms / 1000), 1),
+            "train_loss_first_last": [rec[0][0], rec[-1][0]],
+            "eval_batches": nb, "eval_tokens": ntok, "eval_loss": loss,
+            "eval_tokens_per_s": round(ntok / t_eval, 1)}
+
+
+def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=False,
+               shards=False):
     cfg = mh.PRESETS[preset]
     t0 = time.time()
     m = mh.Model.new(ctx, cfg, 0)
@@ -151,10 +208,16 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
         except (OSError, mh.MidmanError) as e:
             log(f"checkpoint timing skipped: {e}")
     train = time_train(mh, m, B, T, train_steps, 2) if train_steps else None
+    data = None
+    if train_steps and shards:
+        try:
+            data = time_data(mh, m, B, T, train_steps)
+        except (OSError, mh.MidmanError) as e:
+            log(f"shard-fed timing skipped: {e}")
     m.close()
     return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
             "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg,
-            "train": train, "checkpoint": ckpt}
+            "train": train, "checkpoint": ckpt, "data": data}
 
 
 def gemm_sweep(mh, ctx, reps=10):
@@ -249,6 +312,8 @@ def main():
     ap.add_argument("--no-tiny", action="store_true")
     ap.add_argument("--no-checkpoint", action="store_true",
                     help="skip timing the large model's safetensors save/load")
+    ap.add_argument("--no-shards", action="store_true",
+                    help="skip timing training and evaluation fed from token shard files")
     ap.add_argument("--train-steps", type=int, default=5,
                     help="large-preset training steps to time after the forward (0: none)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -275,7 +340,7 @@ def main():
         log("copy probe: add over 2^26 floats done")
 
     large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup, a.train_steps,
-                       checkpoint=not a.no_checkpoint)
+                       checkpoint=not a.no_checkpoint, shards=not a.no_shards)
     if large["checkpoint"]:
         ck = large["checkpoint"]
         log(f"large checkpoint: save {ck['save_s']} s ({ck['save_gbs']} GB/s), "
@@ -286,6 +351,11 @@ def main():
         tr = large["train"]
         log(f"large train step: {tr['ms_per_step']:.1f} ms, {tr['tokens_per_s']:.0f} tok/s, "
             f"loss {tr['first_loss']:.4f} -> {tr['last_loss']:.4f}")
+    if large["data"]:
+        dd = large["data"]
+        log(f"large from shards: load {dd['load_gbs']} GB/s, batch {dd['batch_assembly_us']} us, "
+            f"train {dd['train_ms_per_step']} ms/step ({dd['train_tokens_per_s']:.0f} tok/s), "
+            f"eval {dd['eval_tokens_per_s']:.0f} tok/s")
     tiny = None
     if not a.no_tiny:
         tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5))
@@ -365,6 +435,10 @@ def main():
                                       / 1e12, 2),
                 "loss_first_last": [large["train"]["first_loss"], large["train"]["last_loss"]],
                 "grad_norm": large["train"]["grad_norm"]},
+            "from_shards": None if not large["data"] else dict(
+                workload="large preset B4 T1024 trained (Trainer::step) and evaluated "
+                         "(Trainer::evaluate) from token shard files through the seeded "
+                         "batcher; synthetic uniform ids", **large["data"]),
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),

@@ -324,6 +324,84 @@ int32_t mmh_model_load_checkpoint(mmh_handle model, const char *path);
 int32_t mmh_model_create_from_checkpoint(mmh_handle ctx, const double config[10],
                                          const char *path, mmh_handle *out_model);
 
+/* ---- Training data: midman-data (hash.rs, shard.rs, batch.rs) -------------
+ * Host-only except the two model entry points at the end. Errors carry the
+ * reference's messages: MMH_ERR_ARGUMENT for Error::InvalidArgument,
+ * MMH_ERR_OTHER for Error::Parse, Error::UnsupportedVersion and Error::Io.
+ * A batcher is not safe to use from two threads at once. */
+
+/* sha256 (hash.rs) of len bytes into digest[32]. */
+int32_t mmh_sha256(const uint8_t *data, uint64_t len, uint8_t *digest);
+/* Sha256::new / update / finalize (hash.rs); finalize frees the handle. */
+int32_t mmh_sha256_new(mmh_handle *out);
+int32_t mmh_sha256_update(mmh_handle hasher, const uint8_t *data, uint64_t len);
+int32_t mmh_sha256_finalize(mmh_handle hasher, uint8_t *digest);
+/* The compression path (no reference counterpart): mode 0 = the best the CPU
+ * has, 1 = portable, 2 = the x86 SHA extensions if present; *in_use = 1 or 2. */
+int32_t mmh_sha256_select(int32_t mode, int32_t *in_use);
+
+/* TokenShard::new (shard.rs:66-83): copies the n tokens. */
+int32_t mmh_shard_create(uint32_t vocab_size, uint32_t eos, const uint32_t *tokens, uint64_t n,
+                         mmh_handle *out);
+/* TokenShard::from_bytes (shard.rs:146-223): magic, version, the width for
+ * the vocabulary, eos, the exact length, the SHA-256 and every id checked. */
+int32_t mmh_shard_parse(const uint8_t *bytes, uint64_t len, mmh_handle *out);
+/* TokenShard::load / save (shard.rs:233-260); save writes <path>.tmp, fsyncs
+ * it and renames it over path. */
+int32_t mmh_shard_load(const char *path, mmh_handle *out);
+int32_t mmh_shard_save(mmh_handle shard, const char *path);
+/* vocab_size, eos, len, token_width (shard.rs:86-115) and the file size; any
+ * output may be NULL. */
+int32_t mmh_shard_info(mmh_handle shard, uint32_t *vocab_size, uint32_t *eos, uint64_t *len,
+                       uint32_t *token_width, uint64_t *file_bytes);
+/* TokenShard::tokens: n must be the shard's length. */
+int32_t mmh_shard_tokens(mmh_handle shard, uint32_t *out, uint64_t n);
+/* TokenShard::to_bytes (shard.rs:112-135); out may be NULL to learn *len. */
+int32_t mmh_shard_serialize(mmh_handle shard, uint8_t *out, uint64_t cap, uint64_t *len);
+int32_t mmh_shard_destroy(mmh_handle shard);
+
+/* Sequences::new (batch.rs:45-70) over n_shards shard handles (the shards are
+ * shared, not copied; destroying a shard handle later is fine). */
+int32_t mmh_sequences_create(const mmh_handle *shards, int64_t n_shards, uint64_t seq_len,
+                             mmh_handle *out);
+/* len, seq_len, vocab_size (-1 with no shards) (batch.rs:73-93). */
+int32_t mmh_sequences_info(mmh_handle seqs, uint64_t *len, uint64_t *seq_len,
+                           int64_t *vocab_size);
+/* Sequences::window (batch.rs:96-104): seq_len + 1 ids into out;
+ * MMH_ERR_INDEX where the reference returns None. */
+int32_t mmh_sequences_window(mmh_handle seqs, uint64_t index, uint32_t *out);
+int32_t mmh_sequences_destroy(mmh_handle seqs);
+
+/* Batcher::new (batch.rs:161-172). */
+int32_t mmh_batcher_create(mmh_handle seqs, uint64_t batch_size, uint64_t seed,
+                           mmh_handle *out);
+/* batches_per_epoch, epoch, position (batch.rs:175-190), batch size and
+ * seq_len; any output may be NULL. */
+int32_t mmh_batcher_info(mmh_handle batcher, uint64_t *batches_per_epoch, uint64_t *epoch,
+                         uint64_t *position, uint64_t *batch_size, uint64_t *seq_len);
+/* Batcher::seek (batch.rs:196-208). */
+int32_t mmh_batcher_seek(mmh_handle batcher, uint64_t epoch, uint64_t batches_done);
+/* Batcher::next_batch (batch.rs:211-239): batch_size * seq_len inputs and
+ * targets, row after row; the batch's epoch and index (either may be NULL). */
+int32_t mmh_batcher_next(mmh_handle batcher, uint32_t *inputs, uint32_t *targets,
+                         uint64_t *epoch, uint64_t *index);
+int32_t mmh_batcher_destroy(mmh_handle batcher);
+
+/* Trainer::step (trainer.rs:162-183) at learning rate lr: the batcher's next
+ * batch through mmh_model_train_step. The data must fit the model (Trainer::new,
+ * trainer.rs:83-108: seq_len <= max_seq_len, the same vocabulary). A step that
+ * fails (MMH_STOPPED for a non-finite loss or norm, or any error) changes
+ * nothing and puts the batcher back where it was. epoch and index report the
+ * batch used (either may be NULL). */
+int32_t mmh_model_train_next(mmh_handle model, mmh_handle batcher, float lr, float *loss_host,
+                             float *grad_norm_host, uint64_t *epoch, uint64_t *index);
+/* Trainer::evaluate (trainer.rs:218-258): at most max_batches batches of
+ * min(batch_size, len) sequences, row k of all rows being sequence
+ * k * len / rows; the mean of the batch losses (f64 sum). */
+int32_t mmh_model_evaluate(mmh_handle model, mmh_handle seqs, uint64_t batch_size,
+                           uint64_t max_batches, float *loss_host, uint64_t *batches,
+                           uint64_t *tokens);
+
 #ifdef __cplusplus
 }
 #endif

@@ -93,6 +93,10 @@ uint64_t HostRng::below(uint64_t n) {  // rng.rs:91-105
     return (uint64_t)(product >> 64);
 }
 
+HostRng HostRng::fork(uint64_t stream) {  // rng.rs:117-119
+    return HostRng::seed(next_u64() ^ (stream * 0x9E3779B97F4A7C15ull));
+}
+
 // The stream of pairs is generated sequentially in chunks (xoshiro is cheap);
 // the transcendental work of each chunk is split over threads. Pair i's two
 // draws and its position in dst are fixed by i alone, so the bits equal the

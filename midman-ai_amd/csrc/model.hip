@@ -35,6 +35,7 @@
 #include <mutex>
 
 #include "mmh_checkpoint.h"
+#include "mmh_data.h"
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -1147,6 +1148,99 @@ int32_t mmh_model_train_step(mmh_handle model_h, const int32_t *inputs_host,
     const int32_t st = mmh_model_stage_train(model_h, inputs_host, targets_host, batch, seq);
     if (st != MMH_OK) return st;
     return mmh_model_train_staged(model_h, batch, seq, lr, loss_host, grad_norm_host);
+}
+
+namespace {
+
+// The checks Trainer::new and Trainer::evaluate make between the data and the
+// model (trainer.rs:83-108, :218-235).
+void check_data_for(const Model &m, const Sequences &q) {
+    if (q.seq_len > (uint64_t)m.cfg.max_seq)
+        fail(MMH_ERR_ARGUMENT, "invalid argument: sequences of " + std::to_string(q.seq_len) +
+                                   " tokens are longer than the model's " +
+                                   std::to_string(m.cfg.max_seq));
+    if (q.vocab() < 0) fail(MMH_ERR_ARGUMENT, "invalid argument: the data has no tokens");
+    if (q.vocab() != m.cfg.vocab)
+        fail(MMH_ERR_ARGUMENT, "invalid argument: the data has a vocabulary of " +
+                                   std::to_string(q.vocab()) + " and the model " +
+                                   std::to_string(m.cfg.vocab));
+    if (m.cfg.vocab > INT32_MAX) fail(MMH_ERR_ARGUMENT, "the vocabulary does not fit int32 ids");
+}
+
+}  // namespace
+
+int32_t mmh_model_train_next(mmh_handle model_h, mmh_handle batcher_h, float lr,
+                             float *loss_host, float *grad_norm_host, uint64_t *epoch,
+                             uint64_t *index) {
+    return guard([&] {
+        Model &m = model(model_h);
+        Batcher &b = batcher_of(batcher_h);
+        check_data_for(m, *b.data);
+        const int64_t batch = (int64_t)b.batch, seq = (int64_t)b.data->seq_len;
+        std::vector<uint32_t> in((size_t)(batch * seq)), tg((size_t)(batch * seq));
+        const uint64_t e0 = b.epoch, p0 = b.position;  // trainer.rs:163
+        uint64_t e = 0, i = 0;
+        b.next_batch(in.data(), tg.data(), &e, &i);
+        try {
+            // every id is below the vocabulary, which fits int32
+            m.stage_train(reinterpret_cast<const int32_t *>(in.data()),
+                          reinterpret_cast<const int32_t *>(tg.data()), batch, seq);
+            float l = 0.0f, g = 0.0f;
+            const bool ok = m.train_staged(batch, seq, lr, &l, &g);
+            if (loss_host) *loss_host = l;
+            if (grad_norm_host) *grad_norm_host = g;
+            if (!ok) {
+                if (!std::isfinite(l))
+                    fail(MMH_STOPPED, "the loss is " + std::to_string(l) +
+                                          ", not a finite number");
+                fail(MMH_STOPPED, "clip: the gradient norm is not finite");
+            }
+        } catch (...) {
+            b.seek(e0, p0);  // trainer.rs:177-181: the batcher goes back
+            throw;
+        }
+        if (epoch) *epoch = e;
+        if (index) *index = i;
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_evaluate(mmh_handle model_h, mmh_handle sequences_h, uint64_t batch_size,
+                           uint64_t max_batches, float *loss_host, uint64_t *batches_out,
+                           uint64_t *tokens_out) {
+    return guard([&] {
+        if (!loss_host) fail(MMH_ERR_ARGUMENT, "loss is a null pointer");
+        Model &m = model(model_h);
+        std::shared_ptr<const Sequences> q = sequences_of(sequences_h);
+        check_data_for(m, *q);
+        if (batch_size == 0) fail(MMH_ERR_ARGUMENT, "invalid argument: the batch size is 0");
+        if (max_batches == 0 || q->len() == 0)
+            fail(MMH_ERR_ARGUMENT, "invalid argument: nothing to evaluate");
+        // trainer.rs:236-257: batches of the run's size (or all there is),
+        // row k of `rows` is sequence k * len / rows, the mean of the losses.
+        const uint64_t len = q->len(), seq = q->seq_len;
+        const uint64_t batch = std::min(batch_size, len);
+        const uint64_t batches = std::min(max_batches, len / batch);
+        const uint64_t rows = batches * batch;
+        std::vector<int32_t> in((size_t)(batch * seq)), tg((size_t)(batch * seq));
+        double total = 0.0;
+        for (uint64_t bi = 0; bi < batches; ++bi) {
+            for (uint64_t r = 0; r < batch; ++r) {
+                const uint64_t at =
+                    (uint64_t)((unsigned __int128)(bi * batch + r) * len / rows);
+                const uint32_t *w = q->window(at);
+                std::memcpy(&in[(size_t)(r * seq)], w, (size_t)seq * 4);
+                std::memcpy(&tg[(size_t)(r * seq)], w + 1, (size_t)seq * 4);
+            }
+            float l = 0.0f;
+            m.run(in.data(), tg.data(), (int64_t)batch, (int64_t)seq, nullptr, &l);
+            total += (double)l;
+        }
+        *loss_host = (float)(total / (double)batches);
+        if (batches_out) *batches_out = batches;
+        if (tokens_out) *tokens_out = rows * seq;
+        return MMH_OK;
+    });
 }
 
 int32_t mmh_model_optimizer_steps(mmh_handle model_h, uint64_t *out) {

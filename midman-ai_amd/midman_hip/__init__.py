@@ -66,6 +66,7 @@ _ERRORS = {ERR_ARGUMENT: ArgumentError, ERR_CONFIG: ConfigError, ERR_SHAPE: Shap
 
 _f32p = ctypes.POINTER(ctypes.c_float)
 _i32p = ctypes.POINTER(ctypes.c_int32)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 _vp = ctypes.c_void_p
 _h = ctypes.c_int64
 _i64 = ctypes.c_int64
@@ -153,6 +154,37 @@ _SIGNATURES = {
     "mmh_model_optimizer_steps": [_h, ctypes.POINTER(ctypes.c_uint64)],
     "mmh_warmup_cosine_lr": [ctypes.c_float, ctypes.c_float, ctypes.c_uint64, ctypes.c_uint64,
                              ctypes.c_uint64, _f32p],
+    "mmh_sha256": [ctypes.c_char_p, ctypes.c_uint64, ctypes.c_char_p],
+    "mmh_sha256_new": [ctypes.POINTER(_h)],
+    "mmh_sha256_update": [_h, ctypes.c_char_p, ctypes.c_uint64],
+    "mmh_sha256_finalize": [_h, ctypes.c_char_p],
+    "mmh_sha256_select": [_i32, ctypes.POINTER(_i32)],
+    "mmh_shard_create": [ctypes.c_uint32, ctypes.c_uint32, _u32p, ctypes.c_uint64,
+                         ctypes.POINTER(_h)],
+    "mmh_shard_parse": [ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(_h)],
+    "mmh_shard_load": [ctypes.c_char_p, ctypes.POINTER(_h)],
+    "mmh_shard_save": [_h, ctypes.c_char_p],
+    "mmh_shard_info": [_h, ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint32),
+                       ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint32),
+                       ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_shard_tokens": [_h, _u32p, ctypes.c_uint64],
+    "mmh_shard_serialize": [_h, ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_shard_destroy": [_h],
+    "mmh_sequences_create": [ctypes.POINTER(_h), _i64, ctypes.c_uint64, ctypes.POINTER(_h)],
+    "mmh_sequences_info": [_h, ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64),
+                           ctypes.POINTER(_i64)],
+    "mmh_sequences_window": [_h, ctypes.c_uint64, _u32p],
+    "mmh_sequences_destroy": [_h],
+    "mmh_batcher_create": [_h, ctypes.c_uint64, ctypes.c_uint64, ctypes.POINTER(_h)],
+    "mmh_batcher_info": [_h] + [ctypes.POINTER(ctypes.c_uint64)] * 5,
+    "mmh_batcher_seek": [_h, ctypes.c_uint64, ctypes.c_uint64],
+    "mmh_batcher_next": [_h, _u32p, _u32p, ctypes.POINTER(ctypes.c_uint64),
+                         ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_batcher_destroy": [_h],
+    "mmh_model_train_next": [_h, _h, ctypes.c_float, _f32p, _f32p,
+                             ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
+    "mmh_model_evaluate": [_h, _h, ctypes.c_uint64, ctypes.c_uint64, _f32p,
+                           ctypes.POINTER(ctypes.c_uint64), ctypes.POINTER(ctypes.c_uint64)],
 }
 
 PROFILE_CLASSES = ("embedding", "rms_norm", "gemm_qkv", "gemm_o", "gemm_gate_up", "gemm_down",
@@ -611,6 +643,227 @@ def parameter_names(config) -> list:
     return names
 
 
+# ---- training data: midman-data (hash.rs, shard.rs, batch.rs) -------------------------
+
+def sha256(data: bytes) -> bytes:
+    """midman-data's sha256 (hash.rs)."""
+    out = ctypes.create_string_buffer(32)
+    check(lib().mmh_sha256(data, len(data), out))
+    return out.raw
+
+
+def sha256_select(mode: int) -> int:
+    """The compression path: 0 best available, 1 portable, 2 x86 SHA
+    extensions if present. Returns the path in use (1 or 2)."""
+    v = ctypes.c_int32()
+    check(lib().mmh_sha256_select(mode, ctypes.byref(v)))
+    return v.value
+
+
+class Sha256:
+    """Sha256::new / update / finalize (hash.rs)."""
+
+    def __init__(self):
+        h = _h()
+        check(lib().mmh_sha256_new(ctypes.byref(h)))
+        self.handle = h.value
+
+    def update(self, data: bytes):
+        check(lib().mmh_sha256_update(self.handle, data, len(data)))
+
+    def finalize(self) -> bytes:
+        out = ctypes.create_string_buffer(32)
+        check(lib().mmh_sha256_finalize(self.handle, out))
+        self.handle = 0
+        return out.raw
+
+
+class _Handle:
+    _destroy = ""
+
+    def close(self):
+        if getattr(self, "handle", 0):
+            check(getattr(lib(), self._destroy)(self.handle))
+            self.handle = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+
+class TokenShard(_Handle):
+    """TokenShard (shard.rs:53-260): token ids of one vocabulary, stored as a
+    32-byte header, 2- or 4-byte little-endian ids and a SHA-256."""
+
+    _destroy = "mmh_shard_destroy"
+
+    def __init__(self, vocab_size: int, eos: int, tokens=(), *, _handle: Optional[int] = None):
+        if _handle is None:
+            t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int64).astype(np.uint32))
+            if np.any(np.asarray(tokens, dtype=np.int64) != t):
+                raise ArgumentError(ERR_ARGUMENT, "token ids are 32-bit unsigned")
+            h = _h()
+            check(lib().mmh_shard_create(vocab_size, eos, t.ctypes.data_as(_u32p), t.size,
+                                         ctypes.byref(h)))
+            _handle = h.value
+        self.handle = _handle
+
+    @classmethod
+    def from_bytes(cls, data: bytes) -> "TokenShard":
+        h = _h()
+        check(lib().mmh_shard_parse(data, len(data), ctypes.byref(h)))
+        return cls(0, 0, _handle=h.value)
+
+    @classmethod
+    def load(cls, path: str) -> "TokenShard":
+        h = _h()
+        check(lib().mmh_shard_load(os.fsencode(path), ctypes.byref(h)))
+        return cls(0, 0, _handle=h.value)
+
+    def save(self, path: str):
+        check(lib().mmh_shard_save(self.handle, os.fsencode(path)))
+
+    def _info(self):
+        v, e, w = ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint32()
+        n, fb = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().mmh_shard_info(self.handle, ctypes.byref(v), ctypes.byref(e),
+                                   ctypes.byref(n), ctypes.byref(w), ctypes.byref(fb)))
+        return v.value, e.value, n.value, w.value, fb.value
+
+    def vocab_size(self) -> int:
+        return self._info()[0]
+
+    def eos(self) -> int:
+        return self._info()[1]
+
+    def __len__(self) -> int:
+        return self._info()[2]
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def token_width(self) -> int:
+        return self._info()[3]
+
+    def tokens(self) -> np.ndarray:
+        n = len(self)
+        out = np.empty(n, np.uint32)
+        check(lib().mmh_shard_tokens(self.handle, out.ctypes.data_as(_u32p), n))
+        return out
+
+    def to_bytes(self) -> bytes:
+        n = ctypes.c_uint64()
+        check(lib().mmh_shard_serialize(self.handle, None, 0, ctypes.byref(n)))
+        buf = ctypes.create_string_buffer(max(1, n.value))
+        check(lib().mmh_shard_serialize(self.handle, buf, n.value, ctypes.byref(n)))
+        return buf.raw[: n.value]
+
+    def __eq__(self, other):
+        return (isinstance(other, TokenShard) and self._info()[:3] == other._info()[:3]
+                and np.array_equal(self.tokens(), other.tokens()))
+
+    __hash__ = None
+
+
+class Sequences(_Handle):
+    """Sequences (batch.rs:31-104): windows of seq_len + 1 tokens, one every
+    seq_len tokens of each shard, never across shards."""
+
+    _destroy = "mmh_sequences_destroy"
+
+    def __init__(self, shards, seq_len: int):
+        hs = (_h * max(1, len(shards)))(*[s.handle for s in shards])
+        h = _h()
+        check(lib().mmh_sequences_create(hs, len(shards), seq_len, ctypes.byref(h)))
+        self.handle = h.value
+
+    def _info(self):
+        n, t, v = ctypes.c_uint64(), ctypes.c_uint64(), _i64()
+        check(lib().mmh_sequences_info(self.handle, ctypes.byref(n), ctypes.byref(t),
+                                       ctypes.byref(v)))
+        return n.value, t.value, v.value
+
+    def __len__(self) -> int:
+        return self._info()[0]
+
+    def is_empty(self) -> bool:
+        return len(self) == 0
+
+    def seq_len(self) -> int:
+        return self._info()[1]
+
+    def vocab_size(self) -> Optional[int]:
+        v = self._info()[2]
+        return None if v < 0 else v
+
+    def window(self, index: int) -> Optional[np.ndarray]:
+        """The seq_len + 1 ids of sequence `index`, or None."""
+        if index < 0 or index >= len(self):
+            return None
+        out = np.empty(self.seq_len() + 1, np.uint32)
+        check(lib().mmh_sequences_window(self.handle, index, out.ctypes.data_as(_u32p)))
+        return out
+
+
+class Batch:
+    """One batch (batch.rs:107-122): inputs and targets are batch * seq ids."""
+
+    __slots__ = ("inputs", "targets", "batch", "seq", "epoch", "index")
+
+    def __init__(self, inputs, targets, batch, seq, epoch, index):
+        self.inputs, self.targets = inputs, targets
+        self.batch, self.seq, self.epoch, self.index = batch, seq, epoch, index
+
+    def __eq__(self, other):
+        return (isinstance(other, Batch)
+                and (self.batch, self.seq, self.epoch, self.index)
+                == (other.batch, other.seq, other.epoch, other.index)
+                and np.array_equal(self.inputs, other.inputs)
+                and np.array_equal(self.targets, other.targets))
+
+    __hash__ = None
+
+
+class Batcher(_Handle):
+    """Batcher (batch.rs:144-240): batches of batch_size sequences, endlessly,
+    each pass in the order Rng(seed).fork(epoch).shuffle(0..len)."""
+
+    _destroy = "mmh_batcher_destroy"
+
+    def __init__(self, data: Sequences, batch_size: int, seed: int):
+        h = _h()
+        check(lib().mmh_batcher_create(data.handle, batch_size, seed, ctypes.byref(h)))
+        self.handle = h.value
+        self.data = data
+
+    def _info(self):
+        v = [ctypes.c_uint64() for _ in range(5)]
+        check(lib().mmh_batcher_info(self.handle, *[ctypes.byref(x) for x in v]))
+        return [x.value for x in v]
+
+    def batches_per_epoch(self) -> int:
+        return self._info()[0]
+
+    def epoch(self) -> int:
+        return self._info()[1]
+
+    def position(self) -> int:
+        return self._info()[2]
+
+    def seek(self, epoch: int, batches_done: int):
+        check(lib().mmh_batcher_seek(self.handle, epoch, batches_done))
+
+    def next_batch(self) -> Batch:
+        _, _, _, b, t = self._info()
+        x, y = np.empty(b * t, np.uint32), np.empty(b * t, np.uint32)
+        e, i = ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().mmh_batcher_next(self.handle, x.ctypes.data_as(_u32p),
+                                     y.ctypes.data_as(_u32p), ctypes.byref(e), ctypes.byref(i)))
+        return Batch(x, y, b, t, e.value, i.value)
+
+
 # ---- the model: midman-model/src/model.rs ------------------------------------------
 
 CONFIG_FIELDS = ("vocab_size", "d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff",
@@ -803,6 +1056,26 @@ class Model:
         out = ctypes.c_uint64()
         check(lib().mmh_model_optimizer_steps(self.handle, ctypes.byref(out)))
         return out.value
+
+    def train_next(self, batcher: "Batcher", lr: float):
+        """Trainer::step (trainer.rs:162-183) on the batcher's next batch:
+        (loss, grad_norm, epoch, index). A step that fails raises (Stopped for
+        a non-finite loss or norm) and leaves the batcher where it was."""
+        loss, norm = ctypes.c_float(), ctypes.c_float()
+        e, i = ctypes.c_uint64(), ctypes.c_uint64()
+        st = lib().mmh_model_train_next(self.handle, batcher.handle, lr, ctypes.byref(loss),
+                                        ctypes.byref(norm), ctypes.byref(e), ctypes.byref(i))
+        if st == STOPPED:
+            raise Stopped(st, last_error())
+        check(st)
+        return loss.value, norm.value, e.value, i.value
+
+    def evaluate(self, data: "Sequences", batch_size: int, max_batches: int):
+        """Trainer::evaluate (trainer.rs:218-258): (loss, batches, tokens)."""
+        loss, nb, nt = ctypes.c_float(), ctypes.c_uint64(), ctypes.c_uint64()
+        check(lib().mmh_model_evaluate(self.handle, data.handle, batch_size, max_batches,
+                                       ctypes.byref(loss), ctypes.byref(nb), ctypes.byref(nt)))
+        return loss.value, nb.value, nt.value
 
     def close(self):
         if self.handle:

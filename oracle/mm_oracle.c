@@ -98,6 +98,30 @@ uint64_t mmo_rng_below(mmo_rng *r, uint64_t n) {
     return (uint64_t)(product >> 64);
 }
 
+void mmo_rng_fork(mmo_rng *r, uint64_t stream, mmo_rng *out) {
+    /* rng.rs:117-119: wrapping multiply by the golden-ratio constant, xor */
+    mmo_rng_seed(out, mmo_rng_next_u64(r) ^ (stream * 0x9E3779B97F4A7C15ull));
+}
+
+void mmo_rng_shuffle_u64(mmo_rng *r, uint64_t *items, uint64_t n) {
+    /* rng.rs:108-113 */
+    for (uint64_t i = n ? n - 1 : 0; i >= 1; i--) {
+        const uint64_t j = mmo_rng_below(r, i + 1);
+        const uint64_t t = items[i];
+        items[i] = items[j];
+        items[j] = t;
+    }
+}
+
+void mmo_permutation(uint64_t n, uint64_t seed, uint64_t epoch, uint64_t *out) {
+    /* batch.rs:244-248 */
+    mmo_rng base, f;
+    for (uint64_t i = 0; i < n; i++) out[i] = i;
+    mmo_rng_seed(&base, seed);
+    mmo_rng_fork(&base, epoch, &f);
+    mmo_rng_shuffle_u64(&f, out, n);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Config: crates/midman-model-config/src/config.rs, presets.rs              */
 /* ------------------------------------------------------------------------ */

@@ -43,6 +43,19 @@
  *                     AdamW alone -> its three-step table (adamw.rs:234-259);
  *                     schedule -> lr[0] = max/15, lr[14] = max
  *                     (engine.test.mjs:123-131) and schedule.rs tests
+ *   fork           -> stream 0 reduces to seed(next_u64()) (pinned above);
+ *                     the stream multiplier is floor(2^64/phi), checked
+ *                     against the integer square root of 5; the xor that
+ *                     combines them is pinned only structurally (the
+ *                     reference's rng.rs:231-241 independence test)
+ *   shuffle / permutation -> the draws-to-permutation map is a bijection
+ *                     over all n! draw tuples for n <= 5 (brute force);
+ *                     the reference's batch.rs tests (one pass uses each
+ *                     sequence at most once, seeds and passes differ);
+ *                     PARITY UNPINNED in absolute terms: the reference
+ *                     holds no fixed permutation of a known seed (its one
+ *                     batch digest, data-smoke-results.json, needs the
+ *                     out-of-scope tokenizer and corpus)
  */
 #ifndef MM_ORACLE_H
 #define MM_ORACLE_H
@@ -74,6 +87,13 @@ float mmo_rng_next_f32(mmo_rng *r);                     /* rng.rs:58-60 */
 double mmo_rng_next_f64(mmo_rng *r);                    /* rng.rs:63-65 */
 float mmo_rng_normal(mmo_rng *r);                       /* rng.rs:74-84 */
 uint64_t mmo_rng_below(mmo_rng *r, uint64_t n);         /* rng.rs:91-105 */
+/* Rng::fork (rng.rs:117-119): a generator for stream `stream`; advances r. */
+void mmo_rng_fork(mmo_rng *r, uint64_t stream, mmo_rng *out);
+/* Rng::shuffle (rng.rs:108-113): Fisher-Yates from the end, j = below(i+1). */
+void mmo_rng_shuffle_u64(mmo_rng *r, uint64_t *items, uint64_t n);
+/* The Batcher's order of pass `epoch` (batch.rs:244-248):
+ * Rng::seed_from_u64(seed).fork(epoch).shuffle(0..n). */
+void mmo_permutation(uint64_t n, uint64_t seed, uint64_t epoch, uint64_t *out);
 /* Tensor::randn (tensor.rs:158-162): dst[i] = std * normal(), in order. */
 void mmo_randn(mmo_rng *r, float *dst, int64_t n, float std);
 

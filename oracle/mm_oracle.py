@@ -74,6 +74,11 @@ def lib():
             "mmo_rng_next_f64": (ctypes.c_double, [R]),
             "mmo_rng_normal": (ctypes.c_float, [R]),
             "mmo_rng_below": (ctypes.c_uint64, [R, ctypes.c_uint64]),
+            "mmo_rng_fork": (None, [R, ctypes.c_uint64, R]),
+            "mmo_rng_shuffle_u64": (None, [R, ctypes.POINTER(ctypes.c_uint64),
+                                           ctypes.c_uint64]),
+            "mmo_permutation": (None, [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64,
+                                       ctypes.POINTER(ctypes.c_uint64)]),
             "mmo_randn": (None, [R, _f32p, _i64, ctypes.c_float]),
             "mmo_config_validate": (_i32, [C]),
             "mmo_param_count": (_i64, [C]),
@@ -502,6 +507,113 @@ def lab_train(c, hyper, seed, batch, seq, steps, want_weights=False, threads=Non
     if st != OK:
         raise ValueError(f"lab_train status {st}")
     return losses, norms, lrs, w
+
+
+# ---- token shards, sequences and the batcher (midman-data) -----------------
+
+SHARD_MAGIC = b"MMTOKENS"
+SHARD_HEADER = 32  # shard.rs:22-23: magic 8, four u32, one u64
+SHARD_CHECKSUM = 32
+
+
+def shard_width(vocab):
+    """shard.rs:28-34: 2 bytes per id up to 65,536 ids, else 4."""
+    return 2 if vocab <= 65536 else 4
+
+
+def shard_bytes(vocab, eos, tokens):
+    """TokenShard::to_bytes (shard.rs:112-135): header, little-endian ids, and
+    the SHA-256 of everything before it (hashlib)."""
+    import hashlib
+    import struct
+    w = shard_width(vocab)
+    t = np.asarray(tokens, dtype=np.uint32)
+    body = SHARD_MAGIC + struct.pack("<IIIIQ", 1, w, vocab, eos, t.size) + \
+        t.astype("<u2" if w == 2 else "<u4").tobytes()
+    return body + hashlib.sha256(body).digest()
+
+
+def shard_parse(data):
+    """TokenShard::from_bytes (shard.rs:146-223) restated: returns (vocab, eos,
+    tokens) or raises ValueError whose text holds the reference's reason."""
+    import hashlib
+    import struct
+    if len(data) < SHARD_HEADER + SHARD_CHECKSUM:
+        raise ValueError(f"{len(data)} bytes is shorter than the smallest shard, 64")
+    if data[:8] != SHARD_MAGIC:
+        raise ValueError("the file does not start with `MMTOKENS`")
+    version, width, vocab, eos, count = struct.unpack("<IIIIQ", data[8:32])
+    if version != 1:
+        raise ValueError(f"token shard version {version} is not supported")
+    if vocab == 0:
+        raise ValueError("the vocabulary size is 0")
+    if width != shard_width(vocab):
+        raise ValueError(f"token width {width} is not the one for a vocabulary of {vocab} ids")
+    if eos >= vocab:
+        raise ValueError(f"the end-of-text id {eos} is not below the vocabulary size {vocab}")
+    if count * width + SHARD_HEADER + SHARD_CHECKSUM != len(data):
+        raise ValueError(f"{count} tokens of {width} bytes do not make a file of "
+                         f"{len(data)} bytes")
+    body = len(data) - SHARD_CHECKSUM
+    if hashlib.sha256(data[:body]).digest() != data[body:]:
+        raise ValueError("the checksum does not match: the file is damaged")
+    t = np.frombuffer(data[SHARD_HEADER:body], "<u2" if width == 2 else "<u4").astype(np.uint32)
+    bad = np.nonzero(t >= vocab)[0]
+    if bad.size:
+        at = int(bad[0])
+        raise ValueError(f"token {int(t[at])} at position {at} is not below the vocabulary "
+                         f"size {vocab}")
+    return vocab, eos, t
+
+
+def sequence_windows(shard_tokens, seq_len):
+    """Sequences::new + window (batch.rs:45-104): the window starts of every
+    sequence, as (shard index, first token) pairs in sequence order."""
+    out = []
+    for s, t in enumerate(shard_tokens):
+        n = len(t)
+        if n > seq_len:
+            out += [(s, i * seq_len) for i in range((n - 1) // seq_len)]
+    return out
+
+
+def permutation(n, seed, epoch):
+    """permutation() of batch.rs:244-248 through the C restatement."""
+    out = np.empty(n, dtype=np.uint64)
+    lib().mmo_permutation(n, seed, epoch,
+                          out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)))
+    return out
+
+
+def batches(shard_tokens, seq_len, batch, seed, count):
+    """The first `count` batches of Batcher::new(..).next_batch() (batch.rs:161-239):
+    a list of (inputs, targets, epoch, index), ids as uint32 arrays."""
+    wins = sequence_windows(shard_tokens, seq_len)
+    n = len(wins)
+    per = n // batch
+    if batch == 0 or n < batch:
+        raise ValueError("fewer sequences than one batch")
+    out, epoch, nxt = [], 0, 0
+    order = permutation(n, seed, 0)
+    for _ in range(count):
+        if nxt == per:
+            epoch, nxt = epoch + 1, 0
+            order = permutation(n, seed, epoch)
+        rows = [wins[int(i)] for i in order[nxt * batch:(nxt + 1) * batch]]
+        w = np.stack([np.asarray(shard_tokens[s][a:a + seq_len + 1], np.uint32)
+                      for s, a in rows])
+        out.append((w[:, :seq_len].reshape(-1), w[:, 1:].reshape(-1), epoch, nxt))
+        nxt += 1
+    return out
+
+
+def eval_rows(n, batch_size, max_batches):
+    """Trainer::evaluate's choice of sequences (trainer.rs:236-249): a list of
+    batches, each a list of sequence indices."""
+    batch = min(batch_size, n)
+    nb = min(max_batches, n // batch)
+    rows = nb * batch
+    return [[(b * batch + r) * n // rows for r in range(batch)] for b in range(nb)]
 
 
 # ---- the reference's own C twins (oracle/_ref) -----------------------------
