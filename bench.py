@@ -39,7 +39,7 @@ PEAK_HBM_GBS = 8000.0
 # what the counter reads for the add kernel's known traffic (FETCH x 2.0,
 # WRITE x 1.0): (43,181,710 + 4,935,760) KiB over 81 launches. The counters
 # cannot be read from inside this process; see profiles/large_forward_hbm_traffic.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 608.3e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 641.3e6
 
 
 def log(msg):
