@@ -220,6 +220,42 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
             "train": train, "checkpoint": ckpt, "data": data}
 
 
+def time_block(mh, ctx, hkv, reps=20):
+    """DecoderBlock::forward alone at the BASELINE block config: d 1024, 16
+    heads x 64, SwiGLU 2816, B8 T1024, x ~ N(0,1), W ~ N(0,0.02) seeded.
+    HIP events around `reps` calls after 3 warmups (weights packed per call,
+    as the op-level entry point does)."""
+    import numpy as np
+
+    B, T, d, H, ff = 8, 1024, 1024, 16, 2816
+    hd = d // H
+    kv = hkv * hd
+    r = np.random.default_rng(7)
+    x = ctx.to_device(r.standard_normal((B, T, d), dtype=np.float32))
+    n_w = 2 * d + 2 * d * d + 2 * d * kv + 3 * d * ff
+    w = (0.02 * r.standard_normal(n_w, dtype=np.float32))
+    w[:d] = 1.0
+    w[d + 2 * d * d + 2 * d * kv: 2 * d + 2 * d * d + 2 * d * kv] = 1.0
+    dw = ctx.to_device(w)
+    out = ctx.empty((B, T, d))
+    tabs = mh.RotaryTables(ctx, hd, T, 10000.0)
+    for _ in range(3):
+        mh.block_forward(ctx, x, dw, H, hkv, ff, 1e-5, tabs, out=out)
+    ctx.synchronize()
+    ctx.timer_start()
+    for _ in range(reps):
+        mh.block_forward(ctx, x, dw, H, hkv, ff, 1e-5, tabs, out=out)
+    ms = ctx.timer_stop() / reps
+    n = B * T
+    gemm = 2 * n * d * (d + 2 * kv) + 2 * n * d * d + 2 * n * d * 2 * ff + 2 * n * ff * d
+    attn = 4 * B * H * hd * T * (T + 1) // 2
+    for a in (x, dw, out):
+        a.free()
+    return {"workload": f"block d{d} H{H} Hkv{hkv} hd{hd} ff{ff}, B{B} T{T}",
+            "ms": round(ms, 4), "flops": gemm + attn,
+            "tflops": round((gemm + attn) / (ms / 1000) / 1e12, 2)}
+
+
 def gemm_sweep(mh, ctx, reps=10):
     M = 2048
     rows = []
@@ -356,6 +392,9 @@ def main():
         log(f"large from shards: load {dd['load_gbs']} GB/s, batch {dd['batch_assembly_us']} us, "
             f"train {dd['train_ms_per_step']} ms/step ({dd['train_tokens_per_s']:.0f} tok/s), "
             f"eval {dd['eval_tokens_per_s']:.0f} tok/s")
+    blocks = [time_block(mh, ctx, hkv) for hkv in (16, 8)]
+    for b in blocks:
+        log(f"{b['workload']}: {b['ms']} ms, {b['tflops']} TFLOP/s")
     tiny = None
     if not a.no_tiny:
         tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5))
@@ -439,6 +478,7 @@ def main():
                 workload="large preset B4 T1024 trained (Trainer::step) and evaluated "
                          "(Trainer::evaluate) from token shard files through the seeded "
                          "batcher; synthetic uniform ids", **large["data"]),
+            "block": blocks,
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),

@@ -1,7 +1,9 @@
 /*
  * midman_hip.h -- C ABI of libmidman_hip.so, the MI355X (gfx950) implementation
  * of midman-ai's decoder forward + cross-entropy loss, the autograd matmul
- * backward, the full decoder backward and the clip + AdamW training step.
+ * backward, the full decoder backward, the clip + AdamW training step,
+ * safetensors checkpoints to and from the device, and token shards with the
+ * seeded batcher feeding training and evaluation.
  *
  * Conventions follow the reference's own C ABI (crates/midman-api/src/ffi.rs:5-32):
  *   - Handles, not pointers, for library objects (contexts, models). A stale or
@@ -276,6 +278,18 @@ int32_t mmh_model_optimizer_steps(mmh_handle model, uint64_t *out);
 /* WarmupCosine::new + lr(step) (schedule.rs:25-66), f64 inside, f32 out. */
 int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
                              uint64_t total_steps, uint64_t step, float *lr_out);
+
+/* DecoderBlock::forward (block.rs:67-81): out = h + mlp(mlp_norm(h)) with
+ * h = x + attn(attn_norm(x)), on device buffers. block_weights holds the
+ * block's parameters in DecoderBlock::parameters order (block.rs:85-93):
+ * attn_norm [d], q [d,d], k [d,kv], v [d,kv], o [d,d], mlp_norm [d],
+ * gate [d,ff], up [d,ff], down [ff,d] (kv = hkv * d/h). x, out [b,t,d]; out
+ * may be x itself but must not otherwise overlap it. cos/sin are the rotary
+ * tables (mmh_rope_tables) for at least t positions. Tolerance as
+ * mmh_attention_forward + mmh_swiglu. */
+int32_t mmh_block_forward(mmh_handle ctx, const float *x, const float *block_weights,
+                          const float *cos_dev, const float *sin_dev, int64_t b, int64_t t,
+                          int64_t d, int64_t h, int64_t hkv, int64_t ff, float eps, float *out);
 
 /* ---- Checkpoints: midman-checkpoint (safetensors.rs, params.rs) -----------
  * TensorFile (safetensors.rs:68-330): named F32 tensors + string metadata,

@@ -98,6 +98,98 @@ Config parse_config(const double *v) {
     return c;
 }
 
+// One pre-norm block (block.rs:77-81) on packed weights: x += attn(rms(x)),
+// then x += mlp(rms(x)), the residual adds fused into the O and down GEMMs
+// and SwiGLU into the gate/up GEMM. timed(class, launch) wraps each launch.
+struct BlockRun {
+    const float *attn_norm = nullptr, *wqkv = nullptr, *wo = nullptr;
+    const float *mlp_norm = nullptr, *wgu = nullptr, *wd = nullptr;
+    const float *cos_t = nullptr, *sin_t = nullptr;
+    float *x = nullptr;  // [n, d], updated in place
+    float *xn = nullptr, *qkv = nullptr, *cb = nullptr, *h = nullptr;
+    int64_t batch = 0, seq = 0, d = 0, heads = 0, kv_heads = 0, ff = 0, ff_pad = 0;
+    float eps = 0.0f;
+};
+
+template <class Timed>
+void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
+    const int64_t n = r.batch * r.seq, d = r.d, hd = d / r.heads, kv = r.kv_heads * hd;
+    const int64_t qc = d + 2 * kv;
+    timed(MMH_PROF_RMS_NORM, [&] { launch_rms_norm(c, r.x, r.attn_norm, n, d, r.eps, r.xn); });
+    GemmDesc g;
+    g.a = r.xn;
+    g.b = r.wqkv;
+    g.c = r.qkv;
+    g.m = n;
+    g.k = d;
+    g.n = qc;
+    g.lda = d;
+    g.ldb = qc;
+    g.ldc = qc;
+    timed(MMH_PROF_GEMM_QKV, [&] { gemm(c, g); });
+
+    AttnDesc a{};
+    a.q = r.qkv;
+    a.k = r.qkv + d;
+    a.v = r.qkv + d + kv;
+    a.out = r.cb;
+    a.sqb = a.skb = a.svb = r.seq * qc;
+    a.sqh = a.skh = a.svh = hd;
+    a.sqt = a.skt = a.svt = qc;
+    a.sob = r.seq * d;
+    a.soh = hd;
+    a.sot = d;
+    a.b = r.batch;
+    a.h = r.heads;
+    a.hkv = r.kv_heads;
+    a.t = r.seq;
+    a.hd = hd;
+    a.cos_t = r.cos_t;
+    a.sin_t = r.sin_t;
+    timed(MMH_PROF_ATTENTION, [&] { attention(c, a); });
+
+    GemmDesc o;
+    o.a = r.cb;
+    o.b = r.wo;
+    o.c = r.x;
+    o.m = n;
+    o.k = d;
+    o.n = d;
+    o.lda = d;
+    o.ldb = d;
+    o.ldc = d;
+    o.epi = EPI_ACCUM;
+    timed(MMH_PROF_GEMM_O, [&] { gemm(c, o); });
+
+    timed(MMH_PROF_RMS_NORM, [&] { launch_rms_norm(c, r.x, r.mlp_norm, n, d, r.eps, r.xn); });
+    GemmDesc gu;
+    gu.a = r.xn;
+    gu.b = r.wgu;
+    gu.c = r.h;
+    gu.m = n;
+    gu.k = d;
+    gu.n = 2 * r.ff_pad;
+    gu.lda = d;
+    gu.ldb = 2 * r.ff_pad;
+    gu.ldc = r.ff;
+    gu.epi = EPI_SWIGLU;
+    gu.swiglu_ff = r.ff;
+    timed(MMH_PROF_GEMM_GATE_UP, [&] { gemm(c, gu); });
+
+    GemmDesc dn;
+    dn.a = r.h;
+    dn.b = r.wd;
+    dn.c = r.x;
+    dn.m = n;
+    dn.k = r.ff;
+    dn.n = d;
+    dn.lda = r.ff;
+    dn.ldb = d;
+    dn.ldc = d;
+    dn.epi = EPI_ACCUM;
+    timed(MMH_PROF_GEMM_DOWN, [&] { gemm(c, dn); });
+}
+
 struct Model {
     mmh_handle ctx_handle = 0;
     Context *ctx = nullptr;
@@ -293,85 +385,32 @@ struct Model {
         if (seq > cfg.max_seq) fail(MMH_ERR_ARGUMENT, "forward: sequence length exceeds max_seq_len");
         if (with_loss && !staged_targets) fail(MMH_ERR_ARGUMENT, "no targets staged");
         Context &c = *ctx;
-        const int64_t d = cfg.d, kv = cfg.kv(), hd = cfg.hd(), V = cfg.vocab;
+        const int64_t d = cfg.d, V = cfg.vocab;
         timed(prof, MMH_PROF_EMBEDDING, [&] { launch_embedding(c, embed(), d, ids, n, x); });
+        BlockRun r;
+        r.cos_t = cos_t;
+        r.sin_t = sin_t;
+        r.x = x;
+        r.xn = xn;
+        r.qkv = qkv;
+        r.cb = cb;
+        r.h = h;
+        r.batch = batch;
+        r.seq = seq;
+        r.d = d;
+        r.heads = cfg.heads;
+        r.kv_heads = cfg.kv_heads;
+        r.ff = cfg.ff;
+        r.ff_pad = ff_pad;
+        r.eps = cfg.eps;
         for (int64_t l = 0; l < cfg.layers; ++l) {
-            timed(prof, MMH_PROF_RMS_NORM,
-                  [&] { launch_rms_norm(c, x, attn_norm(l), n, d, cfg.eps, xn); });
-            GemmDesc g;
-            g.a = xn;
-            g.b = wqkv(l);
-            g.c = qkv;
-            g.m = n;
-            g.k = d;
-            g.n = qkv_cols();
-            g.lda = d;
-            g.ldb = qkv_cols();
-            g.ldc = qkv_cols();
-            timed(prof, MMH_PROF_GEMM_QKV, [&] { gemm(c, g); });
-
-            AttnDesc a{};
-            const int64_t ld = qkv_cols();
-            a.q = qkv;
-            a.k = qkv + d;
-            a.v = qkv + d + kv;
-            a.out = cb;
-            a.sqb = a.skb = a.svb = seq * ld;
-            a.sqh = a.skh = a.svh = hd;
-            a.sqt = a.skt = a.svt = ld;
-            a.sob = seq * d;
-            a.soh = hd;
-            a.sot = d;
-            a.b = batch;
-            a.h = cfg.heads;
-            a.hkv = cfg.kv_heads;
-            a.t = seq;
-            a.hd = hd;
-            a.cos_t = cos_t;
-            a.sin_t = sin_t;
-            timed(prof, MMH_PROF_ATTENTION, [&] { attention(c, a); });
-
-            GemmDesc o;
-            o.a = cb;
-            o.b = wo(l);
-            o.c = x;
-            o.m = n;
-            o.k = d;
-            o.n = d;
-            o.lda = d;
-            o.ldb = d;
-            o.ldc = d;
-            o.epi = EPI_ACCUM;
-            timed(prof, MMH_PROF_GEMM_O, [&] { gemm(c, o); });
-
-            timed(prof, MMH_PROF_RMS_NORM,
-                  [&] { launch_rms_norm(c, x, mlp_norm(l), n, d, cfg.eps, xn); });
-            GemmDesc gu;
-            gu.a = xn;
-            gu.b = wgu(l);
-            gu.c = h;
-            gu.m = n;
-            gu.k = d;
-            gu.n = 2 * ff_pad;
-            gu.lda = d;
-            gu.ldb = 2 * ff_pad;
-            gu.ldc = cfg.ff;
-            gu.epi = EPI_SWIGLU;
-            gu.swiglu_ff = cfg.ff;
-            timed(prof, MMH_PROF_GEMM_GATE_UP, [&] { gemm(c, gu); });
-
-            GemmDesc dn;
-            dn.a = h;
-            dn.b = wd(l);
-            dn.c = x;
-            dn.m = n;
-            dn.k = cfg.ff;
-            dn.n = d;
-            dn.lda = cfg.ff;
-            dn.ldb = d;
-            dn.ldc = d;
-            dn.epi = EPI_ACCUM;
-            timed(prof, MMH_PROF_GEMM_DOWN, [&] { gemm(c, dn); });
+            r.attn_norm = attn_norm(l);
+            r.wqkv = wqkv(l);
+            r.wo = wo(l);
+            r.mlp_norm = mlp_norm(l);
+            r.wgu = wgu(l);
+            r.wd = wd(l);
+            enqueue_block(c, r, [&](int cls, auto &&launch) { timed(prof, cls, launch); });
         }
         timed(prof, MMH_PROF_RMS_NORM,
               [&] { launch_rms_norm(c, x, final_norm(), n, d, cfg.eps, xn); });
@@ -1352,6 +1391,67 @@ int32_t mmh_model_create_from_checkpoint(mmh_handle ctx, const double config[10]
         }
         m->pack();
         *out_model = register_model(std::move(m));
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_block_forward(mmh_handle ctx, const float *x, const float *block_weights,
+                          const float *cos_dev, const float *sin_dev, int64_t b, int64_t t,
+                          int64_t d, int64_t h, int64_t hkv, int64_t ff, float eps, float *out) {
+    return guard([&] {
+        Context &c = context(ctx);
+        for (const void *p : {(const void *)x, (const void *)block_weights, (const void *)cos_dev,
+                              (const void *)sin_dev, (const void *)out})
+            if (!p) fail(MMH_ERR_ARGUMENT, "block_forward: a null pointer argument");
+        for (int64_t v : {b, t, d, h, hkv, ff})
+            if (v <= 0) fail(MMH_ERR_ARGUMENT, "block_forward: sizes must be positive");
+        if (d % h || h % hkv)
+            fail(MMH_ERR_SHAPE, "block_forward: d_model % n_heads or n_heads % n_kv_heads != 0");
+        if (!(std::isfinite(eps) && eps > 0.0f))
+            fail(MMH_ERR_ARGUMENT, "block_forward: eps must be positive and finite");
+        const int64_t hd = d / h, kv = hkv * hd, n = b * t, qc = d + 2 * kv;
+        const int64_t ff_pad = (ff + 31) / 32 * 32;
+        // DecoderBlock::parameters order (block.rs:85-93)
+        const float *an = block_weights, *wq = an + d, *wk = wq + d * d, *wv = wk + d * kv;
+        const float *wo = wv + d * kv, *mn = wo + d * d, *wg = mn + d, *wu = wg + d * ff;
+        const float *wdn = wu + d * ff;
+        auto al = [](int64_t v) { return (v + 63) / 64 * 64; };
+        const int64_t sizes[] = {al(d * qc), al(d * 2 * ff_pad), al(n * d), al(n * qc),
+                                 al(n * d), al(n * ff)};
+        int64_t total = 0;
+        for (int64_t v : sizes) total += v;
+        float *ws = static_cast<float *>(c.workspace(2, (size_t)total * 4));
+        float *wqkv = ws, *wgu = wqkv + sizes[0];
+        BlockRun r;
+        r.xn = wgu + sizes[1];
+        r.qkv = r.xn + sizes[2];
+        r.cb = r.qkv + sizes[3];
+        r.h = r.cb + sizes[4];
+        launch_pack_cols(c, wq, d, d, wqkv, qc, 0);
+        launch_pack_cols(c, wk, d, kv, wqkv, qc, d);
+        launch_pack_cols(c, wv, d, kv, wqkv, qc, d + kv);
+        launch_pack_gate_up(c, wg, wu, d, ff, ff_pad, wgu);
+        if (out != x)
+            check_hip(hipMemcpyAsync(out, x, (size_t)(n * d) * 4, hipMemcpyDeviceToDevice,
+                                     c.stream), "block input copy");
+        r.attn_norm = an;
+        r.wqkv = wqkv;
+        r.wo = wo;
+        r.mlp_norm = mn;
+        r.wgu = wgu;
+        r.wd = wdn;
+        r.cos_t = cos_dev;
+        r.sin_t = sin_dev;
+        r.x = out;
+        r.batch = b;
+        r.seq = t;
+        r.d = d;
+        r.heads = h;
+        r.kv_heads = hkv;
+        r.ff = ff;
+        r.ff_pad = ff_pad;
+        r.eps = eps;
+        enqueue_block(c, r, [](int, auto &&launch) { launch(); });
         return MMH_OK;
     });
 }

@@ -100,6 +100,7 @@ _SIGNATURES = {
     "mmh_causal_attention": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
     "mmh_attention_forward": [_h, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                               _i64, _vp],
+    "mmh_block_forward": [_h, _vp, _vp, _vp, _vp] + [_i64] * 6 + [ctypes.c_float, _vp],
     "mmh_swiglu": [_h, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "mmh_add": [_h, _vp, _vp, _vp, _i64],
     "mmh_cross_entropy": [_h, _vp, _i32p, _i64, _i64, _f32p],
@@ -449,6 +450,20 @@ def attention_forward(ctx: Context, x: DeviceArray, wq, wk, wv, wo, n_heads: int
     check(lib().mmh_attention_forward(ctx.handle, x.ptr, _ptr(wq), _ptr(wk), _ptr(wv), _ptr(wo),
                                       tables.cos.ptr, tables.sin.ptr, B, T, d, n_heads,
                                       n_kv_heads, out.ptr))
+    return out
+
+
+def block_forward(ctx: Context, x: DeviceArray, block_weights: DeviceArray, n_heads: int,
+                  n_kv_heads: int, d_ff: int, eps: float, tables: RotaryTables,
+                  out: DeviceArray = None):
+    """DecoderBlock::forward (block.rs:67-81): x [B,T,d] -> [B,T,d]. The
+    weights are one flat array in DecoderBlock::parameters order (attn_norm,
+    q, k, v, o, mlp_norm, gate, up, down)."""
+    B, T, d = x.shape
+    out = out or ctx.empty(x.shape)
+    check(lib().mmh_block_forward(ctx.handle, x.ptr, block_weights.ptr, tables.cos.ptr,
+                                  tables.sin.ptr, B, T, d, n_heads, n_kv_heads, d_ff, eps,
+                                  out.ptr))
     return out
 
 

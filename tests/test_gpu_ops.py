@@ -10,6 +10,8 @@ Tolerances, stated per op:
             MFMA dot order).
   attention_forward / swiglu: |diff| <= 1e-4 * max|ref| per tensor (three or
             four chained GEMMs).
+  block_forward: the block's change out - x within 2e-4 of its max|ref|
+            (two norms and both sublayers chained), out itself within 1e-5.
   cross_entropy: 1e-4 relative to the oracle (the north-star loss
             tolerance; the reference's sequential f32 sum of V exponentials
             drifts by up to ~1e-5 relative at V = 1e5) and 2e-6 relative to a
@@ -149,6 +151,49 @@ def test_attention_forward(ctx, B, T, d, H, Hkv):
     e = rel_max(got, want)
     print(f"  max|diff|/max|ref| {e:.3g}", flush=True)
     assert e <= 1e-4
+
+
+@pytest.mark.parametrize("B,T,d,H,Hkv,ff", [
+    (2, 12, 16, 2, 1, 24), (2, 64, 256, 4, 2, 176), (1, 100, 128, 1, 1, 344),
+    # the BASELINE block config, both kv-head counts
+    (8, 1024, 1024, 16, 16, 2816), (8, 1024, 1024, 16, 8, 2816)])
+def test_block_forward(ctx, B, T, d, H, Hkv, ff):
+    """DecoderBlock::forward (block.rs:77-81) against the oracle's block."""
+    print(f"\n[block_forward] B={B} T={T} d={d} H={H} Hkv={Hkv} ff={ff}", flush=True)
+    hd, kv = d // H, Hkv * (d // H)
+    c = O.config(1, d, 1, H, Hkv, ff, T)
+    r = O.rng(d + ff + Hkv)
+    x = O.randn((B, T, d), 1.0, r)
+    parts = [np.ones(d, np.float32), O.randn((d, d), 0.02, r), O.randn((d, kv), 0.02, r),
+             O.randn((d, kv), 0.02, r), O.randn((d, d), 0.02, r), np.ones(d, np.float32),
+             O.randn((d, ff), 0.02, r), O.randn((d, ff), 0.02, r), O.randn((ff, d), 0.02, r)]
+    bw = np.concatenate([p.reshape(-1) for p in parts])
+    tabs = mh.RotaryTables(ctx, hd, T, 10000.0)
+    cos, sin = O.rope_tables(hd, T, 10000.0)
+    dx, dw = ctx.to_device(x), ctx.to_device(bw)
+    got = mh.block_forward(ctx, dx, dw, H, Hkv, ff, 1e-5, tabs).numpy()
+    want = O.block_forward(c, bw, cos, sin, x)
+    e = rel_max(got - x, want.astype(np.float64) - x)
+    print(f"  change: max|diff|/max|ref| {e:.3g}", flush=True)
+    assert e <= 2e-4
+    assert rel_max(got, want) <= 1e-5
+    # in place: out = x
+    again = mh.block_forward(ctx, dx, dw, H, Hkv, ff, 1e-5, tabs, out=dx).numpy()
+    assert np.array_equal(again, got)
+
+
+def test_block_forward_rejects_bad_arguments(ctx):
+    tabs = mh.RotaryTables(ctx, 8, 4, 10000.0)
+    x = ctx.to_device(np.zeros((1, 4, 16), np.float32))
+    w = ctx.to_device(np.zeros(16 * 200, np.float32))
+    with pytest.raises(mh.ShapeError):
+        mh.block_forward(ctx, x, w, 3, 1, 8, 1e-5, tabs)   # 16 % 3
+    with pytest.raises(mh.ShapeError):
+        mh.block_forward(ctx, x, w, 2, 3, 8, 1e-5, tabs)   # 2 % 3
+    with pytest.raises(mh.ArgumentError):
+        mh.block_forward(ctx, x, w, 2, 1, 8, 0.0, tabs)    # eps
+    with pytest.raises(mh.ArgumentError):
+        mh.block_forward(ctx, x, w, 2, 1, 0, 1e-5, tabs)   # d_ff
 
 
 @pytest.mark.parametrize("rows,d,ff", [(1, 1, 1), (64, 64, 176), (2048, 128, 344), (1024, 2048, 5632)])
