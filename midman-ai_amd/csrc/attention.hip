@@ -7,6 +7,7 @@
 // its last diagonal: every tile is loaded once with float4 loads into
 // registers, written to a double-buffered LDS stage, and shared by the four
 // waves; the next tile's loads are in flight while the current one is used.
+// (attn_fwd_split_kernel below covers small grids.)
 // Each wave keeps an online softmax for its rows, so no [T,T] tensor exists.
 //
 // The products are computed transposed so that every per-query quantity lives
@@ -46,16 +47,18 @@ struct AttnP {
 
 template <int HD>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
+    constexpr int NT = 256;                  // threads
+    constexpr int QB = 128;                  // query rows per workgroup
     constexpr int NS = HD / 2;               // S^T k-steps (lanes 32-63 take dims NS..HD-1)
     constexpr int NDB = (HD + 31) / 32;      // O^T row blocks; block db row i is dim NDB*i+db
     constexpr int KS = HD + 4;               // K row stride: 16-byte aligned rows
     constexpr int OS = HD + 1;               // output staging stride: odd, conflict-free
     constexpr int F4 = 32 * HD / 4;          // float4s per K or V tile
-    constexpr int PER = (F4 + 255) / 256;    // float4s per thread per tile
+    constexpr int PER = (F4 + NT - 1) / NT;  // float4s per thread per tile
     // Two K stages [32][KS] and two V stages [32][HD]; at the end the same
-    // memory holds the 4 waves' outputs as [128][OS].
+    // memory holds the waves' outputs as [QB][OS].
     constexpr int STAGES = 2 * 32 * KS + 2 * 32 * HD;
-    constexpr int OUT = 128 * OS;
+    constexpr int OUT = QB * OS;
     __shared__ __attribute__((aligned(16))) float smem[STAGES > OUT ? STAGES : OUT];
     auto Ks = [&](int buf) { return smem + buf * 32 * KS; };
     auto Vs = [&](int buf) { return smem + 64 * KS + buf * 32 * HD; };
@@ -66,8 +69,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     const int qblk = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
     const int kvh = head / (p.h / p.hkv);
     const int T = p.t;
-    const int q_first = qblk * 128;
-    const int q_last = min(q_first + 127, T - 1);
+    const int q_first = qblk * QB;
+    const int q_last = min(q_first + QB - 1, T - 1);
     const int ntiles = q_last / 32 + 1;            // key tiles the workgroup needs
     const int q0 = q_first + wave * 32;            // this wave's first query
     const int my_tiles = q0 < T ? q0 / 32 + 1 : 0; // tiles this wave needs
@@ -100,7 +103,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int f = tid + i * 256;
+            const int f = tid + i * NT;
             float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
             if (f < F4) {
                 const int j = (4 * f) / HD, c = (4 * f) % HD;
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     auto store_tile = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
-            const int f = tid + i * 256;
+            const int f = tid + i * NT;
             if (f < F4) {
                 const int j = (4 * f) / HD, c = (4 * f) % HD;
                 float *kd = Ks(buf) + j * KS + c;
@@ -261,6 +264,162 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     }
 }
 
+// Key-split variant for grids that would not cover the chip (few batch x head
+// pairs, short T: the tiny preset has 32 pairs of 256 rows). A workgroup owns
+// 32 query rows; its 4 waves take the key tiles up to the diagonal round-robin
+// (wave w: tiles w, w+4, ...), each keeping the online softmax of its share,
+// with K and V read straight from memory into the MFMA operand layouts (no
+// LDS staging; the next tile's loads are in flight during the current one).
+// The 4 partial states then merge through LDS in wave order: m = max m_w,
+// l = sum l_w 2^(m_w - m), O = sum O_w 2^(m_w - m) / l. Heads up to 64 wide.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_fwd_split_kernel(AttnP p) {
+    constexpr int NS = HD / 2;
+    constexpr int NDB = (HD + 31) / 32;
+    constexpr int OS = HD + 1;
+    __shared__ float sm_m[4][32], sm_l[4][32];
+    __shared__ float sm_o[4][32 * OS];
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int head = blockIdx.x, b = blockIdx.y;
+    const int qblk = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
+    const int kvh = head / (p.h / p.hkv);
+    const int T = p.t;
+    const int q0 = qblk * 32;
+    const int qi = q0 + lq;
+    const int ntiles = min(q0 + 31, T - 1) / 32 + 1;
+
+    const float *Q = p.q + b * p.sqb + head * p.sqh;
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+
+    float qr[NS];
+    {
+        const float *src = Q + (int64_t)min(qi, T - 1) * p.sqt + lh * NS;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) qr[s] = src[s];
+    }
+    // Operands of one key tile: kr[s] = K[key lq][lh*NS + s] (S^T's A), and
+    // vr[s][db] = V[key 8*(s/4) + 4*lh + s%4][NDB*lq + db] (O^T's A).
+    // kn/vn receive the wave's next tile while the current one is used.
+    float kr[NS], vr[16][NDB], kn[NS], vn[16][NDB];
+    auto load_tile = [&](int kt, float (&kd)[NS], float (&vd)[16][NDB])
+                         __attribute__((always_inline)) {
+        const int key = kt * 32 + lq;
+        const float *ks = K + (int64_t)min(key, T - 1) * p.skt + lh * NS;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) kd[s] = key < T ? ks[s] : 0.0f;
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int vk = kt * 32 + 8 * (s >> 2) + 4 * lh + (s & 3);
+            const float *vs = V + (int64_t)min(vk, T - 1) * p.svt + NDB * lq;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+                vd[s][db] = (vk < T && NDB * lq + db < HD) ? vs[db] : 0.0f;
+        }
+    };
+
+    floatx16 o[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
+    const float sc = p.scale * 1.4426950408889634f;
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    if (wave < ntiles) load_tile(wave, kr, vr);
+    for (int kt = wave; kt < ntiles; kt += 4) {
+        if (kt + 4 < ntiles) load_tile(kt + 4, kn, vn);
+        floatx16 sacc, sacc1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            sacc[r] = 0.0f;
+            sacc1[r] = 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < NS; s += 2) {
+            sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[s], qr[s], sacc, 0, 0, 0);
+            if (s + 1 < NS)
+                sacc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[s + 1], qr[s + 1], sacc1, 0, 0, 0);
+        }
+        const int k0 = kt * 32;
+        float pv[16];
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            const float sv = (sacc[r] + sacc1[r]) * sc;
+            pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
+            mloc = fmaxf(mloc, pv[r]);
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        const bool need = mloc > m_run + 8.0f;
+        if (__any(need)) {
+            const float m_new = need ? mloc : m_run;
+            const float alpha = exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+            m_run = m_new;
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            pv[r] = exp2f(pv[r] - m_run);
+            lsum += pv[r];
+        }
+        lsum += __shfl_xor(lsum, 32, 64);
+        l_run += lsum;
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+                o[db] = __builtin_amdgcn_mfma_f32_32x32x2f32(vr[s][db], pv[s], o[db], 0, 0, 0);
+#pragma unroll
+        for (int s = 0; s < NS; ++s) kr[s] = kn[s];
+#pragma unroll
+        for (int s = 0; s < 16; ++s)
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) vr[s][db] = vn[s][db];
+    }
+
+    if (lh == 0) {
+        sm_m[wave][lq] = m_run;
+        sm_l[wave][lq] = l_run;
+    }
+    __syncthreads();
+    float mx = sm_m[0][lq];
+#pragma unroll
+    for (int w = 1; w < 4; ++w) mx = fmaxf(mx, sm_m[w][lq]);
+    float L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) L += sm_l[w][lq] * exp2f(sm_m[w][lq] - mx);
+    const float f = exp2f(m_run - mx) / L;  // 0 for a wave that saw no key
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+            const int d = NDB * i + db;
+            if (d < HD) sm_o[wave][lq * OS + d] = o[db][r] * f;
+        }
+    if (p.lse && wave == 0 && lh == 0 && qi < T)
+        p.lse[((int64_t)b * p.h + head) * T + qi] = mx + log2f(L);
+    __syncthreads();
+    for (int idx = tid; idx < 32 * HD; idx += 256) {
+        const int j = idx / HD, c = idx - j * HD;
+        const int q = q0 + j;
+        if (q < T) {
+            const float v = ((sm_o[0][j * OS + c] + sm_o[1][j * OS + c]) + sm_o[2][j * OS + c]) +
+                            sm_o[3][j * OS + c];
+            p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = v;
+        }
+    }
+}
+
 // In-place RoPE (rope.rs:28-32) on heads of a strided layout: element
 // (b, h, t, p) at x[b*sb + h*sh + t*st + p], positions t = 0..T-1. One
 // workgroup per (b, t) row; its threads walk the row's nh*HD/2 rotation pairs.
@@ -293,7 +452,13 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(float *__restrict__ x, i
 }
 
 template <int HD>
-void launch_hd(Context &ctx, const AttnP &p, dim3 grid) {
+void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool split) {
+    if constexpr (HD <= 64) {
+        if (split) {
+            hipLaunchKernelGGL((attn_fwd_split_kernel<HD>), grid, dim3(256), 0, ctx.stream, p);
+            return;
+        }
+    }
     hipLaunchKernelGGL((attn_fwd_kernel<HD>), grid, dim3(256), 0, ctx.stream, p);
 }
 
@@ -369,16 +534,20 @@ void attention(Context &ctx, const AttnDesc &d) {
     p.h = (int)d.h;
     p.hkv = (int)d.hkv;
     p.t = (int)d.t;
-    p.nqb = (int)((d.t + 127) / 128);
+    // The key-split kernel when 128-row query blocks would leave CUs idle
+    // (heads up to 64 wide).
+    const int cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
+    const bool split = d.hd <= 64 && d.b * d.h * ((d.t + 127) / 128) < cus;
+    p.nqb = (int)(split ? (d.t + 31) / 32 : (d.t + 127) / 128);
     p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
     dim3 grid((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
     switch (d.hd) {
-        case 4: launch_hd<4>(ctx, p, grid); break;
-        case 8: launch_hd<8>(ctx, p, grid); break;
-        case 16: launch_hd<16>(ctx, p, grid); break;
-        case 32: launch_hd<32>(ctx, p, grid); break;
-        case 64: launch_hd<64>(ctx, p, grid); break;
-        default: launch_hd<128>(ctx, p, grid); break;
+        case 4: launch_hd<4>(ctx, p, grid, split); break;
+        case 8: launch_hd<8>(ctx, p, grid, split); break;
+        case 16: launch_hd<16>(ctx, p, grid, split); break;
+        case 32: launch_hd<32>(ctx, p, grid, split); break;
+        case 64: launch_hd<64>(ctx, p, grid, split); break;
+        default: launch_hd<128>(ctx, p, grid, split); break;
     }
     check_hip(hipGetLastError(), "attention launch");
 }

@@ -409,6 +409,269 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
         }
 }
 
+// ---- small-tile GEMM ---------------------------------------------------------
+// For shapes with fewer 128x128 tiles than CUs (the tiny preset's projections,
+// M = 2048 with N and K of a few hundred) the big tile leaves most of the chip
+// idle and every workgroup walks the whole K alone. Here a 256-thread
+// workgroup owns a 64x64 tile, each wave one 32x32 MFMA block (16
+// accumulators), K advancing 32 at a time, so the grid holds 4x the
+// workgroups. With so few steps per tile, latency rules: three steps of global
+// loads are kept in flight (a ring of register slots) ahead of the two LDS
+// stages, and each lane reads its operands of a step as four 16-byte LDS
+// reads. The epilogues match the big kernel's; in the SwiGLU epilogue the gate
+// and up columns of a pair sit in neighbouring lanes and meet through one lane
+// exchange.
+constexpr int SBM = 64, SBN = 64, SBK = 32;
+// LDS rows hold one output row (A) or column (B) with its 32 k values
+// contiguous, padded to 36 floats: a lane reads its 16 k values of a step as
+// four 16-byte reads, and eight consecutive rows fall in distinct 16-byte bank
+// groups.
+constexpr int SKS = SBK + 4;
+
+// The K loop of one 64x64 tile. MFMA kk of a step takes k = kk from lanes
+// 0-31 and k = 16 + kk from lanes 32-63 (any split of the step's k values
+// between the two lane halves gives the same sum; A and B agree on it).
+// FAST: every step is a full interior step (no predicates anywhere, so the
+// compiler can count the loads in flight exactly).
+template <bool TA, bool TB, bool FAST>
+__device__ __forceinline__ void small_mainloop(const KParams &p, const float *__restrict__ A,
+                                               const float *__restrict__ B, int64_t m0,
+                                               int64_t n0, int64_t kbeg, int nk, int64_t kend,
+                                               float (*As)[SBM][SKS], float (*Bs)[SBN][SKS],
+                                               floatx16 &acc) {
+    const int tid = threadIdx.x;
+    const int64_t M = p.m, N = p.n;
+    // A tile of each operand is 64 x 32 floats = 512 float4: thread tid moves
+    // float4 idx = tid + 256*i, i < 2. Operands stored row-major in k (A for
+    // nn/nt, B for nt): row idx/8, k (idx%8)*4. Operands stored k-major: k
+    // idx/16, row (idx%16)*4.
+    constexpr int PF = 3;  // k-steps of loads in flight
+    float4 ra[PF][2], rb[PF][2];
+    auto load = [&](int64_t k0, int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f), w = v;
+            if (!TA) {
+                const int64_t gm = m0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
+                const float *src = A + gm * p.lda + gk;
+                if (FAST) {
+                    v = *reinterpret_cast<const float4 *>(src);
+                } else if (gm < M) {
+                    if (gk + 0 < kend) v.x = src[0];
+                    if (gk + 1 < kend) v.y = src[1];
+                    if (gk + 2 < kend) v.z = src[2];
+                    if (gk + 3 < kend) v.w = src[3];
+                }
+            } else {
+                const int64_t gk = k0 + (idx >> 4), gm = m0 + (idx & 15) * 4;
+                const float *src = A + gk * p.lda + gm;
+                if (FAST) {
+                    v = *reinterpret_cast<const float4 *>(src);
+                } else if (gk < kend) {
+                    if (gm + 0 < M) v.x = src[0];
+                    if (gm + 1 < M) v.y = src[1];
+                    if (gm + 2 < M) v.z = src[2];
+                    if (gm + 3 < M) v.w = src[3];
+                }
+            }
+            if (!TB) {
+                const int64_t gk = k0 + (idx >> 4), gn = n0 + (idx & 15) * 4;
+                const float *src = B + gk * p.ldb + gn;
+                if (FAST) {
+                    w = *reinterpret_cast<const float4 *>(src);
+                } else if (gk < kend) {
+                    if (gn + 0 < N) w.x = src[0];
+                    if (gn + 1 < N) w.y = src[1];
+                    if (gn + 2 < N) w.z = src[2];
+                    if (gn + 3 < N) w.w = src[3];
+                }
+            } else {
+                const int64_t gn = n0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
+                const float *src = B + gn * p.ldb + gk;
+                if (FAST) {
+                    w = *reinterpret_cast<const float4 *>(src);
+                } else if (gn < N) {
+                    if (gk + 0 < kend) w.x = src[0];
+                    if (gk + 1 < kend) w.y = src[1];
+                    if (gk + 2 < kend) w.z = src[2];
+                    if (gk + 3 < kend) w.w = src[3];
+                }
+            }
+            ra[slot][i] = v;
+            rb[slot][i] = w;
+        }
+    };
+    auto store = [&](int buf, int slot) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int idx = tid + 256 * i;
+            const float4 va = ra[slot][i], vb = rb[slot][i];
+            if (!TA) {
+                *reinterpret_cast<float4 *>(&As[buf][idx >> 3][(idx & 7) * 4]) = va;
+            } else {
+                const int k = idx >> 4, row = (idx & 15) * 4;
+                As[buf][row + 0][k] = va.x;
+                As[buf][row + 1][k] = va.y;
+                As[buf][row + 2][k] = va.z;
+                As[buf][row + 3][k] = va.w;
+            }
+            if (!TB) {
+                const int k = idx >> 4, col = (idx & 15) * 4;
+                Bs[buf][col + 0][k] = vb.x;
+                Bs[buf][col + 1][k] = vb.y;
+                Bs[buf][col + 2][k] = vb.z;
+                Bs[buf][col + 3][k] = vb.w;
+            } else {
+                *reinterpret_cast<float4 *>(&Bs[buf][idx >> 3][(idx & 7) * 4]) = vb;
+            }
+        }
+    };
+
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+    auto compute = [&](int buf) __attribute__((always_inline)) {
+        const float4 *pa = reinterpret_cast<const float4 *>(&As[buf][wm * 32 + lr][16 * lk]);
+        const float4 *pb = reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + lr][16 * lk]);
+        float4 a[4], b[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            a[q] = pa[q];
+            b[q] = pb[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q].x, b[q].x, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q].y, b[q].y, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q].z, b[q].z, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q].w, b[q].w, acc, 0, 0, 0);
+        }
+    };
+
+    // Steps that do not fill a group of PF run first, one at a time. Then,
+    // per group, sub-iteration j (global step t) stores step t+1 from slot
+    // (j+1)%PF into the LDS stage not in use, loads step t+PF into slot j
+    // (whose step t went to LDS one sub-iteration earlier), runs the MFMAs of
+    // step t and ends with the one barrier. Slot indices are constants of the
+    // unrolled group and every load is issued unconditionally (past the last
+    // step they re-read it, from cache), so the wait before each store counts
+    // exactly the PF-2 younger steps and lets them stay in flight.
+    auto step_k = [&](int t) __attribute__((always_inline)) {
+        return kbeg + (int64_t)min(t, nk - 1) * SBK;
+    };
+    int t = 0;
+    for (; t < nk % PF; ++t) {
+        load(step_k(t), 0);
+        store(0, 0);
+        __syncthreads();
+        compute(0);
+        __syncthreads();
+    }
+    if (t == nk) return;
+#pragma unroll
+    for (int j = 0; j < PF; ++j) load(step_k(t + j), j);
+    store(0, 0);
+    __syncthreads();
+    for (int g = 0; t < nk; ++g, t += PF) {
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            const int cur = (g * PF + j) & 1;
+            store(cur ^ 1, (j + 1) % PF);
+            load(step_k(t + j + PF), j);
+            compute(cur);
+            __syncthreads();
+        }
+    }
+}
+
+template <bool TA, bool TB, int EPI>
+__global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
+    __shared__ __attribute__((aligned(16))) float As[2][SBM][SKS];
+    __shared__ __attribute__((aligned(16))) float Bs[2][SBN][SKS];
+
+    const int tid = threadIdx.x;
+    const int bid = blockIdx.x;
+    const int tm = bid / p.tiles_n, tn = bid - (bid / p.tiles_n) * p.tiles_n;
+    const int64_t m0 = (int64_t)tm * SBM, n0 = (int64_t)tn * SBN;
+    const int64_t batch = blockIdx.y;
+    const int split = blockIdx.z;
+    const float *__restrict__ A = p.a + batch * p.stride_a;
+    const float *__restrict__ B = p.b + batch * p.stride_b;
+    const int64_t kbeg = (int64_t)split * p.k_per_split;
+    const int64_t kend = min(p.k, kbeg + p.k_per_split);
+    const int64_t M = p.m, N = p.n;
+
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    const int nk = (int)((kend - kbeg + SBK - 1) / SBK);
+    if (p.vec_a && p.vec_b && m0 + SBM <= M && n0 + SBN <= N) {
+        // interior: the full steps branch-free, then a K tail (if any) on the
+        // predicated path, after the last barrier of the full steps
+        const int nfull = (int)((kend - kbeg) / SBK);
+        small_mainloop<TA, TB, true>(p, A, B, m0, n0, kbeg, nfull, kend, As, Bs, acc);
+        if (nfull < nk)
+            small_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg + (int64_t)nfull * SBK, 1, kend,
+                                          As, Bs, acc);
+    } else {
+        small_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg, nk, kend, As, Bs, acc);
+    }
+
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31, lk = lane >> 5;
+    // Register r of lane l is C[row][col], row = m0 + wm*32 + 8*(r/4) +
+    // 4*(l/32) + r%4, col = n0 + wn*32 + l%32.
+    const int64_t col = n0 + wn * 32 + lr;
+    auto row_of = [&](int r) { return m0 + wm * 32 + 8 * (r >> 2) + 4 * lk + (r & 3); };
+    if (p.splits > 1) {
+        float *P = p.partial + (int64_t)split * M * N;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = row_of(r);
+            if (row < M && col < N) P[row * N + col] = acc[r];
+        }
+        return;
+    }
+    float *C = p.c + batch * p.stride_c;
+    if (EPI == EPI_SWIGLU) {
+        // gate f at column 2f (even lane), up f at 2f+1 (the next lane)
+        const bool even = (lr & 1) == 0;
+        const int64_t f = col >> 1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float up = __shfl_xor(acc[r], 1, 64);
+            const int64_t row = row_of(r);
+            if (!even || row >= M) continue;
+            if (p.aux && col + 1 < N)
+                *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) =
+                    make_float2(acc[r], up);
+            if (f < p.swiglu_ff) C[row * p.ldc + f] = __fmul_rn(silu_f(acc[r]), up);
+        }
+        return;
+    }
+    if (EPI == EPI_SWIGLU_BWD) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = row_of(r);
+            if (row >= M || col >= N) continue;
+            const float2 gu = *reinterpret_cast<const float2 *>(p.aux + row * p.ldaux + 2 * col);
+            const float2 o = swiglu_bwd_f(acc[r], gu.x, gu.y);
+            *reinterpret_cast<float2 *>(C + row * p.ldc + 2 * col) = o;
+        }
+        return;
+    }
+    const float *R = p.resid ? p.resid + batch * p.stride_c : C;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = row_of(r);
+        if (row >= M || col >= N) continue;
+        const float v = acc[r];
+        C[row * p.ldc + col] = EPI == EPI_ACCUM ? __fadd_rn(R[row * p.ldc + col], v) : v;
+    }
+}
+
 // Sums split partials in split order, then applies the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial,
@@ -429,16 +692,19 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ p
 }
 
 template <bool TA, bool TB, int EPI>
-void launch(Context &ctx, const KParams &p, dim3 grid) {
-    hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI>), grid, dim3(256), 0, ctx.stream, p);
+void launch(Context &ctx, const KParams &p, dim3 grid, bool small) {
+    if (small)
+        hipLaunchKernelGGL((gemm_f32_mfma_small<TA, TB, EPI>), grid, dim3(256), 0, ctx.stream, p);
+    else
+        hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI>), grid, dim3(256), 0, ctx.stream, p);
 }
 
 template <int EPI>
-void dispatch_t(Context &ctx, bool ta, bool tb, const KParams &p, dim3 grid) {
-    if (!ta && !tb) launch<false, false, EPI>(ctx, p, grid);
-    else if (!ta && tb) launch<false, true, EPI>(ctx, p, grid);
-    else if (ta && !tb) launch<true, false, EPI>(ctx, p, grid);
-    else launch<true, true, EPI>(ctx, p, grid);
+void dispatch_t(Context &ctx, bool ta, bool tb, const KParams &p, dim3 grid, bool small) {
+    if (!ta && !tb) launch<false, false, EPI>(ctx, p, grid, small);
+    else if (!ta && tb) launch<false, true, EPI>(ctx, p, grid, small);
+    else if (ta && !tb) launch<true, false, EPI>(ctx, p, grid, small);
+    else launch<true, true, EPI>(ctx, p, grid, small);
 }
 
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
@@ -471,8 +737,13 @@ void gemm(Context &ctx, const GemmDesc &d) {
             fail(MMH_ERR_ARGUMENT, "gemm: swiglu pairs need 16-byte aligned rows of >= 2n");
         if (d.batch != 1) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogues take one matrix");
     }
-    p.tiles_m = (int)((d.m + BM - 1) / BM);
-    p.tiles_n = (int)((d.n + BN - 1) / BN);
+    const int cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
+    // Small tiles when the big ones cannot fill the chip and K is short
+    // enough that one workgroup walking it alone stays cheap.
+    const int64_t big_tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN) * d.batch;
+    const bool small = d.force_splits == 0 && big_tiles < cus && d.k <= 1024;
+    p.tiles_m = (int)(small ? (d.m + SBM - 1) / SBM : (d.m + BM - 1) / BM);
+    p.tiles_n = (int)(small ? (d.n + SBN - 1) / SBN : (d.n + BN - 1) / BN);
     // The interior path addresses a tile with byte offsets below 2^31 (128 rows of ld).
     const int64_t off_limit = int64_t(1) << 29;
     p.vec_a = (d.lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(d.a) &&
@@ -483,18 +754,28 @@ void gemm(Context &ctx, const GemmDesc &d) {
               (reinterpret_cast<uintptr_t>(d.c) & 7) == 0;
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-    const int64_t ktiles = (d.k + BK - 1) / BK;
+    const int64_t ktiles = (d.k + (small ? SBK : BK) - 1) / (small ? SBK : BK);
     int splits = 1;
     if (d.force_splits > 0) {
         splits = d.force_splits;
     } else if (d.batch == 1 && d.epi != EPI_SWIGLU && d.epi != EPI_SWIGLU_BWD) {
-        // Fill the chip: at least two tiles per CU, at least 8 K-steps per split.
-        const int64_t target = 2 * (int64_t)(ctx.cu_count > 0 ? ctx.cu_count : 256);
-        while (tiles * splits < target && splits < 16 && ktiles / (splits * 2) >= 8) splits *= 2;
+        if (small) {
+            // Split only while a split keeps >= 8 steps of 32 (the reduce
+            // launch costs about what 8 steps do) and the grid is below a
+            // workgroup per CU.
+            while (tiles * splits < cus && splits < 16 && ktiles / (splits * 2) >= 8)
+                splits *= 2;
+        } else {
+            // Fill the chip: at least two tiles per CU, at least 8 K-steps per split.
+            const int64_t target = 2 * (int64_t)cus;
+            while (tiles * splits < target && splits < 16 && ktiles / (splits * 2) >= 8)
+                splits *= 2;
+        }
     }
     if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD) splits = 1;
+    const int64_t kstep = small ? SBK : BK;
     const int64_t kt_per = (ktiles + splits - 1) / splits;
-    p.k_per_split = kt_per * BK;
+    p.k_per_split = kt_per * kstep;
     splits = (int)((ktiles + kt_per - 1) / kt_per);
     p.splits = splits;
     if (splits > 1) p.partial = static_cast<float *>(ctx.get_scratch((size_t)splits * d.m * d.n * 4));
@@ -504,14 +785,14 @@ void gemm(Context &ctx, const GemmDesc &d) {
     const int epi = splits > 1 ? EPI_STORE : d.epi;
     if (epi == EPI_SWIGLU) {
         if (d.ta || d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogue needs the nn form");
-        launch<false, false, EPI_SWIGLU>(ctx, p, grid);
+        launch<false, false, EPI_SWIGLU>(ctx, p, grid, small);
     } else if (epi == EPI_SWIGLU_BWD) {
         if (d.ta || !d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu backward epilogue needs the nt form");
-        launch<false, true, EPI_SWIGLU_BWD>(ctx, p, grid);
+        launch<false, true, EPI_SWIGLU_BWD>(ctx, p, grid, small);
     } else if (epi == EPI_ACCUM) {
-        dispatch_t<EPI_ACCUM>(ctx, d.ta, d.tb, p, grid);
+        dispatch_t<EPI_ACCUM>(ctx, d.ta, d.tb, p, grid, small);
     } else {
-        dispatch_t<EPI_STORE>(ctx, d.ta, d.tb, p, grid);
+        dispatch_t<EPI_STORE>(ctx, d.ta, d.tb, p, grid, small);
     }
     check_hip(hipGetLastError(), "gemm launch");
     if (splits > 1) {
