@@ -12,7 +12,8 @@
 //       dP^T  = V . dO^T, dS^T = P^T * (dP^T - D)
 //       dQ^T += K^T . dS^T                             (dS^T straight from the
 //                                                      accumulators)
-//   dkv kernel (one workgroup = 4 waves x 32 keys of one (batch, kv head)):
+//   dkv kernel (one workgroup = 4 waves x 32 keys of one (batch, kv head),
+//   or of one query head when GQA partials are wanted, see below):
 //       for every query head of the group and every query tile at or after
 //       the keys: S = Q . K^T, P, dP = dO . V^T, dS as above,
 //       dV^T += dO^T . P and dK^T += Q^T . dS
@@ -22,9 +23,15 @@
 // 8*(r/4) + 4*(l/32) + r%4), a product whose B operand is an accumulator
 // block is summed over the accumulator's rows in that permuted order, which
 // the A operand follows. Summing the group's heads inside one workgroup (in
-// head order) makes dK and dV deterministic without atomics. The gradient of
+// head order) makes dK and dV deterministic without atomics. With GQA and a
+// scratch buffer, each query head gets its own workgroups instead (twice the
+// grid at 2 heads per kv head, so the long key blocks near the start of the
+// sequence no longer leave CUs waiting) and writes its partial dK, dV; a
+// second kernel sums a group's partials in head order. The gradient of
 // the scaled scores is dS*scale (attention.rs:83), applied to dQ and dK at
 // the end. Entries above the diagonal have P = 0 and contribute nothing.
+#include <algorithm>
+
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -36,6 +43,7 @@ struct BwdP {
     const float *q, *k, *v, *o, *dout, *lse;
     float *dq, *dk, *dv, *dvec;
     int64_t sqb, sqh, sqt, skb, skh, skt, svb, svh, svt, sob, soh, sot;
+    float *part;  // per-query-head partial dK, dV [2][B][H][T][hd], or null
     int h, hkv, t, nqb, nkb;
     float scale;
 };
@@ -270,10 +278,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lq = lane & 31, lh = lane >> 5;
-    const int kvh = blockIdx.x, b = blockIdx.y;
+    const int groups = p.h / p.hkv;
+    // kv head and the group's heads this workgroup covers: all of them, or
+    // one (query head blockIdx.x) when writing partials
+    const int kvh = p.part ? (int)blockIdx.x / groups : (int)blockIdx.x;
+    const int g0 = p.part ? (int)blockIdx.x - kvh * groups : 0;
+    const int ng = p.part ? 1 : groups;
+    const int b = blockIdx.y;
     const int kblk = blockIdx.z;  // block 0 sees the most queries and starts first
     const int T = p.t;
-    const int groups = p.h / p.hkv;
     const int k_first = kblk * 128;
     const int k0 = k_first + wave * 32;  // this wave's first key
     const int kj = k0 + lq;
@@ -281,7 +294,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
     const int qt_first = k_first / 32;
     const int nqt = (T + 31) / 32;
     const int per_head = nqt - qt_first;
-    const int total = groups * per_head;
+    const int total = ng * per_head;
     const int my_first = k0 / 32;  // query tiles before this one are all above the keys
 
     const float *K = p.k + b * p.skb + kvh * p.skh;
@@ -295,7 +308,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
     auto load_tile = [&](int it) __attribute__((always_inline)) {
         const int g = it / per_head;
         const int qt = qt_first + (it - g * per_head);
-        const int head = kvh * groups + g;
+        const int head = kvh * groups + g0 + g;
         const float *Qh = p.q + b * p.sqb + head * p.sqh;
         const float *Gh = p.dout + b * p.sob + head * p.soh;
 #pragma unroll
@@ -418,8 +431,16 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
         }
         __syncthreads();
         if (k0 < T) {
-            float *dst = which == 0 ? p.dk + b * p.skb + kvh * p.skh : p.dv + b * p.svb + kvh * p.svh;
-            const int64_t st = which == 0 ? p.skt : p.svt;
+            float *dst;
+            int64_t st;
+            if (p.part) {
+                const int64_t plane = (int64_t)gridDim.y * p.h * T * HD;
+                dst = p.part + which * plane + ((int64_t)b * p.h + blockIdx.x) * T * HD;
+                st = HD;
+            } else {
+                dst = which == 0 ? p.dk + b * p.skb + kvh * p.skh : p.dv + b * p.svb + kvh * p.svh;
+                st = which == 0 ? p.skt : p.svt;
+            }
             for (int idx = lane; idx < 32 * HD; idx += 64) {
                 const int j = idx / HD, c = idx - j * HD;
                 const int key = k0 + j;
@@ -430,9 +451,45 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
     }
 }
 
+// dK, dV of kv head j = the sum of its group's partials in head order.
+// One thread per 4 consecutive dims of one (batch, kv head, key).
+__global__ __launch_bounds__(256) void dkv_group_sum_kernel(const float *__restrict__ part, int b,
+                                                            int h, int hkv, int t, int hd,
+                                                            float *dk, int64_t skb, int64_t skh,
+                                                            int64_t skt, float *dv, int64_t svb,
+                                                            int64_t svh, int64_t svt) {
+    const int groups = h / hkv, q4 = hd / 4;
+    const int64_t n = (int64_t)b * hkv * t * q4;
+    const int64_t plane = (int64_t)b * h * t * hd;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % q4) * 4;
+        const int64_t r = i / q4;
+        const int key = (int)(r % t);
+        const int64_t bk = r / t;
+        const int kvh = (int)(bk % hkv), bb = (int)(bk / hkv);
+        const float *src = part + (((int64_t)bb * h + (int64_t)kvh * groups) * t + key) * hd + c;
+        float4 a = *reinterpret_cast<const float4 *>(src);
+        float4 v = *reinterpret_cast<const float4 *>(src + plane);
+        for (int g = 1; g < groups; ++g) {
+            const float4 x = *reinterpret_cast<const float4 *>(src + (int64_t)g * t * hd);
+            const float4 y = *reinterpret_cast<const float4 *>(src + plane + (int64_t)g * t * hd);
+            a = make_float4(a.x + x.x, a.y + x.y, a.z + x.z, a.w + x.w);
+            v = make_float4(v.x + y.x, v.y + y.y, v.z + y.z, v.w + y.w);
+        }
+        *reinterpret_cast<float4 *>(dk + bb * skb + kvh * skh + (int64_t)key * skt + c) = a;
+        *reinterpret_cast<float4 *>(dv + bb * svb + kvh * svh + (int64_t)key * svt + c) = v;
+    }
+}
+
 bool al16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 }  // namespace
+
+int64_t attention_backward_scratch_floats(int64_t b, int64_t h, int64_t hkv, int64_t t,
+                                          int64_t hd) {
+    return h > hkv ? 2 * b * h * t * hd : 0;
+}
 
 void attention_backward(Context &ctx, const AttnBwdDesc &d) {
     if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
@@ -471,8 +528,11 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
     p.nqb = (int)((d.t + 127) / 128);
     p.nkb = p.nqb;
     p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
+    // GQA: per-query-head partials when the caller gave room for them and the
+    // head is wide enough for the float4 sum (hd >= 4 always holds).
+    p.part = d.h > d.hkv && d.scratch ? d.scratch : nullptr;
     const dim3 gq((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
-    const dim3 gk((unsigned)d.hkv, (unsigned)d.b, (unsigned)p.nkb);
+    const dim3 gk((unsigned)(p.part ? d.h : d.hkv), (unsigned)d.b, (unsigned)p.nkb);
     const dim3 blk(256);
 #define MMH_BWD_CASE(HD)                                                                   \
     case HD:                                                                               \
@@ -489,6 +549,14 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
     }
 #undef MMH_BWD_CASE
     check_hip(hipGetLastError(), "attention backward launch");
+    if (p.part) {
+        const int64_t n4 = d.b * d.hkv * d.t * (d.hd / 4);
+        const unsigned blocks = (unsigned)std::min<int64_t>((n4 + 255) / 256, 4096);
+        hipLaunchKernelGGL(dkv_group_sum_kernel, dim3(blocks), dim3(256), 0, ctx.stream, p.part,
+                           (int)d.b, (int)d.h, (int)d.hkv, (int)d.t, (int)d.hd, d.dk, d.skb,
+                           d.skh, d.skt, d.dv, d.svb, d.svh, d.svt);
+        check_hip(hipGetLastError(), "dk/dv group sum launch");
+    }
     if (d.cos_t) {
         if (d.dk == d.dq + d.h * d.sqh && d.skb == d.sqb && d.skh == d.sqh && d.skt == d.sqt) {
             launch_rope_strided(ctx, d.dq, d.sqb, d.sqh, d.sqt, d.b, d.h + d.hkv, d.t, d.hd,

@@ -165,7 +165,13 @@ struct AttnBwdDesc {
     int64_t sob, soh, sot;
     int64_t b, h, hkv, t, hd;
     const float *cos_t = nullptr, *sin_t = nullptr;
+    // Optional, attention_backward_scratch_floats() floats: with GQA the
+    // query heads then run as separate workgroups (better balanced) and their
+    // partial dK, dV are summed in head order.
+    float *scratch = nullptr;
 };
+int64_t attention_backward_scratch_floats(int64_t b, int64_t h, int64_t hkv, int64_t t,
+                                          int64_t hd);
 void attention_backward(Context &ctx, const AttnBwdDesc &d);
 // In-place RoPE on strided heads; inverse rotates by -angle (the backward).
 void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,

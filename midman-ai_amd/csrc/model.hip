@@ -224,7 +224,8 @@ struct Model {
         float *xs = nullptr, *xn1 = nullptr, *qkv = nullptr, *cb = nullptr, *lse = nullptr,
               *hres = nullptr, *xn2 = nullptr, *gu = nullptr, *h = nullptr, *xnf = nullptr,
               *dx = nullptr, *dy = nullptr, *dxn = nullptr, *dctx = nullptr, *dqkv = nullptr,
-              *dvec = nullptr, *wtmp = nullptr, *rms = nullptr, *norm = nullptr;
+              *dvec = nullptr, *wtmp = nullptr, *rms = nullptr, *norm = nullptr,
+              *apart = nullptr;  // attention backward's per-head dK, dV (GQA)
         double *norm_scratch = nullptr;
         int32_t *uniq = nullptr, *start = nullptr, *order = nullptr;
         int64_t n_unique = 0;
@@ -521,6 +522,7 @@ struct Model {
             al(d * wcols),                  // wtmp
             al(rms_norm_backward_scratch(n, d)),  // rms
             64,                             // norm
+            al(attention_backward_scratch_floats(1, cfg.heads, cfg.kv_heads, n, cfg.hd())),
             al(global_norm_scratch_bytes() / 4),  // norm_scratch (doubles)
             al(n), al(n + 1), al(n),        // uniq, start, order (int32)
         };
@@ -530,9 +532,9 @@ struct Model {
         float *p = tr.mem;
         float **slots[] = {&tr.xs,   &tr.xn1, &tr.qkv,  &tr.cb,   &tr.lse,  &tr.hres, &tr.xn2,
                            &tr.gu,   &tr.h,   &tr.xnf,  &tr.dx,   &tr.dy,   &tr.dxn,  &tr.dctx,
-                           &tr.dqkv, &tr.dvec, &tr.wtmp, &tr.rms, &tr.norm};
+                           &tr.dqkv, &tr.dvec, &tr.wtmp, &tr.rms, &tr.norm, &tr.apart};
         int i = 0;
-        for (; i < 19; ++i) {
+        for (; i < 20; ++i) {
             *slots[i] = p;
             p += sizes[i];
         }
@@ -726,6 +728,7 @@ struct Model {
             ab.hd = hd;
             ab.cos_t = cos_t;
             ab.sin_t = sin_t;
+            ab.scratch = cfg.kv_heads < cfg.heads ? tr.apart : nullptr;
             attention_backward(c, ab);
             gemm(c, desc(tr.dqkv, false, qc, wqkv(l), true, qc, tr.dxn, d, n, qc, d));
             gemm(c, desc(xn1, true, d, tr.dqkv, false, qc, tr.wtmp, qc, d, n, qc));

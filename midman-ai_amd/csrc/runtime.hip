@@ -705,8 +705,10 @@ int32_t mmh_causal_attention_backward(mmh_handle ctx, const float *q, const floa
         const int64_t rows = b * h * t;
         const size_t o_floats = ((size_t)(rows * hd) + 63) / 64 * 64;
         const size_t r_floats = ((size_t)rows + 63) / 64 * 64;
-        float *o = static_cast<float *>(cx.workspace(2, (o_floats + 2 * r_floats) * 4));
-        float *lse = o + o_floats, *dvec = lse + r_floats;
+        const size_t s_floats = (size_t)attention_backward_scratch_floats(b, h, hkv, t, hd);
+        float *o = static_cast<float *>(
+            cx.workspace(2, (o_floats + 2 * r_floats + s_floats) * 4));
+        float *lse = o + o_floats, *dvec = lse + r_floats, *part = dvec + r_floats;
         AttnDesc f{};
         f.q = q;
         f.k = k;
@@ -751,6 +753,7 @@ int32_t mmh_causal_attention_backward(mmh_handle ctx, const float *q, const floa
         g.hkv = hkv;
         g.t = t;
         g.hd = hd;
+        g.scratch = s_floats ? part : nullptr;
         attention_backward(cx, g);
         return MMH_OK;
     });
