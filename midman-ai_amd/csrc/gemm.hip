@@ -63,6 +63,11 @@ struct KParams {
     int tiles_m, tiles_n;
     int splits;
     int vec_a, vec_b, vec_c;
+    // small kernel only: A-row RMSNorm in the loads, RoPE in the epilogue
+    const float *norm_w;
+    float norm_eps;
+    const float *rope_cos, *rope_sin;
+    int rope_seq, rope_hd, rope_cols;
 };
 
 __device__ __forceinline__ float silu_f(float x) {
@@ -433,12 +438,12 @@ constexpr int SKS = SBK + 4;
 // between the two lane halves gives the same sum; A and B agree on it).
 // FAST: every step is a full interior step (no predicates anywhere, so the
 // compiler can count the loads in flight exactly).
-template <bool TA, bool TB, bool FAST>
+template <bool TA, bool TB, bool FAST, bool NORM>
 __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__restrict__ A,
                                                const float *__restrict__ B, int64_t m0,
                                                int64_t n0, int64_t kbeg, int nk, int64_t kend,
                                                float (*As)[SBM][SKS], float (*Bs)[SBN][SKS],
-                                               floatx16 &acc) {
+                                               floatx16 &acc, float (&ss)[2]) {
     const int tid = threadIdx.x;
     const int64_t M = p.m, N = p.n;
     // A tile of each operand is 64 x 32 floats = 512 float4: thread tid moves
@@ -446,8 +451,23 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
     // nn/nt, B for nt): row idx/8, k (idx%8)*4. Operands stored k-major: k
     // idx/16, row (idx%16)*4.
     constexpr int PF = 3;  // k-steps of loads in flight
-    float4 ra[PF][2], rb[PF][2];
+    float4 ra[PF][2], rb[PF][2], rw[PF];  // rw: the norm weights of A's k values
     auto load = [&](int64_t k0, int slot) __attribute__((always_inline)) {
+        if (NORM) {
+            // both of a thread's A float4 cover k = k0 + (tid%8)*4 .. +3
+            const int64_t gk = k0 + (tid & 7) * 4;
+            const float *wk = p.norm_w + gk;
+            float4 w4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (FAST) {
+                w4 = *reinterpret_cast<const float4 *>(wk);
+            } else {
+                if (gk + 0 < kend) w4.x = wk[0];
+                if (gk + 1 < kend) w4.y = wk[1];
+                if (gk + 2 < kend) w4.z = wk[2];
+                if (gk + 3 < kend) w4.w = wk[3];
+            }
+            rw[slot] = w4;
+        }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
@@ -502,11 +522,28 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
             rb[slot][i] = w;
         }
     };
-    auto store = [&](int buf, int slot) __attribute__((always_inline)) {
+    // real: the slot holds a k-step not yet summed (the ring's last stores
+    // repeat the final step into the idle stage; those must not count)
+    auto store = [&](int buf, int slot, bool real) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
-            const float4 va = ra[slot][i], vb = rb[slot][i];
+            float4 va = ra[slot][i];
+            const float4 vb = rb[slot][i];
+            if (NORM) {
+                // the row's sum of squares as its values pass, and x * w; the
+                // row's 1/rms scales the products in the epilogue
+                const float4 w4 = rw[slot];
+                float t = __fadd_rn(ss[i], __fmul_rn(va.x, va.x));
+                t = __fadd_rn(t, __fmul_rn(va.y, va.y));
+                t = __fadd_rn(t, __fmul_rn(va.z, va.z));
+                t = __fadd_rn(t, __fmul_rn(va.w, va.w));
+                ss[i] = real ? t : ss[i];
+                va.x = __fmul_rn(va.x, w4.x);
+                va.y = __fmul_rn(va.y, w4.y);
+                va.z = __fmul_rn(va.z, w4.z);
+                va.w = __fmul_rn(va.w, w4.w);
+            }
             if (!TA) {
                 *reinterpret_cast<float4 *>(&As[buf][idx >> 3][(idx & 7) * 4]) = va;
             } else {
@@ -563,7 +600,7 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
     int t = 0;
     for (; t < nk % PF; ++t) {
         load(step_k(t), 0);
-        store(0, 0);
+        store(0, 0, true);
         __syncthreads();
         compute(0);
         __syncthreads();
@@ -571,13 +608,13 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
     if (t == nk) return;
 #pragma unroll
     for (int j = 0; j < PF; ++j) load(step_k(t + j), j);
-    store(0, 0);
+    store(0, 0, true);
     __syncthreads();
     for (int g = 0; t < nk; ++g, t += PF) {
 #pragma unroll
         for (int j = 0; j < PF; ++j) {
             const int cur = (g * PF + j) & 1;
-            store(cur ^ 1, (j + 1) % PF);
+            store(cur ^ 1, (j + 1) % PF, t + j + 1 < nk);
             load(step_k(t + j + PF), j);
             compute(cur);
             __syncthreads();
@@ -585,10 +622,11 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
     }
 }
 
-template <bool TA, bool TB, int EPI>
+template <bool TA, bool TB, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
     __shared__ __attribute__((aligned(16))) float As[2][SBM][SKS];
     __shared__ __attribute__((aligned(16))) float Bs[2][SBN][SKS];
+    __shared__ float sm_inv[SBM];  // NORM: 1/rms of the tile's rows
 
     const int tid = threadIdx.x;
     const int bid = blockIdx.x;
@@ -605,17 +643,43 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    // NORM: sums of squares of this thread's two A rows (the loads give
+    // thread tid rows tid/8 and 32 + tid/8 at every K-step), gathered as the
+    // values pass through the LDS stores.
+    float ss[2] = {0.0f, 0.0f};
     const int nk = (int)((kend - kbeg + SBK - 1) / SBK);
     if (p.vec_a && p.vec_b && m0 + SBM <= M && n0 + SBN <= N) {
         // interior: the full steps branch-free, then a K tail (if any) on the
         // predicated path, after the last barrier of the full steps
         const int nfull = (int)((kend - kbeg) / SBK);
-        small_mainloop<TA, TB, true>(p, A, B, m0, n0, kbeg, nfull, kend, As, Bs, acc);
+        small_mainloop<TA, TB, true, NORM>(p, A, B, m0, n0, kbeg, nfull, kend, As, Bs, acc,
+                                           ss);
         if (nfull < nk)
-            small_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg + (int64_t)nfull * SBK, 1, kend,
-                                          As, Bs, acc);
+            small_mainloop<TA, TB, false, NORM>(p, A, B, m0, n0, kbeg + (int64_t)nfull * SBK, 1,
+                                                kend, As, Bs, acc, ss);
     } else {
-        small_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg, nk, kend, As, Bs, acc);
+        small_mainloop<TA, TB, false, NORM>(p, A, B, m0, n0, kbeg, nk, kend, As, Bs, acc, ss);
+    }
+    // NORM: each row's 1/rms = (sum/K + eps)^-1/2 (norm.rs:21-39) combined
+    // over the row's 8 threads, through LDS to the lanes holding its results,
+    // which scale their accumulators by it before any epilogue
+    if (NORM) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float t = ss[i];
+            t = __fadd_rn(t, __shfl_xor(t, 1, 64));
+            t = __fadd_rn(t, __shfl_xor(t, 2, 64));
+            t = __fadd_rn(t, __shfl_xor(t, 4, 64));
+            const float mean = __fmul_rn(t, __fdiv_rn(1.0f, (float)p.k));
+            if ((tid & 7) == 0)
+                sm_inv[((tid + 256 * i) >> 3)] =
+                    __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, p.norm_eps)));
+        }
+        __syncthreads();
+        const int lw = tid >> 6, ll = tid & 63;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            acc[r] = __fmul_rn(acc[r], sm_inv[(lw >> 1) * 32 + 8 * (r >> 2) + 4 * (ll >> 5) + (r & 3)]);
     }
 
     const int lane = tid & 63, wave = tid >> 6;
@@ -625,6 +689,7 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
     // 4*(l/32) + r%4, col = n0 + wn*32 + l%32.
     const int64_t col = n0 + wn * 32 + lr;
     auto row_of = [&](int r) { return m0 + wm * 32 + 8 * (r >> 2) + 4 * lk + (r & 3); };
+
     if (p.splits > 1) {
         float *P = p.partial + (int64_t)split * M * N;
 #pragma unroll
@@ -662,6 +727,28 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
         }
         return;
     }
+    if (EPI == EPI_STORE && p.rope_cos) {
+        // rope.rs:28-32 on heads of rope_hd (<= 32, dividing 32) columns: the
+        // pair (c, c + hd/2) of a head sits in lanes lr and lr ^ hd/2.
+        const int hd = p.rope_hd, half = hd >> 1;
+        const int pc = (int)(col % hd);
+        const bool rot = col < p.rope_cols;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float other = __shfl_xor(acc[r], half, 64);
+            const int64_t row = row_of(r);
+            if (row >= M || col >= N) continue;
+            float v = acc[r];
+            if (rot) {
+                const int64_t pos = row % p.rope_seq;
+                const int c = pc < half ? pc : pc - half;
+                const float cs = p.rope_cos[pos * half + c], sn = p.rope_sin[pos * half + c];
+                v = pc < half ? v * cs - other * sn : v * cs + other * sn;
+            }
+            C[row * p.ldc + col] = v;
+        }
+        return;
+    }
     const float *R = p.resid ? p.resid + batch * p.stride_c : C;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -693,8 +780,16 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ p
 
 template <bool TA, bool TB, int EPI>
 void launch(Context &ctx, const KParams &p, dim3 grid, bool small) {
+    if constexpr (!TA && !TB && (EPI == EPI_STORE || EPI == EPI_SWIGLU)) {
+        if (small && p.norm_w) {
+            hipLaunchKernelGGL((gemm_f32_mfma_small<false, false, EPI, true>), grid, dim3(256), 0,
+                               ctx.stream, p);
+            return;
+        }
+    }
     if (small)
-        hipLaunchKernelGGL((gemm_f32_mfma_small<TA, TB, EPI>), grid, dim3(256), 0, ctx.stream, p);
+        hipLaunchKernelGGL((gemm_f32_mfma_small<TA, TB, EPI, false>), grid, dim3(256), 0,
+                           ctx.stream, p);
     else
         hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI>), grid, dim3(256), 0, ctx.stream, p);
 }
@@ -710,6 +805,36 @@ void dispatch_t(Context &ctx, bool ta, bool tb, const KParams &p, dim3 grid, boo
 bool aligned16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }
 
 }  // namespace
+
+namespace {
+
+int cus_of(const Context &ctx) { return ctx.cu_count > 0 ? ctx.cu_count : 256; }
+
+// Small tiles when the big ones cannot fill the chip and K is short enough
+// that one workgroup walking it alone stays cheap.
+bool use_small(const Context &ctx, const GemmDesc &d) {
+    const int64_t big_tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN) * d.batch;
+    return d.force_splits == 0 && big_tiles < cus_of(ctx) && d.k <= 1024;
+}
+
+bool vec_a_of(const GemmDesc &d, const float *a, int64_t lda) {
+    const int64_t off_limit = int64_t(1) << 29;  // interior byte offsets stay below 2^31
+    return (lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(a) &&
+           lda * BM < off_limit;
+}
+
+}  // namespace
+
+GemmFusion gemm_fusion(const Context &ctx, const GemmDesc &d) {
+    GemmFusion f;
+    const bool small = use_small(ctx, d);
+    f.norm = small && !d.ta && !d.tb && d.batch == 1 && d.k <= 256 && d.k % 4 == 0 &&
+             vec_a_of(d, d.a, d.lda) && aligned16(d.norm_w) &&
+             (d.epi == EPI_STORE || d.epi == EPI_SWIGLU);
+    f.rope = small && d.batch == 1 && d.epi == EPI_STORE && d.rope_hd > 0 &&
+             d.rope_hd <= 32 && 32 % d.rope_hd == 0;
+    return f;
+}
 
 void gemm(Context &ctx, const GemmDesc &d) {
     if (d.m <= 0 || d.n <= 0 || d.k <= 0 || d.batch <= 0) fail(MMH_ERR_SHAPE, "gemm: empty shape");
@@ -737,21 +862,34 @@ void gemm(Context &ctx, const GemmDesc &d) {
             fail(MMH_ERR_ARGUMENT, "gemm: swiglu pairs need 16-byte aligned rows of >= 2n");
         if (d.batch != 1) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogues take one matrix");
     }
-    const int cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
-    // Small tiles when the big ones cannot fill the chip and K is short
-    // enough that one workgroup walking it alone stays cheap.
-    const int64_t big_tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN) * d.batch;
-    const bool small = d.force_splits == 0 && big_tiles < cus && d.k <= 1024;
+    const int cus = cus_of(ctx);
+    const bool small = use_small(ctx, d);
+    const GemmFusion fuse = gemm_fusion(ctx, d);
     p.tiles_m = (int)(small ? (d.m + SBM - 1) / SBM : (d.m + BM - 1) / BM);
     p.tiles_n = (int)(small ? (d.n + SBN - 1) / SBN : (d.n + BN - 1) / BN);
     // The interior path addresses a tile with byte offsets below 2^31 (128 rows of ld).
     const int64_t off_limit = int64_t(1) << 29;
-    p.vec_a = (d.lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(d.a) &&
-              d.lda * BM < off_limit;
+    p.vec_a = vec_a_of(d, d.a, d.lda);
     p.vec_b = (d.ldb % 4 == 0) && (d.batch == 1 || d.stride_b % 4 == 0) && aligned16(d.b) &&
               d.ldb * BN < off_limit;
     p.vec_c = (d.ldc % 2 == 0) && (d.batch == 1 || d.stride_c % 2 == 0) &&
               (reinterpret_cast<uintptr_t>(d.c) & 7) == 0;
+
+    // RMSNorm of A: in the small kernel's loads, or first as its own kernel.
+    if (d.norm_w) {
+        if (d.ta || d.batch != 1 || d.force_splits > 0)
+            fail(MMH_ERR_ARGUMENT, "gemm: the A-row norm takes one row-major A");
+        if (fuse.norm) {
+            p.norm_w = d.norm_w;
+            p.norm_eps = d.norm_eps;
+        } else {
+            if (!d.norm_tmp) fail(MMH_ERR_ARGUMENT, "gemm: the A-row norm needs norm_tmp");
+            launch_rms_norm(ctx, d.a, d.norm_w, d.m, d.k, d.norm_eps, d.norm_tmp);
+            p.a = d.norm_tmp;
+            p.lda = d.k;
+            p.vec_a = vec_a_of(d, d.norm_tmp, d.k);
+        }
+    }
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
     const int64_t ktiles = (d.k + (small ? SBK : BK) - 1) / (small ? SBK : BK);
@@ -772,13 +910,28 @@ void gemm(Context &ctx, const GemmDesc &d) {
                 splits *= 2;
         }
     }
-    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD) splits = 1;
+    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD || p.norm_w) splits = 1;
     const int64_t kstep = small ? SBK : BK;
     const int64_t kt_per = (ktiles + splits - 1) / splits;
     p.k_per_split = kt_per * kstep;
     splits = (int)((ktiles + kt_per - 1) / kt_per);
     p.splits = splits;
     if (splits > 1) p.partial = static_cast<float *>(ctx.get_scratch((size_t)splits * d.m * d.n * 4));
+
+    // RoPE in the small kernel's epilogue when a head fits 32 columns.
+    const bool rope = d.rope_cos != nullptr;
+    if (rope) {
+        if (d.batch != 1 || d.rope_hd <= 0 || d.rope_hd % 2 || d.rope_seq <= 0 ||
+            d.m % d.rope_seq || d.rope_cols % d.rope_hd || d.rope_cols > d.n || !d.rope_sin)
+            fail(MMH_ERR_ARGUMENT, "gemm: bad rope arguments");
+        if (fuse.rope && splits == 1) {
+            p.rope_cos = d.rope_cos;
+            p.rope_sin = d.rope_sin;
+            p.rope_seq = (int)d.rope_seq;
+            p.rope_hd = (int)d.rope_hd;
+            p.rope_cols = (int)d.rope_cols;
+        }
+    }
 
     if (tiles > 0x7fffffff || d.batch > 65535) fail(MMH_ERR_SHAPE, "gemm: grid too large");
     dim3 grid((unsigned)tiles, (unsigned)d.batch, (unsigned)splits);
@@ -806,6 +959,10 @@ void gemm(Context &ctx, const GemmDesc &d) {
                                p.partial, d.c, nullptr, d.m, d.n, d.ldc, splits);
         check_hip(hipGetLastError(), "split-k reduce launch");
     }
+    if (rope && !p.rope_cos)
+        launch_rope_strided(ctx, d.c, d.rope_seq * d.ldc, d.rope_hd, d.ldc, d.m / d.rope_seq,
+                            d.rope_cols / d.rope_hd, d.rope_seq, d.rope_hd, d.rope_cos,
+                            d.rope_sin);
 }
 
 }  // namespace mmh

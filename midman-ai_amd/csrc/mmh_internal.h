@@ -82,9 +82,28 @@ struct GemmDesc {
     float *aux = nullptr;          // EPI_SWIGLU(_BWD): interleaved gate/up pairs
     int64_t ldaux = 0;
     int force_splits = 0;   // 0 = heuristic
+    // RMSNorm of A's rows first (norm.rs:21-39; nn form, batch 1): A is x and
+    // the product uses (x * inv) * norm_w with inv = (mean(x^2) + eps)^-1/2.
+    // Folded into the small-tile kernel's loads when K <= 256; otherwise the
+    // norm runs as its own kernel into norm_tmp ([m, k]) first.
+    const float *norm_w = nullptr;
+    float norm_eps = 0.0f;
+    float *norm_tmp = nullptr;
+    // RoPE (rope.rs:28-32) on the result's columns [0, rope_cols): heads of
+    // rope_hd columns, row r at position r % rope_seq; applied in the small
+    // kernel's epilogue when a head fits a wave's 32 columns (EPI_STORE),
+    // otherwise by the rope kernel after the product. Same bits either way.
+    const float *rope_cos = nullptr, *rope_sin = nullptr;
+    int64_t rope_seq = 0, rope_hd = 0, rope_cols = 0;
 };
 
 void gemm(Context &ctx, const GemmDesc &d);
+// Whether gemm() folds the A-row norm and the RoPE of d into its kernel (so a
+// caller can time or schedule them as kernels of their own otherwise).
+struct GemmFusion {
+    bool norm = false, rope = false;
+};
+GemmFusion gemm_fusion(const Context &ctx, const GemmDesc &d);
 
 // ---- bandwidth kernels ------------------------------------------------------
 void launch_embedding(Context &ctx, const float *table, int64_t d, const int32_t *ids_dev,

@@ -99,8 +99,11 @@ Config parse_config(const double *v) {
 }
 
 // One pre-norm block (block.rs:77-81) on packed weights: x += attn(rms(x)),
-// then x += mlp(rms(x)), the residual adds fused into the O and down GEMMs
-// and SwiGLU into the gate/up GEMM. timed(class, launch) wraps each launch.
+// then x += mlp(rms(x)), the residual adds fused into the O and down GEMMs,
+// SwiGLU into the gate/up GEMM, and the two norms and the q, k rotation
+// handed to the QKV and gate/up GEMMs (which fold them in for small widths
+// and run them as kernels of their own otherwise). timed(class, launch)
+// wraps each launch.
 struct BlockRun {
     const float *attn_norm = nullptr, *wqkv = nullptr, *wo = nullptr;
     const float *mlp_norm = nullptr, *wgu = nullptr, *wd = nullptr;
@@ -115,9 +118,12 @@ template <class Timed>
 void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
     const int64_t n = r.batch * r.seq, d = r.d, hd = d / r.heads, kv = r.kv_heads * hd;
     const int64_t qc = d + 2 * kv;
-    timed(MMH_PROF_RMS_NORM, [&] { launch_rms_norm(c, r.x, r.attn_norm, n, d, r.eps, r.xn); });
+    // attn_norm and the q, k rotation ride on the QKV product where the GEMM
+    // folds them in; otherwise they run (and are timed) as their own kernels
     GemmDesc g;
-    g.a = r.xn;
+    g.a = r.x;
+    g.norm_w = r.attn_norm;
+    g.norm_eps = r.eps;
     g.b = r.wqkv;
     g.c = r.qkv;
     g.m = n;
@@ -126,6 +132,19 @@ void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
     g.lda = d;
     g.ldb = qc;
     g.ldc = qc;
+    g.rope_cos = r.cos_t;
+    g.rope_sin = r.sin_t;
+    g.rope_seq = r.seq;
+    g.rope_hd = hd;
+    g.rope_cols = d + kv;
+    const GemmFusion fq = gemm_fusion(c, g);
+    if (!fq.norm) {
+        timed(MMH_PROF_RMS_NORM,
+              [&] { launch_rms_norm(c, r.x, r.attn_norm, n, d, r.eps, r.xn); });
+        g.a = r.xn;
+        g.norm_w = nullptr;
+    }
+    if (!fq.rope) g.rope_cos = g.rope_sin = nullptr;
     timed(MMH_PROF_GEMM_QKV, [&] { gemm(c, g); });
 
     AttnDesc a{};
@@ -144,8 +163,10 @@ void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
     a.hkv = r.kv_heads;
     a.t = r.seq;
     a.hd = hd;
-    a.cos_t = r.cos_t;
-    a.sin_t = r.sin_t;
+    if (!fq.rope) {  // attention() rotates q and k first
+        a.cos_t = r.cos_t;
+        a.sin_t = r.sin_t;
+    }
     timed(MMH_PROF_ATTENTION, [&] { attention(c, a); });
 
     GemmDesc o;
@@ -161,9 +182,10 @@ void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
     o.epi = EPI_ACCUM;
     timed(MMH_PROF_GEMM_O, [&] { gemm(c, o); });
 
-    timed(MMH_PROF_RMS_NORM, [&] { launch_rms_norm(c, r.x, r.mlp_norm, n, d, r.eps, r.xn); });
     GemmDesc gu;
-    gu.a = r.xn;
+    gu.a = r.x;
+    gu.norm_w = r.mlp_norm;
+    gu.norm_eps = r.eps;
     gu.b = r.wgu;
     gu.c = r.h;
     gu.m = n;
@@ -174,6 +196,11 @@ void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
     gu.ldc = r.ff;
     gu.epi = EPI_SWIGLU;
     gu.swiglu_ff = r.ff;
+    if (!gemm_fusion(c, gu).norm) {
+        timed(MMH_PROF_RMS_NORM, [&] { launch_rms_norm(c, r.x, r.mlp_norm, n, d, r.eps, r.xn); });
+        gu.a = r.xn;
+        gu.norm_w = nullptr;
+    }
     timed(MMH_PROF_GEMM_GATE_UP, [&] { gemm(c, gu); });
 
     GemmDesc dn;
