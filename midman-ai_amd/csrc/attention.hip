@@ -79,7 +79,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     const float *K = p.k + b * p.skb + kvh * p.skh;
     const float *V = p.v + b * p.svb + kvh * p.svh;
 
-    // Q operand: lane holds Q[q0 + lq][lh * NS + s], s < NS.
+    // Q operand: lane holds Q[q0 + lq][lh * NS + s] * scale * log2(e), s < NS
+    // (the scores come out of the MFMAs already in log2 units).
+    const float sc = p.scale * 1.4426950408889634f;
     float qr[NS];
     {
         const int qi = min(q0 + lq, T - 1);
@@ -88,33 +90,30 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
 #pragma unroll
             for (int s = 0; s < NS / 4; ++s) {
                 const float4 v = reinterpret_cast<const float4 *>(src)[s];
-                qr[4 * s + 0] = v.x;
-                qr[4 * s + 1] = v.y;
-                qr[4 * s + 2] = v.z;
-                qr[4 * s + 3] = v.w;
+                qr[4 * s + 0] = v.x * sc;
+                qr[4 * s + 1] = v.y * sc;
+                qr[4 * s + 2] = v.z * sc;
+                qr[4 * s + 3] = v.w * sc;
             }
         } else {
 #pragma unroll
-            for (int s = 0; s < NS; ++s) qr[s] = src[s];
+            for (int s = 0; s < NS; ++s) qr[s] = src[s] * sc;
         }
     }
 
+    // Keys past T read row T-1 instead (real, finite values: their scores
+    // are masked and their P is 0), so every load is unconditional.
     float4 kreg[PER], vreg[PER];
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int f = tid + i * NT;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (f < F4) {
+            if (F4 % NT == 0 || f < F4) {
                 const int j = (4 * f) / HD, c = (4 * f) % HD;
-                const int key = kt * 32 + j;
-                if (key < T) {
-                    kv = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + c);
-                    vv = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + c);
-                }
+                const int key = min(kt * 32 + j, T - 1);
+                kreg[i] = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + c);
+                vreg[i] = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + c);
             }
-            kreg[i] = kv;
-            vreg[i] = vv;
         }
     };
     auto store_tile = [&](int buf) __attribute__((always_inline)) {
@@ -143,10 +142,10 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[db][r] = 0.0f;
     // Softmax state in log2 units: scores are scaled by scale * log2(e) and
-    // exponentials are exp2. m_run is raised only when some lane's max grows
-    // by more than 8 (then every exponential stays <= 2^8); O and l share the
-    // same stale max, so O / l is unchanged.
-    const float sc = p.scale * 1.4426950408889634f;
+    // exponentials are exp2 (the hardware's, which flushes results below
+    // 2^-126 to 0). m_run is raised only when some lane's max grows by more
+    // than 8 (then every exponential stays <= 2^8); O and l share the same
+    // stale max, so O / l is unchanged.
     float m_run = -INFINITY, l_run = 0.0f;
     const int qi = q0 + lq;
 
@@ -184,18 +183,27 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
             const int k0 = kt * 32;
             float pv[16];
             float mloc = -INFINITY;
+            // only a tile that reaches the wave's first query or T needs the mask
+            if (k0 + 31 <= q0 && k0 + 31 < T) {
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const float sv = (sacc[r] + sacc1[r]) * sc;
-                pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
-                mloc = fmaxf(mloc, pv[r]);
+                for (int r = 0; r < 16; ++r) {
+                    pv[r] = sacc[r] + sacc1[r];
+                    mloc = fmaxf(mloc, pv[r]);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const float sv = sacc[r] + sacc1[r];
+                    pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
+                    mloc = fmaxf(mloc, pv[r]);
+                }
             }
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
             const bool need = mloc > m_run + 8.0f;  // always true on the first tile
             if (__any(need)) {
                 const float m_new = need ? mloc : m_run;
-                const float alpha = exp2f(m_run - m_new);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
                 l_run *= alpha;
 #pragma unroll
                 for (int db = 0; db < NDB; ++db)
@@ -206,7 +214,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
             float lsum = 0.0f;
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                pv[r] = exp2f(pv[r] - m_run);
+                pv[r] = __builtin_amdgcn_exp2f(pv[r] - m_run);
                 lsum += pv[r];
             }
             lsum += __shfl_xor(lsum, 32, 64);
