@@ -142,8 +142,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(BwdP p) {
     const float *dO = p.dout + b * p.sob + head * p.soh;
     const int64_t rows = ((int64_t)b * p.h + head) * T;
 
+    // qr carries scale * log2(e), so S comes out of the MFMAs in log2 units
+    const float sc = p.scale * 1.4426950408889634f;
     float qr[NS], gr[NS];
     load_run<NS>(qr, Q + (int64_t)qc * p.sqt + lh * NS);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qr[s] *= sc;
     load_run<NS>(gr, dO + (int64_t)qc * p.sot + lh * NS);
     float dsum = 0.0f;
     {
@@ -156,22 +160,18 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(BwdP p) {
     const float L2 = p.lse[rows + qc];
     if (lh == 0 && qi < T) p.dvec[rows + qi] = Dq;
 
+    // keys past T read row T-1 (finite values whose P is 0): no predicates
     float4 kreg[PER], vreg[PER];
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int f = tid + i * 256;
-            float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-            if (f < F4) {
+            if (F4 % 256 == 0 || f < F4) {
                 const int j = (4 * f) / HD, c = (4 * f) % HD;
-                const int key = kt * 32 + j;
-                if (key < T) {
-                    kv = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + c);
-                    vv = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + c);
-                }
+                const int key = min(kt * 32 + j, T - 1);
+                kreg[i] = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + c);
+                vreg[i] = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + c);
             }
-            kreg[i] = kv;
-            vreg[i] = vv;
         }
     };
     auto store_tile = [&](int buf) __attribute__((always_inline)) {
@@ -199,7 +199,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(BwdP p) {
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
         for (int r = 0; r < 16; ++r) dq[db][r] = 0.0f;
-    const float sc = p.scale * 1.4426950408889634f;
 
     load_tile(0);
     store_tile(0);
@@ -221,12 +220,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(BwdP p) {
             dot_chains<NS>(Kb + lq * KS + lh * NS, qr, s0, s1);
             dot_chains<NS>(Vb + lq * KS + lh * NS, gr, g0, g1);
             const int k0 = kt * 32;
+            // only a tile reaching the wave's first query or T needs the mask;
+            // exp2 is the hardware's (results below 2^-126 flush to 0)
+            const bool full = k0 + 31 <= q0 && k0 + 31 < T;
             float ds[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const float sv = (s0[r] + s1[r]) * sc;
-                const float pr = (key <= qi && key < T) ? exp2f(sv - L2) : 0.0f;
+                const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - L2);
+                const float pr = (full || (key <= qi && key < T)) ? e : 0.0f;
                 ds[r] = pr * ((g0[r] + g1[r]) - Dq);
             }
 #pragma unroll
@@ -299,8 +301,12 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
 
     const float *K = p.k + b * p.skb + kvh * p.skh;
     const float *V = p.v + b * p.svb + kvh * p.svh;
+    // kr carries scale * log2(e), so S comes out of the MFMAs in log2 units
+    const float sc = p.scale * 1.4426950408889634f;
     float kr[NS], vr[NS];
     load_run<NS>(kr, K + (int64_t)kc * p.skt + lh * NS);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) kr[s] *= sc;
     load_run<NS>(vr, V + (int64_t)kc * p.svt + lh * NS);
 
     float4 qreg[PER], greg[PER];
@@ -311,25 +317,22 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
         const int head = kvh * groups + g0 + g;
         const float *Qh = p.q + b * p.sqb + head * p.sqh;
         const float *Gh = p.dout + b * p.sob + head * p.soh;
+        // rows past T read row T-1 (finite; their P is 0): no predicates
 #pragma unroll
         for (int i = 0; i < PER; ++i) {
             const int f = tid + i * 256;
-            float4 qv = make_float4(0.f, 0.f, 0.f, 0.f), gv = qv;
-            if (f < F4) {
+            if (F4 % 256 == 0 || f < F4) {
                 const int j = (4 * f) / HD, c = (4 * f) % HD;
-                const int q = qt * 32 + j;
-                if (q < T) {
-                    qv = *reinterpret_cast<const float4 *>(Qh + (int64_t)q * p.sqt + c);
-                    gv = *reinterpret_cast<const float4 *>(Gh + (int64_t)q * p.sot + c);
-                }
+                const int q = min(qt * 32 + j, T - 1);
+                qreg[i] = *reinterpret_cast<const float4 *>(Qh + (int64_t)q * p.sqt + c);
+                greg[i] = *reinterpret_cast<const float4 *>(Gh + (int64_t)q * p.sot + c);
             }
-            qreg[i] = qv;
-            greg[i] = gv;
         }
-        if (tid < 64) {
-            const int q = qt * 32 + (tid & 31);
+        {
+            // lanes 0-31 fetch the tile's log-sum-exps, 32-63 its D values
+            const int q = min(qt * 32 + (tid & 31), T - 1);
             const int64_t at = ((int64_t)b * p.h + head) * T + q;
-            lreg = q < T ? (tid < 32 ? p.lse[at] : p.dvec[at]) : 0.0f;
+            lreg = ((tid & 32) ? p.dvec : p.lse)[at];
         }
     };
     auto store_tile = [&](int buf) __attribute__((always_inline)) {
@@ -364,8 +367,6 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
             dk[db][r] = 0.0f;
             dv[db][r] = 0.0f;
         }
-    const float sc = p.scale * 1.4426950408889634f;
-
     load_tile(0);
     store_tile(0);
     __syncthreads();
@@ -389,13 +390,15 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
             }
             dot_chains<NS>(Qb + lq * KS + lh * NS, kr, s0, s1);
             dot_chains<NS>(Gb + lq * KS + lh * NS, vr, g0, g1);
+            // the mask only where the tile reaches the wave's keys or T
+            const bool full = qt * 32 >= k0 + 31 && qt * 32 + 31 < T && k0 + 31 < T;
             float pv[16], ds[16];
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
                 const int q = qt * 32 + row;
-                const float sv = (s0[r] + s1[r]) * sc;
-                const float pr = (kj <= q && q < T && kj < T) ? exp2f(sv - Lb[row]) : 0.0f;
+                const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - Lb[row]);
+                const float pr = (full || (kj <= q && q < T && kj < T)) ? e : 0.0f;
                 pv[r] = pr;
                 ds[r] = pr * ((g0[r] + g1[r]) - Db[row]);
             }
