@@ -382,19 +382,37 @@ __global__ __launch_bounds__(256) void unpack_gate_up_kernel(const float *__rest
 // ---- global norm ---------------------------------------------------------------------
 constexpr int NORM_BLOCKS = 1024;
 
-// Block b sums the squares of elements b*256 + t, stepping by NORM_BLOCKS*256,
-// in f64; then a tree inside the block. Fixed order for a given n.
+__device__ __forceinline__ double sumsq4(float4 v) {
+    const double x = v.x, y = v.y, z = v.z, w = v.w;
+    return (x * x + y * y) + (z * z + w * w);
+}
+
+// Thread t of block b sums the squares of float4s b*256 + t, stepping by
+// NORM_BLOCKS*256, in f64 into four accumulators (four loads in flight);
+// block 0 adds the n % 4 tail; then a tree inside the block. Fixed order for
+// a given n.
 __global__ __launch_bounds__(256) void sumsq_partial_kernel(const float *__restrict__ g,
                                                             int64_t n,
                                                             double *__restrict__ partial) {
     __shared__ double part[256];
-    double acc = 0.0;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
-         i += (int64_t)NORM_BLOCKS * 256) {
-        const double v = (double)g[i];
-        acc += v * v;
+    const int64_t n4 = n / 4, stride = (int64_t)NORM_BLOCKS * 256;
+    const float4 *__restrict__ g4 = reinterpret_cast<const float4 *>(g);
+    double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+    int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    for (; i + 3 * stride < n4; i += 4 * stride) {
+        const float4 v0 = g4[i], v1 = g4[i + stride], v2 = g4[i + 2 * stride],
+                     v3 = g4[i + 3 * stride];
+        a0 += sumsq4(v0);
+        a1 += sumsq4(v1);
+        a2 += sumsq4(v2);
+        a3 += sumsq4(v3);
     }
-    part[threadIdx.x] = acc;
+    for (; i < n4; i += stride) a0 += sumsq4(g4[i]);
+    if (blockIdx.x == 0 && (int64_t)threadIdx.x < n - 4 * n4) {
+        const double v = g[4 * n4 + threadIdx.x];
+        a0 += v * v;
+    }
+    part[threadIdx.x] = (a0 + a1) + (a2 + a3);
     __syncthreads();
     for (int stride = 128; stride > 0; stride >>= 1) {
         if ((int)threadIdx.x < stride) part[threadIdx.x] += part[threadIdx.x + stride];
