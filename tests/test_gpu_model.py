@@ -98,6 +98,32 @@ def test_large_dims_reduced_depth_against_oracle(ctx):
     m.close()
 
 
+@pytest.mark.parametrize("cfg,batch,seq", [
+    # small widths take the folded RMSNorm (K <= 256) and, for heads of at most
+    # 32 columns, the folded rotation; ragged rows exercise the edge tiles
+    ([97, 128, 2, 4, 2, 96, 96, 10000.0, 1e-5, 1], 3, 37),    # hd 32, GQA
+    ([64, 128, 2, 2, 2, 200, 64, 500.0, 1e-6, 0], 2, 29),     # hd 64: norm only
+    ([50, 256, 1, 16, 4, 100, 40, 10000.0, 1e-5, 1], 1, 40),  # hd 16, K = 256
+    ([33, 260, 1, 65, 13, 64, 16, 10000.0, 1e-5, 1], 2, 9),   # K = 260: norm unfolded
+])
+def test_small_width_forwards_against_oracle(ctx, cfg, batch, seq):
+    print(f"\n[model] {cfg[:7]} B{batch} T{seq}", flush=True)
+    c = oracle_config(cfg)
+    w = O.init_weights(c, O.rng(17), std=0.1)
+    r = np.random.default_rng(seq)
+    x = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    y = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    m = mh.Model.from_weights(ctx, cfg, w)
+    try:
+        loss, logits = m.forward_loss(x, y, batch, seq)
+        ref_loss, ref_logits = O.forward_loss(c, w, x, y, batch, seq)
+        print(f"  loss gpu {loss:.7f} oracle {ref_loss:.7f}", flush=True)
+        assert abs(loss - ref_loss) / ref_loss <= 1e-4
+        check_logits(logits, ref_logits, "small-width logits")
+    finally:
+        m.close()
+
+
 def test_untied_head_against_oracle(ctx):
     cfg = [13, 16, 2, 4, 2, 24, 8, 10000.0, 1e-5, 0]
     c = oracle_config(cfg)
