@@ -39,7 +39,7 @@ PEAK_HBM_GBS = 8000.0
 # what the counter reads for the add kernel's known traffic (FETCH x 2.0,
 # WRITE x 1.0): (43,181,710 + 4,935,760) KiB over 81 launches. The counters
 # cannot be read from inside this process; see profiles/large_forward_hbm_traffic.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 641.3e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 641.5e6
 
 
 def log(msg):
@@ -348,6 +348,8 @@ def main():
     ap.add_argument("--no-tiny", action="store_true")
     ap.add_argument("--no-checkpoint", action="store_true",
                     help="skip timing the large model's safetensors save/load")
+    ap.add_argument("--no-block", action="store_true",
+                    help="skip timing the BASELINE single-block config")
     ap.add_argument("--no-shards", action="store_true",
                     help="skip timing training and evaluation fed from token shard files")
     ap.add_argument("--train-steps", type=int, default=5,
@@ -392,7 +394,7 @@ def main():
         log(f"large from shards: load {dd['load_gbs']} GB/s, batch {dd['batch_assembly_us']} us, "
             f"train {dd['train_ms_per_step']} ms/step ({dd['train_tokens_per_s']:.0f} tok/s), "
             f"eval {dd['eval_tokens_per_s']:.0f} tok/s")
-    blocks = [time_block(mh, ctx, hkv) for hkv in (16, 8)]
+    blocks = [] if a.no_block else [time_block(mh, ctx, hkv) for hkv in (16, 8)]
     for b in blocks:
         log(f"{b['workload']}: {b['ms']} ms, {b['tflops']} TFLOP/s")
     tiny = None
@@ -478,7 +480,7 @@ def main():
                 workload="large preset B4 T1024 trained (Trainer::step) and evaluated "
                          "(Trainer::evaluate) from token shard files through the seeded "
                          "batcher; synthetic uniform ids", **large["data"]),
-            "block": blocks,
+            "block": blocks or None,
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),
