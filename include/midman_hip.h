@@ -291,6 +291,20 @@ int32_t mmh_block_forward(mmh_handle ctx, const float *x, const float *block_wei
                           const float *cos_dev, const float *sin_dev, int64_t b, int64_t t,
                           int64_t d, int64_t h, int64_t hkv, int64_t ff, float eps, float *out);
 
+/* Backward of swiglu (mlp.rs:20-24: out = (silu(x Wg) * (x Wu)) Wd) for the
+ * incoming dout [rows, d]: dx [rows, d], dwg, dwu [d, ff], dwd [ff, d], all
+ * overwritten (g, u and h are recomputed from x). The silu*mul closure
+ * (ops_elementwise.rs:287, :355-364) is elementwise-exact; the products
+ * carry the GEMM tolerance. */
+int32_t mmh_swiglu_backward(mmh_handle ctx, const float *x, const float *wg, const float *wu,
+                            const float *wd, const float *dout, int64_t rows, int64_t d,
+                            int64_t ff, float *dx, float *dwg, float *dwu, float *dwd);
+/* Backward of embedding (ops_shape.rs:261-269): dtable [vocab, d] = zeros,
+ * plus for each position i the row dy[i] added to dtable[ids[i]], in position
+ * order (no atomics: bit-exact). ids on the host (MMH_ERR_INDEX for >= vocab). */
+int32_t mmh_embedding_backward(mmh_handle ctx, const int32_t *ids_host, int64_t n,
+                               const float *dy, int64_t vocab, int64_t d, float *dtable);
+
 /* ---- Checkpoints: midman-checkpoint (safetensors.rs, params.rs) -----------
  * TensorFile (safetensors.rs:68-330): named F32 tensors + string metadata,
  * read with the reference's validation (8-byte length, <= 100 MB header of

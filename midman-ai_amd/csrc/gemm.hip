@@ -70,23 +70,6 @@ struct KParams {
     int rope_seq, rope_hd, rope_cols;
 };
 
-__device__ __forceinline__ float silu_f(float x) {
-    // ops_elementwise.rs:239-241, :355-364: x * (1 / (1 + e^-x))
-    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
-    return __fmul_rn(x, s);
-}
-
-// Backward of h = silu(g) * u (mul then silu, ops_elementwise.rs:287, :355-364):
-// dsilu = dh*u, du = dh*silu(g), dg = dsilu * s*(1 + g*(1 - s)).
-__device__ __forceinline__ float2 swiglu_bwd_f(float dh, float g, float u) {
-    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
-    const float sv = __fmul_rn(g, s);
-    const float dsilu = __fmul_rn(dh, u);
-    const float du = __fmul_rn(dh, sv);
-    const float deriv = __fmul_rn(s, __fadd_rn(1.0f, __fmul_rn(g, __fsub_rn(1.0f, s))));
-    return make_float2(__fmul_rn(dsilu, deriv), du);
-}
-
 // Row strides (floats) of the k-major LDS stages: even, so the 8-byte operand
 // reads stay aligned; +2 where the stores transpose (spreads consecutive k rows
 // over the banks), +4 where they are float4 (keeps 16-byte alignment).

@@ -14,6 +14,23 @@
 
 namespace mmh {
 
+// silu (ops_elementwise.rs:239-241, :355-364): x * (1 / (1 + e^-x)).
+__device__ __forceinline__ float silu_f(float x) {
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
+    return __fmul_rn(x, s);
+}
+
+// Backward of h = silu(g) * u (mul then silu, ops_elementwise.rs:287, :355-364):
+// dsilu = dh*u, du = dh*silu(g), dg = dsilu * s*(1 + g*(1 - s)); returns (dg, du).
+__device__ __forceinline__ float2 swiglu_bwd_f(float dh, float g, float u) {
+    const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+    const float sv = __fmul_rn(g, s);
+    const float dsilu = __fmul_rn(dh, u);
+    const float du = __fmul_rn(dh, sv);
+    const float deriv = __fmul_rn(s, __fadd_rn(1.0f, __fmul_rn(g, __fsub_rn(1.0f, s))));
+    return make_float2(__fmul_rn(dsilu, deriv), du);
+}
+
 // An error that the C-ABI boundary turns into a status code + message.
 struct Error {
     int32_t status;
@@ -112,6 +129,9 @@ void launch_rms_norm(Context &ctx, const float *x, const float *w, int64_t rows,
                      float eps, float *out);
 void launch_add(Context &ctx, const float *a, const float *b, float *out, int64_t n);
 void launch_silu_mul(Context &ctx, const float *g, const float *u, float *out, int64_t n);
+// (dg, du) of h = silu(g) * u for the incoming dh; dg and du may alias g and u.
+void launch_silu_mul_backward(Context &ctx, const float *dh, float *g, float *u, float *dg,
+                              float *du, int64_t n);
 void launch_rope(Context &ctx, const float *x, int64_t bh, int64_t t, int64_t hd,
                  const float *cos_t, const float *sin_t, float *out);
 // Row losses then their f64 mean; loss_dev receives one float.

@@ -146,9 +146,19 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float *__restrict__
                                                        float *__restrict__ out, int64_t n) {
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        const float x = g[i];
-        const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
-        out[i] = __fmul_rn(__fmul_rn(x, s), u[i]);
+        out[i] = __fmul_rn(silu_f(g[i]), u[i]);
+    }
+}
+
+// dg and du may be g and u themselves: each element is read before written.
+__global__ __launch_bounds__(256) void silu_mul_backward_kernel(const float *__restrict__ dh,
+                                                                const float *g, const float *u,
+                                                                float *dg, float *du, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const float2 r = swiglu_bwd_f(dh[i], g[i], u[i]);
+        dg[i] = r.x;
+        du[i] = r.y;
     }
 }
 
@@ -348,6 +358,13 @@ void launch_silu_mul(Context &ctx, const float *g, const float *u, float *out, i
     hipLaunchKernelGGL(silu_mul_kernel, dim3(grid_for(n)), dim3(256), 0, ctx.stream, g, u, out,
                        n);
     check_hip(hipGetLastError(), "silu_mul launch");
+}
+
+void launch_silu_mul_backward(Context &ctx, const float *dh, float *g, float *u, float *dg,
+                              float *du, int64_t n) {
+    hipLaunchKernelGGL(silu_mul_backward_kernel, dim3(grid_for(n)), dim3(256), 0, ctx.stream, dh,
+                       g, u, dg, du, n);
+    check_hip(hipGetLastError(), "silu_mul backward launch");
 }
 
 void launch_rope(Context &ctx, const float *x, int64_t bh, int64_t t, int64_t hd,

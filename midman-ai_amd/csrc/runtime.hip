@@ -759,6 +759,100 @@ int32_t mmh_causal_attention_backward(mmh_handle ctx, const float *q, const floa
     });
 }
 
+int32_t mmh_swiglu_backward(mmh_handle ctx, const float *x, const float *wg, const float *wu,
+                            const float *wd, const float *dout, int64_t rows, int64_t d,
+                            int64_t ff, float *dx, float *dwg, float *dwu, float *dwd) {
+    return guard([&] {
+        Context &cx = context(ctx);
+        for (const void *p : {(const void *)x, (const void *)wg, (const void *)wu,
+                              (const void *)wd, (const void *)dout, (const void *)dx,
+                              (const void *)dwg, (const void *)dwu, (const void *)dwd})
+            need(p, "swiglu_backward argument");
+        positive(rows, "rows");
+        positive(d, "d_model");
+        positive(ff, "d_ff");
+        // g = x.Wg, u = x.Wu, h = silu(g)*u recomputed (the forward keeps no
+        // intermediates), then the closures of mlp.rs:20-24 in reverse.
+        const size_t rf = ((size_t)(rows * ff) + 63) / 64 * 64;
+        float *ws = static_cast<float *>(cx.workspace(2, 4 * rf * 4));
+        float *g = ws, *u = g + rf, *h = u + rf, *dh = h + rf;
+        auto mm = [&](const float *a, bool ta, int64_t lda, const float *b, bool tb, int64_t ldb,
+                      float *c, int64_t m, int64_t k, int64_t n, int epi) {
+            GemmDesc gd;
+            gd.a = a;
+            gd.ta = ta;
+            gd.lda = lda;
+            gd.b = b;
+            gd.tb = tb;
+            gd.ldb = ldb;
+            gd.c = c;
+            gd.ldc = n;
+            gd.m = m;
+            gd.k = k;
+            gd.n = n;
+            gd.epi = epi;
+            gemm(cx, gd);
+        };
+        mm(x, false, d, wg, false, ff, g, rows, d, ff, EPI_STORE);
+        mm(x, false, d, wu, false, ff, u, rows, d, ff, EPI_STORE);
+        launch_silu_mul(cx, g, u, h, rows * ff);
+        mm(h, true, ff, dout, false, d, dwd, ff, rows, d, EPI_STORE);    // dWd = h^T dout
+        mm(dout, false, d, wd, true, d, dh, rows, d, ff, EPI_STORE);    // dh = dout Wd^T
+        launch_silu_mul_backward(cx, dh, g, u, g, u, rows * ff);        // g, u <- dg, du
+        mm(x, true, d, g, false, ff, dwg, d, rows, ff, EPI_STORE);      // dWg = x^T dg
+        mm(x, true, d, u, false, ff, dwu, d, rows, ff, EPI_STORE);      // dWu = x^T du
+        mm(g, false, ff, wg, true, ff, dx, rows, ff, d, EPI_STORE);     // dx = dg Wg^T
+        mm(u, false, ff, wu, true, ff, dx, rows, ff, d, EPI_ACCUM);     //    + du Wu^T
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_embedding_backward(mmh_handle ctx, const int32_t *ids_host, int64_t n,
+                               const float *dy, int64_t vocab, int64_t d, float *dtable) {
+    return guard([&] {
+        Context &cx = context(ctx);
+        need(dy, "dy");
+        need(dtable, "dtable");
+        positive(n, "n");
+        positive(vocab, "vocab");
+        positive(d, "d");
+        check_ids(ids_host, n, vocab, "token id");
+        // the distinct ids ascending, and per id its positions ascending (a
+        // counting sort), so each table row sums its gradient rows in
+        // position order as ops_shape.rs:261-269 adds them
+        std::vector<int32_t> count((size_t)vocab + 1, 0);
+        for (int64_t i = 0; i < n; ++i) count[(size_t)ids_host[i] + 1]++;
+        std::vector<int32_t> index;  // uniq | start | order
+        index.reserve((size_t)(3 * n + 1));
+        std::vector<int32_t> at((size_t)vocab, 0);
+        int32_t run = 0;
+        std::vector<int32_t> uniq, start;
+        for (int64_t v = 0; v < vocab; ++v) {
+            const int32_t c = count[(size_t)v + 1];
+            if (c) {
+                uniq.push_back((int32_t)v);
+                start.push_back(run);
+            }
+            at[(size_t)v] = run;
+            run += c;
+        }
+        start.push_back(run);
+        std::vector<int32_t> order((size_t)n);
+        for (int64_t i = 0; i < n; ++i) order[(size_t)at[(size_t)ids_host[i]]++] = (int32_t)i;
+        const int64_t nu = (int64_t)uniq.size();
+        index.insert(index.end(), uniq.begin(), uniq.end());
+        index.insert(index.end(), start.begin(), start.end());
+        index.insert(index.end(), order.begin(), order.end());
+        int32_t *dev = static_cast<int32_t *>(cx.workspace(3, index.size() * 4));
+        check_hip(hipMemcpyAsync(dev, index.data(), index.size() * 4, hipMemcpyHostToDevice,
+                                 cx.stream), "index upload");
+        launch_fill(cx, dtable, vocab * d, 0.0f);
+        launch_embedding_backward(cx, dy, d, dev, dev + nu, dev + 2 * nu + 1, nu, dtable, false);
+        check_hip(hipStreamSynchronize(cx.stream), "index upload sync");
+        return MMH_OK;
+    });
+}
+
 int32_t mmh_cross_entropy_backward(mmh_handle ctx, const float *logits,
                                    const int32_t *targets_host, int64_t n, int64_t vocab,
                                    float *dlogits, float *loss_host) {

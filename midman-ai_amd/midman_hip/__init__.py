@@ -122,6 +122,8 @@ _SIGNATURES = {
     "mmh_apply_rope_backward": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
     "mmh_causal_attention_backward": [_h, _vp, _vp, _vp, _vp] + [_i64] * 5 + [_vp] * 3,
     "mmh_cross_entropy_backward": [_h, _vp, _i32p, _i64, _i64, _vp, _f32p],
+    "mmh_swiglu_backward": [_h] + [_vp] * 5 + [_i64] * 3 + [_vp] * 4,
+    "mmh_embedding_backward": [_h, _i32p, _i64, _vp, _i64, _i64, _vp],
     "mmh_tensorfile_create": [ctypes.POINTER(_h)],
     "mmh_tensorfile_parse": [ctypes.c_char_p, ctypes.c_uint64, ctypes.POINTER(_h)],
     "mmh_tensorfile_push": [_h, ctypes.c_char_p, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64),
@@ -549,6 +551,31 @@ def cross_entropy_backward(ctx: Context, logits: DeviceArray, targets: np.ndarra
     check(lib().mmh_cross_entropy_backward(ctx.handle, logits.ptr, _ip(targets), n, v, out.ptr,
                                            ctypes.byref(loss)))
     return loss.value, out
+
+
+def swiglu_backward(ctx: Context, x: DeviceArray, wg: DeviceArray, wu: DeviceArray,
+                    wd: DeviceArray, dout: DeviceArray):
+    """Backward of swiglu (mlp.rs:20-24): (dx, dwg, dwu, dwd)."""
+    d = x.shape[-1]
+    ff = wg.shape[1]
+    rows = x.size // d
+    if wg.shape != (d, ff) or wu.shape != (d, ff) or wd.shape != (ff, d) or dout.size != x.size:
+        raise ShapeError(ERR_SHAPE, "swiglu_backward: x [.., d], wg, wu [d, ff], wd [ff, d]")
+    dx, dwg, dwu, dwd = ctx.empty(x.shape), ctx.empty((d, ff)), ctx.empty((d, ff)), ctx.empty((ff, d))
+    check(lib().mmh_swiglu_backward(ctx.handle, x.ptr, wg.ptr, wu.ptr, wd.ptr, dout.ptr, rows, d,
+                                    ff, dx.ptr, dwg.ptr, dwu.ptr, dwd.ptr))
+    return dx, dwg, dwu, dwd
+
+
+def embedding_backward(ctx: Context, ids: np.ndarray, dy: DeviceArray, vocab: int):
+    """Backward of embedding (ops_shape.rs:261-269): dtable [vocab, d]."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    d = dy.shape[-1]
+    if dy.size != ids.size * d:
+        raise ShapeError(ERR_SHAPE, "embedding_backward: dy must be [n, d] for n ids")
+    out = ctx.empty((vocab, d))
+    check(lib().mmh_embedding_backward(ctx.handle, _ip(ids), ids.size, dy.ptr, vocab, d, out.ptr))
+    return out
 
 
 # ---- checkpoints: midman-checkpoint ----------------------------------------------------

@@ -150,6 +150,49 @@ def test_cross_entropy_backward_matches_oracle(ctx, n, v):
     assert abs(loss - mo.cross_entropy(z, t)) <= 1e-4 * abs(loss)
 
 
+@pytest.mark.parametrize("rows,d,ff", [(1, 1, 1), (7, 16, 24), (64, 64, 176), (300, 128, 344),
+                                        (1024, 2048, 5632)])
+def test_swiglu_backward_matches_oracle(ctx, rows, d, ff):
+    """The op-level swiglu backward against the oracle's closures: silu*mul
+    backward (bit-exact elementwise) between matmul backwards."""
+    print(f"\n[swiglu backward] rows={rows} d={d} ff={ff}", flush=True)
+    r = mo.rng(rows + d + ff)
+    x = mo.randn((rows, d), 1.0, r)
+    wg, wu, wd = mo.randn((d, ff), 0.02, r), mo.randn((d, ff), 0.02, r), mo.randn((ff, d), 0.02, r)
+    dout = mo.randn((rows, d), 1.0, r)
+    dev = [ctx.to_device(a) for a in (x, wg, wu, wd, dout)]
+    dx, dwg, dwu, dwd = (t.numpy() for t in mh.swiglu_backward(ctx, *dev))
+    # oracle: the closures of mlp.rs:20-24 in reverse
+    g = mo.gemm("nn", x, wg, rows, d, ff)
+    u = mo.gemm("nn", x, wu, rows, d, ff)
+    h = (g * (1.0 / (1.0 + np.exp(-g.astype(np.float64))))).astype(np.float32) * u
+    dh, want_dwd = mo.matmul_backward(h, wd, dout, rows, ff, d)
+    dg, du = mo.silu_mul_backward(g, u, dh)
+    dx_g, want_dwg = mo.matmul_backward(x, wg, dg, rows, d, ff)
+    dx_u, want_dwu = mo.matmul_backward(x, wu, du, rows, d, ff)
+    want_dx = dx_g + dx_u
+    for got, want, name in [(dx, want_dx, "dx"), (dwg, want_dwg, "dwg"), (dwu, want_dwu, "dwu"),
+                            (dwd, want_dwd, "dwd")]:
+        scale = max(float(np.max(np.abs(want))), 1e-30)
+        e = float(np.max(np.abs(got.astype(np.float64) - want))) / scale
+        print(f"  {name}: max|diff|/max|ref| {e:.3g}", flush=True)
+        assert e <= 2e-4, name
+
+
+@pytest.mark.parametrize("n,vocab,d", [(1, 1, 1), (13, 7, 16), (4096, 32000, 64), (777, 50, 300)])
+def test_embedding_backward_is_bit_exact(ctx, n, vocab, d):
+    """Rows added per id in position order, untouched rows zero: the oracle's
+    bits (ops_shape.rs:261-269)."""
+    r = np.random.default_rng(n + vocab)
+    ids = r.integers(0, vocab, n).astype(np.int32)
+    dy = r.standard_normal((n, d), dtype=np.float32)
+    got = mh.embedding_backward(ctx, ids, ctx.to_device(dy), vocab).numpy()
+    want = mo.embedding_backward(ids, dy, vocab)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    with pytest.raises(mh.IndexOutOfRange):
+        mh.embedding_backward(ctx, np.array([vocab], np.int32), ctx.to_device(dy[:1]), vocab)
+
+
 def test_lab_goldens_on_device(ctx, goldens):
     g = goldens["lab_native"]
     lab = mh.Lab(ctx, g["config"], g["hyper"], g["seed"], g["batch"], g["seq"])
