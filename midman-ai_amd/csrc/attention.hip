@@ -2,12 +2,17 @@
 // the reference's materialised path (midman-nn/src/attention.rs:79-101,146-170):
 // repeat_interleave of K/V, Q.K^T, scale, additive -1e9 mask, softmax, P.V.
 //
-// A 256-thread workgroup (4 wave64s) owns 128 query rows of one (batch, head);
-// each wave owns 32 of them. The workgroup walks 32-key tiles of K and V up to
-// its last diagonal: every tile is loaded once with float4 loads into
-// registers, written to a double-buffered LDS stage, and shared by the four
-// waves; the next tile's loads are in flight while the current one is used.
-// (attn_fwd_split_kernel below covers small grids.)
+// A 512-thread workgroup (8 wave64s) owns two 128-row query blocks of one
+// (batch, head), paired so that every workgroup carries the same causal work:
+// block nqb-1-z (the longest rows) on waves 0-3 and block z on waves 4-7, each
+// wave owning 32 rows. The workgroup walks 32-key tiles of K and V up to the
+// long block's last diagonal; the short block's keys are a prefix of those,
+// so every tile is loaded once with float4 loads into registers, written to a
+// double-buffered LDS stage, and shared by all eight waves; the next tile's
+// loads are in flight while the current one is used. A SIMD then runs one wave
+// of each block, nqb+1 blocks' worth of tiles in every workgroup, where
+// unpaired blocks would leave the CUs that drew two long blocks working while
+// the rest idle. (attn_fwd_split_kernel below covers small grids.)
 // Each wave keeps an online softmax for its rows, so no [T,T] tensor exists.
 //
 // The products are computed transposed so that every per-query quantity lives
@@ -46,9 +51,9 @@ struct AttnP {
 };
 
 template <int HD>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
-    constexpr int NT = 256;                  // threads
-    constexpr int QB = 128;                  // query rows per workgroup
+__global__ __launch_bounds__(512) void attn_fwd_kernel(AttnP p) {
+    constexpr int NT = 512;                  // threads
+    constexpr int QB = 128;                  // query rows per block (4 waves)
     constexpr int NS = HD / 2;               // S^T k-steps (lanes 32-63 take dims NS..HD-1)
     constexpr int NDB = (HD + 31) / 32;      // O^T row blocks; block db row i is dim NDB*i+db
     constexpr int KS = HD + 4;               // K row stride: 16-byte aligned rows
@@ -56,7 +61,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     constexpr int F4 = 32 * HD / 4;          // float4s per K or V tile
     constexpr int PER = (F4 + NT - 1) / NT;  // float4s per thread per tile
     // Two K stages [32][KS] and two V stages [32][HD]; at the end the same
-    // memory holds the waves' outputs as [QB][OS].
+    // memory holds one block's outputs as [QB][OS], one block after the other.
     constexpr int STAGES = 2 * 32 * KS + 2 * 32 * HD;
     constexpr int OUT = QB * OS;
     __shared__ __attribute__((aligned(16))) float smem[STAGES > OUT ? STAGES : OUT];
@@ -64,16 +69,18 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
     auto Vs = [&](int buf) { return smem + 64 * KS + buf * 32 * HD; };
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int half = wave >> 2, w4 = wave & 3;     // block of the pair, wave in it
     const int lq = lane & 31, lh = lane >> 5;
     const int head = blockIdx.x, b = blockIdx.y;
-    const int qblk = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
+    const int long_blk = p.nqb - 1 - (int)blockIdx.z;
+    const int qblk = half ? (int)blockIdx.z : long_blk;
+    // with nqb odd the middle block pairs with itself: waves 4-7 sit it out
+    const bool active = half == 0 || qblk < long_blk;
     const int kvh = head / (p.h / p.hkv);
     const int T = p.t;
-    const int q_first = qblk * QB;
-    const int q_last = min(q_first + QB - 1, T - 1);
-    const int ntiles = q_last / 32 + 1;            // key tiles the workgroup needs
-    const int q0 = q_first + wave * 32;            // this wave's first query
-    const int my_tiles = q0 < T ? q0 / 32 + 1 : 0; // tiles this wave needs
+    const int ntiles = min(long_blk * QB + QB - 1, T - 1) / 32 + 1;  // key tiles to walk
+    const int q0 = qblk * QB + w4 * 32;            // this wave's first query
+    const int my_tiles = active && q0 < T ? q0 / 32 + 1 : 0;  // tiles this wave needs
 
     const float *Q = p.q + b * p.sqb + head * p.sqh;
     const float *K = p.k + b * p.skb + kvh * p.skh;
@@ -247,28 +254,35 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(AttnP p) {
         __syncthreads();
     }
 
-    // O^T -> LDS as [q][d], then coalesced row stores.
-    float *Os = smem + wave * 32 * OS;
-    if (my_tiles > 0) {
-        const float inv = 1.0f / l_run;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
-                const int d = NDB * i + db;
-                if (d < HD) Os[lq * OS + d] = o[db][r] * inv;
-            }
-    }
     if (p.lse && my_tiles > 0 && lh == 0 && qi < T)
         p.lse[((int64_t)b * p.h + head) * T + qi] = m_run + log2f(l_run);
-    __syncthreads();
-    if (my_tiles > 0) {
-        for (int idx = lane; idx < 32 * HD; idx += 64) {
-            const int j = idx / HD, c = idx - j * HD;
-            const int q = q0 + j;
-            if (q < T) p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = Os[j * OS + c];
+    // O^T -> LDS as [q][d], then coalesced row stores; the long block's waves
+    // first, then the short block's, through the same staging rows.
+    float *Os = smem + w4 * 32 * OS;
+#pragma unroll
+    for (int round = 0; round < 2; ++round) {
+        const bool mine = half == round && my_tiles > 0;
+        if (mine) {
+            const float inv = 1.0f / l_run;
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const int d = NDB * i + db;
+                    if (d < HD) Os[lq * OS + d] = o[db][r] * inv;
+                }
         }
+        __syncthreads();
+        if (mine) {
+            for (int idx = lane; idx < 32 * HD; idx += 64) {
+                const int j = idx / HD, c = idx - j * HD;
+                const int q = q0 + j;
+                if (q < T)
+                    p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = Os[j * OS + c];
+            }
+        }
+        if (round == 0) __syncthreads();
     }
 }
 
@@ -467,7 +481,8 @@ void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool split) {
             return;
         }
     }
-    hipLaunchKernelGGL((attn_fwd_kernel<HD>), grid, dim3(256), 0, ctx.stream, p);
+    grid.z = (grid.z + 1) / 2;  // query blocks in pairs
+    hipLaunchKernelGGL((attn_fwd_kernel<HD>), grid, dim3(512), 0, ctx.stream, p);
 }
 
 bool al16(const void *ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; }

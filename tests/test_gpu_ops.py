@@ -95,6 +95,10 @@ ATTN_CASES = [
     (1, 16, 8, 1024, 128),
     (2, 16, 8, 77, 128),
     (3, 6, 3, 1, 64),
+    # odd counts of 128-row query blocks (the middle one has no partner)
+    (1, 4, 2, 300, 128),
+    (8, 16, 8, 300, 64),
+    (16, 8, 8, 260, 32),
 ]
 
 
