@@ -605,6 +605,42 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
     }
 }
 
+// One accumulator value v of C[row][col] of a 32-column MFMA block (lane lr
+// holds column col) through the epilogues of the small kernels. Every lane of
+// the wave calls it: the SwiGLU gate/up pair and the RoPE pair meet through
+// lane exchanges. SwiGLU: gate f at column 2f (even lane), up f at 2f+1 (the
+// next lane). RoPE (rope.rs:28-32) on heads of rope_hd (<= 32, dividing 32)
+// columns: the pair (c, c + hd/2) of a head sits in lanes lr and lr ^ hd/2.
+template <int EPI>
+__device__ __forceinline__ void block32_epilogue(const KParams &p, float *C, const float *R,
+                                                 int64_t row, int64_t col, int lr, float v) {
+    if (EPI == EPI_SWIGLU) {
+        const float up = __shfl_xor(v, 1, 64);
+        if ((lr & 1) || row >= p.m) return;
+        const int64_t f = col >> 1;
+        if (p.aux && col + 1 < p.n)
+            *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) = make_float2(v, up);
+        if (f < p.swiglu_ff) C[row * p.ldc + f] = __fmul_rn(silu_f(v), up);
+        return;
+    }
+    if (EPI == EPI_STORE && p.rope_cos) {
+        const int hd = p.rope_hd, half = hd >> 1;
+        const float other = __shfl_xor(v, half, 64);
+        if (row >= p.m || col >= p.n) return;
+        if (col < p.rope_cols) {
+            const int pc = (int)(col % hd);
+            const int64_t pos = row % p.rope_seq;
+            const int c = pc < half ? pc : pc - half;
+            const float cs = p.rope_cos[pos * half + c], sn = p.rope_sin[pos * half + c];
+            v = pc < half ? v * cs - other * sn : v * cs + other * sn;
+        }
+        C[row * p.ldc + col] = v;
+        return;
+    }
+    if (row >= p.m || col >= p.n) return;
+    C[row * p.ldc + col] = EPI == EPI_ACCUM ? __fadd_rn(R[row * p.ldc + col], v) : v;
+}
+
 template <bool TA, bool TB, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
     __shared__ __attribute__((aligned(16))) float As[2][SBM][SKS];
@@ -683,22 +719,6 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
         return;
     }
     float *C = p.c + batch * p.stride_c;
-    if (EPI == EPI_SWIGLU) {
-        // gate f at column 2f (even lane), up f at 2f+1 (the next lane)
-        const bool even = (lr & 1) == 0;
-        const int64_t f = col >> 1;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float up = __shfl_xor(acc[r], 1, 64);
-            const int64_t row = row_of(r);
-            if (!even || row >= M) continue;
-            if (p.aux && col + 1 < N)
-                *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) =
-                    make_float2(acc[r], up);
-            if (f < p.swiglu_ff) C[row * p.ldc + f] = __fmul_rn(silu_f(acc[r]), up);
-        }
-        return;
-    }
     if (EPI == EPI_SWIGLU_BWD) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -710,36 +730,151 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
         }
         return;
     }
-    if (EPI == EPI_STORE && p.rope_cos) {
-        // rope.rs:28-32 on heads of rope_hd (<= 32, dividing 32) columns: the
-        // pair (c, c + hd/2) of a head sits in lanes lr and lr ^ hd/2.
-        const int hd = p.rope_hd, half = hd >> 1;
-        const int pc = (int)(col % hd);
-        const bool rot = col < p.rope_cols;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float other = __shfl_xor(acc[r], half, 64);
-            const int64_t row = row_of(r);
-            if (row >= M || col >= N) continue;
-            float v = acc[r];
-            if (rot) {
-                const int64_t pos = row % p.rope_seq;
-                const int c = pc < half ? pc : pc - half;
-                const float cs = p.rope_cos[pos * half + c], sn = p.rope_sin[pos * half + c];
-                v = pc < half ? v * cs - other * sn : v * cs + other * sn;
-            }
-            C[row * p.ldc + col] = v;
-        }
-        return;
-    }
     const float *R = p.resid ? p.resid + batch * p.stride_c : C;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-        const int64_t row = row_of(r);
-        if (row >= M || col >= N) continue;
-        const float v = acc[r];
-        C[row * p.ldc + col] = EPI == EPI_ACCUM ? __fadd_rn(R[row * p.ldc + col], v) : v;
+    for (int r = 0; r < 16; ++r) block32_epilogue<EPI>(p, C, R, row_of(r), col, lr, acc[r]);
+}
+
+// ---- K-split 32x32 GEMM -------------------------------------------------------
+// For nn shapes that leave most of the chip idle with a K of a few steps (the
+// tiny preset's projections: M = 2048, N = 128-704, K = 128-352) the cost is
+// latency, not the MFMA rate: a 64x64 tile walks its K steps one after
+// another on one workgroup. Here a workgroup owns a 32x32 tile of C and its
+// NW waves take the 32-wide K steps round-robin (wave w: steps w, w + NW,
+// ...), so a tile's steps run side by side and the grid holds 4x the
+// workgroups. Operands go straight from memory into the MFMA layout, no LDS
+// staging: lane l takes row (A) or column (B) l%32 and k 16*(l/32) .. +15 of
+// a step, A as four float4 reads of its row and B as sixteen reads that are
+// coalesced across the lanes. The NW partial tiles meet in LDS and are summed
+// in wave order; then wave w applies the epilogue to accumulator registers
+// w, w + NW, ... of the sum.
+// NORM: the A rows are RMS-normalised on the way in, as in the small kernel:
+// x * w feeds the MFMAs, the sums of squares of x are gathered per lane and
+// combined over the lane halves and then the waves, and each row's 1/rms
+// scales the summed results.
+// FULLK: K is a multiple of 32 and the A rows (and the norm weights) are
+// 16-byte aligned; otherwise every load is predicated on k < K.
+template <int EPI, bool NORM, int NW, bool FULLK>
+__global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
+    __shared__ float part[NW][16][64];
+    __shared__ float sm_ss[NW][32];
+    __shared__ float sm_inv[32];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lr = lane & 31, lk = lane >> 5;
+    const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x - tm * p.tiles_n;
+    const int64_t m0 = (int64_t)tm * 32, n0 = (int64_t)tn * 32;
+    const int64_t M = p.m, N = p.n, K = p.k;
+    const int nsteps = (int)((K + 31) / 32);
+    // rows and columns past the edge read the last one; their results are not stored
+    const float *arow = p.a + min(m0 + lr, M - 1) * p.lda;
+    const float *bcol = p.b + min(n0 + lr, N - 1);
+
+    floatx16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    float ss = 0.0f;
+    for (int st = wave; st < nsteps; st += NW) {
+        const int64_t kb = (int64_t)st * 32 + 16 * lk;  // this lane's first k of the step
+        float a[16], b[16];
+        if (FULLK) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = reinterpret_cast<const float4 *>(arow + kb)[i];
+                a[4 * i + 0] = v.x;
+                a[4 * i + 1] = v.y;
+                a[4 * i + 2] = v.z;
+                a[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) a[j] = kb + j < K ? arow[kb + j] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+            b[j] = (FULLK || kb + j < K) ? bcol[(kb + j) * p.ldb] : 0.0f;
+        if (NORM) {
+            float w[16];
+            if (FULLK) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float4 v = reinterpret_cast<const float4 *>(p.norm_w + kb)[i];
+                    w[4 * i + 0] = v.x;
+                    w[4 * i + 1] = v.y;
+                    w[4 * i + 2] = v.z;
+                    w[4 * i + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 16; ++j) w[j] = kb + j < K ? p.norm_w[kb + j] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                ss = __fadd_rn(ss, __fmul_rn(a[j], a[j]));
+                a[j] = __fmul_rn(a[j], w[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[j], b[j], acc, 0, 0, 0);
     }
+
+    if (NORM) {
+        // this wave's share of row lr: k 0-15 of its steps in lane lr, 16-31 in lane lr+32
+        ss = __fadd_rn(ss, __shfl_xor(ss, 32, 64));
+        if (lk == 0) sm_ss[wave][lr] = ss;
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) part[wave][r][lane] = acc[r];
+    __syncthreads();
+    if (NORM) {
+        if (tid < 32) {
+            float t = sm_ss[0][tid];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) t = __fadd_rn(t, sm_ss[w][tid]);
+            const float mean = __fmul_rn(t, __fdiv_rn(1.0f, (float)K));  // norm.rs:21-39
+            sm_inv[tid] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, p.norm_eps)));
+        }
+        __syncthreads();
+    }
+    // Register r of lane l is C[m0 + 8*(r/4) + 4*(l/32) + r%4][n0 + l%32].
+    float *C = p.c;
+    const float *R = p.resid ? p.resid : C;
+    const int64_t col = n0 + lr;
+    for (int r = wave; r < 16; r += NW) {
+        float v = part[0][r][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v = __fadd_rn(v, part[w][r][lane]);
+        const int rl = 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (NORM) v = __fmul_rn(v, sm_inv[rl]);
+        block32_epilogue<EPI>(p, C, R, m0 + rl, col, lr, v);
+    }
+}
+
+template <int EPI, bool NORM>
+void launch_ksplit_nw(Context &ctx, const KParams &p, dim3 grid, bool fullk, int nw) {
+    if (nw == 4) {
+        if (fullk)
+            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 4, true>), grid, dim3(256), 0, ctx.stream, p);
+        else
+            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 4, false>), grid, dim3(256), 0, ctx.stream, p);
+    } else {
+        if (fullk)
+            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 8, true>), grid, dim3(512), 0, ctx.stream, p);
+        else
+            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 8, false>), grid, dim3(512), 0, ctx.stream, p);
+    }
+}
+
+// Four waves up to four K steps (one step each), eight beyond.
+template <int EPI>
+void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, bool fullk) {
+    const int nw = (p.k + 31) / 32 <= 4 ? 4 : 8;
+    if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
+        if (p.norm_w) {
+            launch_ksplit_nw<EPI, true>(ctx, p, grid, fullk, nw);
+            return;
+        }
+    }
+    launch_ksplit_nw<EPI, false>(ctx, p, grid, fullk, nw);
 }
 
 // Sums split partials in split order, then applies the epilogue.
@@ -800,6 +935,17 @@ bool use_small(const Context &ctx, const GemmDesc &d) {
     return d.force_splits == 0 && big_tiles < cus_of(ctx) && d.k <= 1024;
 }
 
+// The K-split kernel for the small nn shapes of one matrix whose K is at most
+// 15 steps of 32, with the store, accumulate and SwiGLU epilogues, while the
+// 64x64 tiles number under two per CU (beyond that the small kernel's grid is
+// deep enough and its tiles share their operands through LDS).
+bool use_ksplit(const Context &ctx, const GemmDesc &d) {
+    const int64_t small_tiles = ((d.m + SBM - 1) / SBM) * ((d.n + SBN - 1) / SBN);
+    return use_small(ctx, d) && !d.ta && !d.tb && d.batch == 1 && d.k <= 480 &&
+           small_tiles < 2 * cus_of(ctx) &&
+           (d.epi == EPI_STORE || d.epi == EPI_ACCUM || d.epi == EPI_SWIGLU);
+}
+
 bool vec_a_of(const GemmDesc &d, const float *a, int64_t lda) {
     const int64_t off_limit = int64_t(1) << 29;  // interior byte offsets stay below 2^31
     return (lda % 4 == 0) && (d.batch == 1 || d.stride_a % 4 == 0) && aligned16(a) &&
@@ -847,9 +993,10 @@ void gemm(Context &ctx, const GemmDesc &d) {
     }
     const int cus = cus_of(ctx);
     const bool small = use_small(ctx, d);
+    const bool ksplit = use_ksplit(ctx, d);
     const GemmFusion fuse = gemm_fusion(ctx, d);
-    p.tiles_m = (int)(small ? (d.m + SBM - 1) / SBM : (d.m + BM - 1) / BM);
-    p.tiles_n = (int)(small ? (d.n + SBN - 1) / SBN : (d.n + BN - 1) / BN);
+    p.tiles_m = (int)(ksplit ? (d.m + 31) / 32 : small ? (d.m + SBM - 1) / SBM : (d.m + BM - 1) / BM);
+    p.tiles_n = (int)(ksplit ? (d.n + 31) / 32 : small ? (d.n + SBN - 1) / SBN : (d.n + BN - 1) / BN);
     // The interior path addresses a tile with byte offsets below 2^31 (128 rows of ld).
     const int64_t off_limit = int64_t(1) << 29;
     p.vec_a = vec_a_of(d, d.a, d.lda);
@@ -893,7 +1040,8 @@ void gemm(Context &ctx, const GemmDesc &d) {
                 splits *= 2;
         }
     }
-    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD || p.norm_w) splits = 1;
+    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD || p.norm_w || ksplit)
+        splits = 1;
     const int64_t kstep = small ? SBK : BK;
     const int64_t kt_per = (ktiles + splits - 1) / splits;
     p.k_per_split = kt_per * kstep;
@@ -919,7 +1067,15 @@ void gemm(Context &ctx, const GemmDesc &d) {
     if (tiles > 0x7fffffff || d.batch > 65535) fail(MMH_ERR_SHAPE, "gemm: grid too large");
     dim3 grid((unsigned)tiles, (unsigned)d.batch, (unsigned)splits);
     const int epi = splits > 1 ? EPI_STORE : d.epi;
-    if (epi == EPI_SWIGLU) {
+    if (ksplit) {
+        const bool fullk = d.k % 32 == 0 && p.vec_a && (!p.norm_w || aligned16(p.norm_w));
+        if (epi == EPI_SWIGLU)
+            launch_ksplit<EPI_SWIGLU>(ctx, p, grid, fullk);
+        else if (epi == EPI_ACCUM)
+            launch_ksplit<EPI_ACCUM>(ctx, p, grid, fullk);
+        else
+            launch_ksplit<EPI_STORE>(ctx, p, grid, fullk);
+    } else if (epi == EPI_SWIGLU) {
         if (d.ta || d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogue needs the nn form");
         launch<false, false, EPI_SWIGLU>(ctx, p, grid, small);
     } else if (epi == EPI_SWIGLU_BWD) {

@@ -76,7 +76,10 @@ def test_sweep_forward_and_backward(ctx, k, n):
 
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (12, 16, 32), (33, 17, 65),
                                    (129, 250, 131), (64, 4097, 40), (300, 8, 1000),
-                                   (2048, 128, 4096)])
+                                   (2048, 128, 4096),
+                                   # short-K shapes of the tiny preset and its edges
+                                   (2048, 128, 384), (2048, 352, 128), (2047, 480, 97),
+                                   (2000, 481, 50), (65, 33, 700)])
 @pytest.mark.parametrize("form", ["nn", "nt", "tn"])
 def test_ragged_shapes_and_accumulate(ctx, m, k, n, form):
     print(f"\n[gemm ragged] {form} m={m} k={k} n={n}", flush=True)
