@@ -354,6 +354,8 @@ def main():
                     help="skip timing training and evaluation fed from token shard files")
     ap.add_argument("--train-steps", type=int, default=5,
                     help="large-preset training steps to time after the forward (0: none)")
+    ap.add_argument("--no-mfma-probe", action="store_true",
+                    help="skip the fp32 MFMA issue-rate probe (the measured ceiling)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one add kernel over 2^26 floats (read 512 MiB, write "
                          "256 MiB) to calibrate HBM byte counters")
@@ -420,6 +422,11 @@ def main():
         breakdown[k] = e
     total_flops = sum(flops.values())
     log(f"GEMM {achieved:.1f} TFLOP/s over {gemm_launches} launches ({gemm_ms:.1f} ms)")
+    ceiling = None
+    if not a.no_mfma_probe:
+        ceiling = ctx.mfma_peak_tflops()
+        log(f"fp32 MFMA issue-rate probe (no memory traffic): {ceiling:.1f} TFLOP/s; "
+            f"the GEMMs reach {achieved / ceiling:.1%} of it")
 
     sweep = None
     if not a.no_sweep:
@@ -459,7 +466,10 @@ def main():
                      "traffic": GEMM_TRAFFIC_BYTES_PER_LAUNCH,
                      "traffic_source": "rocprofv3 FETCH_SIZE/WRITE_SIZE passes, scaled x2.0/x1.0",
                      "kernel": "gemm_f32_mfma (all GEMM launches of one large forward)",
-                     "launches": gemm_launches, "avg_launch_ms": round(gemm_ms / gemm_launches, 4)},
+                     "launches": gemm_launches, "avg_launch_ms": round(gemm_ms / gemm_launches, 4),
+                     "measured_mfma_ceiling": None if ceiling is None else round(ceiling, 1),
+                     "frac_of_measured_ceiling": None if ceiling is None else
+                     round(achieved / ceiling, 4)},
         "cpu_baseline": cpu,
         "extra": {
             "model_tflops": round(total_flops / (large["ms_per_step"] / 1000) / 1e12, 2),

@@ -72,6 +72,13 @@ int32_t mmh_context_destroy(mmh_handle ctx);
 int32_t mmh_synchronize(mmh_handle ctx);
 /* Device name (NUL-terminated, truncated to cap) and compute-unit count. */
 int32_t mmh_device_info(mmh_handle ctx, char *name, uint32_t cap, int32_t *cu_count);
+/* Diagnostic with no reference counterpart: the fp32 MFMA rate the whole chip
+ * sustains on register operands with no memory traffic (4 independent
+ * 32x32x2 chains per wave, 4 waves per SIMD, operands with pseudo-random
+ * mantissas changing every MFMA as a GEMM's do), in TFLOP/s: the practical
+ * ceiling under the published 157.3 TFLOP/s for the GEMM kernels (the clock
+ * the matrix cores hold drops with the operand bits they toggle). */
+int32_t mmh_mfma_peak_probe(mmh_handle ctx, double *tflops);
 
 /* Device memory owned by the caller through the context. */
 int32_t mmh_alloc(mmh_handle ctx, uint64_t bytes, void **out_dev);

@@ -877,6 +877,43 @@ void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, bool fullk) {
     launch_ksplit_nw<EPI, false>(ctx, p, grid, fullk, nw);
 }
 
+// ---- fp32 MFMA issue-rate probe ---------------------------------------------------
+// Every wave runs n MFMAs in 4 independent accumulator chains on register
+// operands, with no memory traffic but one store per lane at the end. As in a
+// GEMM, the operands change from one MFMA to the next: each lane cycles
+// through 8 values with pseudo-random mantissas in [-1, 1) (the matrix
+// cores' power, and so the clock they hold, depends on how many operand bits
+// toggle; fixed operands run near the peak clock). The result is the rate
+// the matrix cores sustain under full MFMA load on GEMM-like data: the
+// practical ceiling under the published peak for the GEMM kernels.
+__global__ __launch_bounds__(512) void mfma_peak_kernel(float *out, int n, uint32_t seed) {
+    floatx16 acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[c][r] = 0.0f;
+    float v[8];
+    uint32_t h = seed ^ (blockIdx.x * 0x9e3779b9u) ^ (threadIdx.x * 0x85ebca6bu);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        h ^= h << 13;
+        h ^= h >> 17;
+        h ^= h << 5;
+        v[i] = (float)(int32_t)h * (1.0f / 2147483648.0f);
+    }
+    for (int i = 0; i < n; i += 8) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            acc[j & 3] = __builtin_amdgcn_mfma_f32_32x32x2f32(v[j], v[(j + 3) & 7], acc[j & 3], 0, 0, 0);
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s += acc[c][r];
+    out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+}
+
 // Sums split partials in split order, then applies the epilogue.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial,
@@ -1102,6 +1139,30 @@ void gemm(Context &ctx, const GemmDesc &d) {
         launch_rope_strided(ctx, d.c, d.rope_seq * d.ldc, d.rope_hd, d.ldc, d.m / d.rope_seq,
                             d.rope_cols / d.rope_hd, d.rope_seq, d.rope_hd, d.rope_cos,
                             d.rope_sin);
+}
+
+double mfma_peak_tflops(Context &ctx) {
+    // two 512-thread workgroups per CU (4 waves per SIMD), 8192 MFMAs per wave
+    // (about 0.5 ms a launch); 20 launches first bring the clock to its
+    // steady state under this load, then 40 are timed
+    const int blocks = 2 * cus_of(ctx), threads = 512, n = 8192;
+    float *out = static_cast<float *>(ctx.get_scratch((size_t)blocks * threads * 4));
+    for (int i = 0; i < 20; ++i)
+        hipLaunchKernelGGL(mfma_peak_kernel, dim3(blocks), dim3(threads), 0, ctx.stream, out, n,
+                           1u + (uint32_t)i);
+    check_hip(hipGetLastError(), "mfma probe launch");
+    const int reps = 40;
+    check_hip(hipEventRecord(ctx.t0, ctx.stream), "event record");
+    for (int i = 0; i < reps; ++i)
+        hipLaunchKernelGGL(mfma_peak_kernel, dim3(blocks), dim3(threads), 0, ctx.stream, out, n,
+                           100u + (uint32_t)i);
+    check_hip(hipGetLastError(), "mfma probe launch");
+    check_hip(hipEventRecord(ctx.t1, ctx.stream), "event record");
+    check_hip(hipEventSynchronize(ctx.t1), "event sync");
+    float ms = 0.0f;
+    check_hip(hipEventElapsedTime(&ms, ctx.t0, ctx.t1), "elapsed time");
+    const double flops = 2.0 * 32 * 32 * 2 * (double)n * (blocks * threads / 64) * reps;
+    return flops / (ms * 1e-3) / 1e12;
 }
 
 }  // namespace mmh

@@ -121,6 +121,9 @@ struct GemmFusion {
     bool norm = false, rope = false;
 };
 GemmFusion gemm_fusion(const Context &ctx, const GemmDesc &d);
+// TFLOP/s of an fp32 MFMA issue-rate probe (register operands, no memory
+// traffic) over the whole chip; uses the context's scratch and its events.
+double mfma_peak_tflops(Context &ctx);
 
 // ---- bandwidth kernels ------------------------------------------------------
 void launch_embedding(Context &ctx, const float *table, int64_t d, const int32_t *ids_dev,

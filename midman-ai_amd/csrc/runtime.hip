@@ -184,6 +184,14 @@ int32_t mmh_device_info(mmh_handle ctx, char *name, uint32_t cap, int32_t *cu_co
     });
 }
 
+int32_t mmh_mfma_peak_probe(mmh_handle ctx, double *tflops) {
+    return guard([&] {
+        need(tflops, "tflops");
+        *tflops = mfma_peak_tflops(context(ctx));
+        return MMH_OK;
+    });
+}
+
 int32_t mmh_alloc(mmh_handle ctx, uint64_t bytes, void **out_dev) {
     return guard([&] {
         need(out_dev, "out_dev");

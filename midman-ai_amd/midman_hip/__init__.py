@@ -81,6 +81,7 @@ _SIGNATURES = {
     "mmh_context_destroy": [_h],
     "mmh_synchronize": [_h],
     "mmh_device_info": [_h, ctypes.c_char_p, ctypes.c_uint32, ctypes.POINTER(_i32)],
+    "mmh_mfma_peak_probe": [_h, ctypes.POINTER(ctypes.c_double)],
     "mmh_alloc": [_h, ctypes.c_uint64, ctypes.POINTER(_vp)],
     "mmh_free": [_h, _vp],
     "mmh_upload": [_h, _vp, _vp, ctypes.c_uint64],
@@ -289,6 +290,13 @@ class Context:
         cu = _i32()
         check(lib().mmh_device_info(self.handle, buf, 256, ctypes.byref(cu)))
         return buf.value.decode(), cu.value
+
+    def mfma_peak_tflops(self) -> float:
+        """The fp32 MFMA rate the chip sustains with no memory traffic (a
+        diagnostic ceiling under the published peak)."""
+        v = ctypes.c_double()
+        check(lib().mmh_mfma_peak_probe(self.handle, ctypes.byref(v)))
+        return v.value
 
     def empty(self, shape, dtype=np.float32) -> "DeviceArray":
         return DeviceArray(self, shape, dtype)

@@ -253,3 +253,11 @@ def test_cross_entropy_known_values_and_errors(ctx):
         mh.cross_entropy(ctx, L([[0.0, 0.0, 0.0]]), [3])
     with pytest.raises(mh.ShapeError):
         mh.cross_entropy(ctx, L([[0.0, 0.0, 0.0]]), [0, 1])
+
+
+def test_mfma_peak_probe_is_a_plausible_ceiling(ctx):
+    """The diagnostic MFMA probe runs and reports a rate under the published
+    157.3 TFLOP/s fp32 matrix peak (it cannot exceed the peak clock's rate)."""
+    tf = ctx.mfma_peak_tflops()
+    print(f"\n  fp32 MFMA probe: {tf:.1f} TFLOP/s", flush=True)
+    assert 50.0 < tf <= 157.3 * 1.02
