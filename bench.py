@@ -285,6 +285,52 @@ def gemm_sweep(mh, ctx, reps=10):
     return rows
 
 
+def time_bandwidth(mh, ctx, reps=20):
+    """The op-level bandwidth kernels at the large preset's shapes, each timed
+    as `reps` back-to-back launches between two HIP events: the per-launch
+    time then holds the dispatch gap between consecutive kernels but not the
+    event overhead that the per-class breakdown adds to every short kernel.
+    Bytes are algorithmic (each input read once, each output written once)."""
+    rng = np.random.default_rng(0)
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        ctx.synchronize()
+        ctx.timer_start()
+        for _ in range(reps):
+            fn()
+        return ctx.timer_stop() / reps
+
+    def entry(shape, ms, nbytes):
+        gbs = nbytes / (ms / 1000) / 1e9
+        return {"shape": shape, "us": round(ms * 1000, 2), "gbs": round(gbs, 1),
+                "frac_of_hbm": round(gbs / PEAK_HBM_GBS, 3)}
+
+    out = {}
+    x = ctx.to_device(rng.standard_normal((4096, 2048)).astype(np.float32))
+    w = ctx.to_device(np.ones(2048, np.float32))
+    y = ctx.empty((4096, 2048))
+    ms = timed(lambda: mh.rms_norm(ctx, x, w, 1e-5, y))
+    out["rms_norm"] = entry("4096 rows x 2048", ms, 2 * x.size * 4 + 2048 * 4)
+    for b in (x, w, y):
+        b.free()
+    tabs = mh.RotaryTables(ctx, 128, 1024)
+    q = ctx.to_device(rng.standard_normal((4 * 24, 1024, 128)).astype(np.float32))
+    qo = ctx.empty(q.shape)
+    ms = timed(lambda: mh.apply_rope(ctx, q, tabs, qo))
+    out["apply_rope"] = entry("B4 x 24 q/k heads x T1024 x 128", ms, 2 * q.size * 4)
+    for b in (q, qo, tabs.cos, tabs.sin):
+        b.free()
+    n = 1 << 26
+    a, b2, c = ctx.empty((n,)), ctx.empty((n,)), ctx.empty((n,))
+    ms = timed(lambda: mh.add(ctx, a, b2, c))
+    out["add"] = entry("2^26 floats", ms, 3 * n * 4)
+    for t in (a, b2, c):
+        t.free()
+    return out
+
+
 def cpu_baseline_large():
     """The oracle (a C restatement of the reference CPU path: 4x16 AVX tile,
     separate multiply and add, glibc libm) on ONE host core, on a bounded
@@ -428,6 +474,10 @@ def main():
         log(f"fp32 MFMA issue-rate probe (no memory traffic): {ceiling:.1f} TFLOP/s; "
             f"the GEMMs reach {achieved / ceiling:.1%} of it")
 
+    bandwidth = time_bandwidth(mh, ctx)
+    log("bandwidth kernels (back-to-back launches): " + ", ".join(
+        f"{k} {v['gbs']:.0f} GB/s ({v['frac_of_hbm']:.0%})" for k, v in bandwidth.items()))
+
     sweep = None
     if not a.no_sweep:
         sweep = gemm_sweep(mh, ctx)
@@ -476,6 +526,10 @@ def main():
             "pcie_inclusive_tokens_per_s": round(large["pcie_inclusive_tokens_per_s"], 1),
             "large_loss": large["loss"],
             "kernel_classes": breakdown,
+            "kernel_classes_timing": "HIP events around each launch of one forward; a short "
+                                     "kernel's rate includes a few us of launch gap (kernel "
+                                     "durations: profiles/large_forward_kernel_trace.md)",
+            "bandwidth_kernels": bandwidth,
             "checkpoint": large["checkpoint"],
             "train_step": None if not large["train"] else {
                 "workload": "large preset training step B4 T1024: forward + loss + backward "
