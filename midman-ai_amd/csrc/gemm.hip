@@ -752,9 +752,14 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
 // x * w feeds the MFMAs, the sums of squares of x are gathered per lane and
 // combined over the lane halves and then the waves, and each row's 1/rms
 // scales the summed results.
-// FULLK: K is a multiple of 32 and the A rows (and the norm weights) are
-// 16-byte aligned; otherwise every load is predicated on k < K.
-template <int EPI, bool NORM, int NW, bool FULLK>
+// MODE: 2 when K is a multiple of 32 and the A rows (and the norm weights)
+// are 16-byte aligned: float4 reads, no predicates; 1 when only the rows are
+// aligned: a lane whose 16 k values all lie below K reads them as float4,
+// the lanes of the partial last step one predicated value at a time; 0
+// otherwise: every read predicated. (Keeping the predicated path out of mode
+// 2 keeps its registers low; a separate tail step measured slower than the
+// per-lane test of mode 1.)
+template <int EPI, bool NORM, int NW, int MODE>
 __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     __shared__ float part[NW][16][64];
     __shared__ float sm_ss[NW][32];
@@ -775,8 +780,9 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     float ss = 0.0f;
     for (int st = wave; st < nsteps; st += NW) {
         const int64_t kb = (int64_t)st * 32 + 16 * lk;  // this lane's first k of the step
+        const bool whole = MODE == 2 || (MODE == 1 && kb + 16 <= K);
         float a[16], b[16];
-        if (FULLK) {
+        if (whole) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float4 v = reinterpret_cast<const float4 *>(arow + kb)[i];
@@ -790,11 +796,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
             for (int j = 0; j < 16; ++j) a[j] = kb + j < K ? arow[kb + j] : 0.0f;
         }
 #pragma unroll
-        for (int j = 0; j < 16; ++j)
-            b[j] = (FULLK || kb + j < K) ? bcol[(kb + j) * p.ldb] : 0.0f;
+        for (int j = 0; j < 16; ++j) b[j] = (whole || kb + j < K) ? bcol[(kb + j) * p.ldb] : 0.0f;
         if (NORM) {
             float w[16];
-            if (FULLK) {
+            if (whole) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float4 v = reinterpret_cast<const float4 *>(p.norm_w + kb)[i];
@@ -849,32 +854,35 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     }
 }
 
+template <int EPI, bool NORM, int MODE>
+void launch_ksplit_mode(Context &ctx, const KParams &p, dim3 grid, int nw) {
+    if (nw == 4)
+        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 4, MODE>), grid, dim3(256), 0, ctx.stream, p);
+    else
+        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 8, MODE>), grid, dim3(512), 0, ctx.stream, p);
+}
+
 template <int EPI, bool NORM>
-void launch_ksplit_nw(Context &ctx, const KParams &p, dim3 grid, bool fullk, int nw) {
-    if (nw == 4) {
-        if (fullk)
-            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 4, true>), grid, dim3(256), 0, ctx.stream, p);
-        else
-            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 4, false>), grid, dim3(256), 0, ctx.stream, p);
-    } else {
-        if (fullk)
-            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 8, true>), grid, dim3(512), 0, ctx.stream, p);
-        else
-            hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 8, false>), grid, dim3(512), 0, ctx.stream, p);
-    }
+void launch_ksplit_nw(Context &ctx, const KParams &p, dim3 grid, bool vec, int nw) {
+    if (vec && p.k % 32 == 0)
+        launch_ksplit_mode<EPI, NORM, 2>(ctx, p, grid, nw);
+    else if (vec)
+        launch_ksplit_mode<EPI, NORM, 1>(ctx, p, grid, nw);
+    else
+        launch_ksplit_mode<EPI, NORM, 0>(ctx, p, grid, nw);
 }
 
 // Four waves up to four K steps (one step each), eight beyond.
 template <int EPI>
-void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, bool fullk) {
+void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, bool vec) {
     const int nw = (p.k + 31) / 32 <= 4 ? 4 : 8;
     if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
         if (p.norm_w) {
-            launch_ksplit_nw<EPI, true>(ctx, p, grid, fullk, nw);
+            launch_ksplit_nw<EPI, true>(ctx, p, grid, vec, nw);
             return;
         }
     }
-    launch_ksplit_nw<EPI, false>(ctx, p, grid, fullk, nw);
+    launch_ksplit_nw<EPI, false>(ctx, p, grid, vec, nw);
 }
 
 // ---- fp32 MFMA issue-rate probe ---------------------------------------------------
@@ -1105,13 +1113,14 @@ void gemm(Context &ctx, const GemmDesc &d) {
     dim3 grid((unsigned)tiles, (unsigned)d.batch, (unsigned)splits);
     const int epi = splits > 1 ? EPI_STORE : d.epi;
     if (ksplit) {
-        const bool fullk = d.k % 32 == 0 && p.vec_a && (!p.norm_w || aligned16(p.norm_w));
+        // vec_a holds lda % 4 == 0 and a 16-byte aligned A
+        const bool vec = p.vec_a && (!p.norm_w || aligned16(p.norm_w));
         if (epi == EPI_SWIGLU)
-            launch_ksplit<EPI_SWIGLU>(ctx, p, grid, fullk);
+            launch_ksplit<EPI_SWIGLU>(ctx, p, grid, vec);
         else if (epi == EPI_ACCUM)
-            launch_ksplit<EPI_ACCUM>(ctx, p, grid, fullk);
+            launch_ksplit<EPI_ACCUM>(ctx, p, grid, vec);
         else
-            launch_ksplit<EPI_STORE>(ctx, p, grid, fullk);
+            launch_ksplit<EPI_STORE>(ctx, p, grid, vec);
     } else if (epi == EPI_SWIGLU) {
         if (d.ta || d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogue needs the nn form");
         launch<false, false, EPI_SWIGLU>(ctx, p, grid, small);
