@@ -68,10 +68,14 @@ def model_bytes(cfg, B, T):
     outputs written once, f32)."""
     V, d, L = (int(v) for v in cfg[:3])
     N = B * T
+    tiles = (V + 127) // 128
     return {
         "embedding": 8 * N * d + 4 * N,
         "rms_norm": (2 * L + 1) * (8 * N * d + 4 * d),
-        "loss": 4 * N * V + 4 * N,
+        # the loss folded into the head GEMM: this class merges each row's
+        # per-tile (max, sum) pairs (read) into the row term (written), then
+        # the f64 mean reads the row terms
+        "loss": 8 * N * tiles + 4 * N + 4 * N + 4 * N,
     }
 
 

@@ -325,20 +325,39 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(AttnP p) {
     // Operands of one key tile: kr[s] = K[key lq][lh*NS + s] (S^T's A), and
     // vr[s][db] = V[key 8*(s/4) + 4*lh + s%4][NDB*lq + db] (O^T's A).
     // kn/vn receive the wave's next tile while the current one is used.
+    // Every read is unconditional (keys past T read row T-1, head dims past
+    // HD read dim HD-1: real, finite values whose scores are masked, whose P
+    // is 0, or whose output rows are never stored), so the compiler can keep
+    // the next tile's reads in flight instead of waiting on each one.
     float kr[NS], vr[16][NDB], kn[NS], vn[16][NDB];
     auto load_tile = [&](int kt, float (&kd)[NS], float (&vd)[16][NDB])
                          __attribute__((always_inline)) {
         const int key = kt * 32 + lq;
         const float *ks = K + (int64_t)min(key, T - 1) * p.skt + lh * NS;
+        if constexpr (NS % 4 == 0) {
 #pragma unroll
-        for (int s = 0; s < NS; ++s) kd[s] = key < T ? ks[s] : 0.0f;
+            for (int s = 0; s < NS / 4; ++s) {
+                const float4 v = reinterpret_cast<const float4 *>(ks)[s];
+                kd[4 * s + 0] = v.x;
+                kd[4 * s + 1] = v.y;
+                kd[4 * s + 2] = v.z;
+                kd[4 * s + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < NS; ++s) kd[s] = ks[s];
+        }
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
-            const int vk = kt * 32 + 8 * (s >> 2) + 4 * lh + (s & 3);
-            const float *vs = V + (int64_t)min(vk, T - 1) * p.svt + NDB * lq;
-#pragma unroll
-            for (int db = 0; db < NDB; ++db)
-                vd[s][db] = (vk < T && NDB * lq + db < HD) ? vs[db] : 0.0f;
+            const int vk = min(kt * 32 + 8 * (s >> 2) + 4 * lh + (s & 3), T - 1);
+            const float *vs = V + (int64_t)vk * p.svt;
+            if constexpr (NDB == 2) {
+                const float2 v2 = reinterpret_cast<const float2 *>(vs)[lq];
+                vd[s][0] = v2.x;
+                vd[s][NDB > 1 ? 1 : 0] = v2.y;
+            } else {
+                vd[s][0] = vs[HD >= 32 ? lq : min(lq, HD - 1)];
+            }
         }
     };
 

@@ -68,6 +68,9 @@ struct KParams {
     float norm_eps;
     const float *rope_cos, *rope_sin;
     int rope_seq, rope_hd, rope_cols;
+    // EPI_CE (128x128 kernel): targets in, per-tile (max, sum) pairs and target logits out
+    const int32_t *ce_targets;
+    float *ce_part, *ce_zt;
 };
 
 // Row strides (floats) of the k-major LDS stages: even, so the 8-byte operand
@@ -81,6 +84,38 @@ template <bool TB>
 struct LdsB {
     static constexpr int S = BN + (TB ? 2 : 4);
 };
+
+// Reductions over each 32-lane half of a wave with DPP moves (quad permutes,
+// then rotations within a 16-lane row) and one swizzle across the two rows of
+// the half. For the max every lane ends with the result; for the sum the
+// lanes associate the terms differently, and lane 0 of the half (the one read)
+// always the same way.
+__device__ __forceinline__ float dpp_f(float v, int ctrl) {
+    switch (ctrl) {
+        case 0xB1: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+        case 0x4E: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+        case 0x124: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x124, 0xF, 0xF, false));
+        default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+    }
+}
+__device__ __forceinline__ float swap16_f(float v) {
+    // ds_swizzle bit mode: and 0x1f, or 0, xor 0x10 (lane ^ 16 within 32)
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+}
+__device__ __forceinline__ float half_max32(float v) {
+    v = fmaxf(v, dpp_f(v, 0xB1));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f(v, 0x4E));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f(v, 0x124));  // row_ror:4
+    v = fmaxf(v, dpp_f(v, 0x128));  // row_ror:8
+    return fmaxf(v, swap16_f(v));
+}
+__device__ __forceinline__ float half_sum32(float v) {
+    v += dpp_f(v, 0xB1);
+    v += dpp_f(v, 0x4E);
+    v += dpp_f(v, 0x124);
+    v += dpp_f(v, 0x128);
+    return v + swap16_f(v);
+}
 
 // The K loop of one 128x128 tile; see the file comment.
 template <bool TA, bool TB, bool FAST>
@@ -328,6 +363,49 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
                     if (col + 1 < N) P[row * N + col + 1] = acc[i][1][r];
                 }
             }
+        return;
+    }
+    if constexpr (EPI == EPI_CE) {
+        // Cross-entropy partials of this tile's columns (ops_reduce.rs:236-259
+        // split by column tiles): per row, the max of the logits and the sum of
+        // exp(z - max) over the lane's two columns, over the 32 lanes of its
+        // half by xor exchanges, then over the two waves sharing the rows
+        // through LDS. The lane holding a row's target column keeps its logit.
+        __shared__ float ce_m[2][BM], ce_s[2][BM];
+        __shared__ int ce_t[BM];
+        if (tid < BM) ce_t[tid] = m0 + tid < M ? p.ce_targets[m0 + tid] : -1;
+        __syncthreads();
+        constexpr float kLog2e = 1.4426950408889634f;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
+                const int64_t row = m0 + rl;
+                const float v0 = acc[i][0][r], v1 = acc[i][1][r];
+                const float x0 = col < N ? v0 : -INFINITY, x1 = col + 1 < N ? v1 : -INFINITY;
+                const float mx = half_max32(fmaxf(x0, x1));
+                // exp(z - max) through the hardware's exp2 (no flush concern: the
+                // terms that matter are within a few hundred of 1)
+                const float e = half_sum32(
+                    mx == -INFINITY ? 0.0f
+                                    : __builtin_amdgcn_exp2f((x0 - mx) * kLog2e) +
+                                          __builtin_amdgcn_exp2f((x1 - mx) * kLog2e));
+                if (lr == 0) {
+                    ce_m[wn][rl] = mx;
+                    ce_s[wn][rl] = e;
+                }
+                const int t = ce_t[rl];
+                if (t == col) p.ce_zt[row] = v0;
+                if (t == col + 1) p.ce_zt[row] = v1;
+            }
+        __syncthreads();
+        if (tid < BM && m0 + tid < M) {
+            float m = ce_m[0][tid], sum = ce_s[0][tid];
+            lse_merge(m, sum, ce_m[1][tid], ce_s[1][tid]);
+            reinterpret_cast<float2 *>(p.ce_part)[(m0 + tid) * p.tiles_n + tn] =
+                make_float2(m, sum);
+        }
         return;
     }
     float *C = p.c + batch * p.stride_c;
@@ -1010,8 +1088,16 @@ GemmFusion gemm_fusion(const Context &ctx, const GemmDesc &d) {
     return f;
 }
 
+int64_t gemm_ce_tiles(const Context &ctx, const GemmDesc &d) {
+    if (use_small(ctx, d) || d.batch != 1 || d.force_splits || d.ta || d.norm_w || d.rope_cos)
+        return 0;
+    return (d.n + BN - 1) / BN;
+}
+
 void gemm(Context &ctx, const GemmDesc &d) {
     if (d.m <= 0 || d.n <= 0 || d.k <= 0 || d.batch <= 0) fail(MMH_ERR_SHAPE, "gemm: empty shape");
+    if (d.epi == EPI_CE && (gemm_ce_tiles(ctx, d) == 0 || !d.ce_targets || !d.ce_part || !d.ce_zt))
+        fail(MMH_ERR_ARGUMENT, "gemm: the loss folds only into the 128x128 kernel of one matrix");
     KParams p{};
     p.a = d.a;
     p.b = d.b;
@@ -1029,6 +1115,9 @@ void gemm(Context &ctx, const GemmDesc &d) {
     p.resid = d.resid;
     p.aux = d.aux;
     p.ldaux = d.ldaux;
+    p.ce_targets = d.ce_targets;
+    p.ce_part = d.ce_part;
+    p.ce_zt = d.ce_zt;
     if (d.epi == EPI_SWIGLU_BWD || (d.epi == EPI_SWIGLU && d.aux)) {
         if (!d.aux || d.ldaux < (d.epi == EPI_SWIGLU ? d.n : 2 * d.n) || d.ldaux % 4 ||
             !aligned16(d.aux) ||
@@ -1085,7 +1174,8 @@ void gemm(Context &ctx, const GemmDesc &d) {
                 splits *= 2;
         }
     }
-    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD || p.norm_w || ksplit)
+    if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD || d.epi == EPI_CE ||
+        p.norm_w || ksplit)
         splits = 1;
     const int64_t kstep = small ? SBK : BK;
     const int64_t kt_per = (ktiles + splits - 1) / splits;
@@ -1121,6 +1211,13 @@ void gemm(Context &ctx, const GemmDesc &d) {
             launch_ksplit<EPI_ACCUM>(ctx, p, grid, vec);
         else
             launch_ksplit<EPI_STORE>(ctx, p, grid, vec);
+    } else if (epi == EPI_CE) {
+        if (d.tb)
+            hipLaunchKernelGGL((gemm_f32_mfma<false, true, EPI_CE>), grid, dim3(256), 0,
+                               ctx.stream, p);
+        else
+            hipLaunchKernelGGL((gemm_f32_mfma<false, false, EPI_CE>), grid, dim3(256), 0,
+                               ctx.stream, p);
     } else if (epi == EPI_SWIGLU) {
         if (d.ta || d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogue needs the nn form");
         launch<false, false, EPI_SWIGLU>(ctx, p, grid, small);

@@ -31,6 +31,23 @@ __device__ __forceinline__ float2 swiglu_bwd_f(float dh, float g, float u) {
     return make_float2(__fmul_rn(dsilu, deriv), du);
 }
 
+// Merges a log-sum-exp pair (m2, s2) into (m, s): the pair (max, sum of
+// exp(z - max)) of the union, -inf / 0 standing for an empty set.
+__device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2) {
+    if (m2 == -INFINITY) return;
+    if (m == -INFINITY) {
+        m = m2;
+        s = s2;
+        return;
+    }
+    if (m2 > m) {
+        s = s * expf(m - m2) + s2;
+        m = m2;
+    } else {
+        s = s + s2 * expf(m2 - m);
+    }
+}
+
 // An error that the C-ABI boundary turns into a status code + message.
 struct Error {
     int32_t status;
@@ -83,7 +100,13 @@ void release_models_of(mmh_handle ctx);
 // EPI_SWIGLU: columns (2f, 2f+1) are (gate f, up f); C[row][f] = silu(gate)*up,
 // and aux (when set) receives the raw pair. EPI_SWIGLU_BWD: acc is dh [M, ff];
 // with (g, u) = aux[row][2f, 2f+1], C[row][2f, 2f+1] = (dg, du) (C may be aux).
-enum Epilogue : int { EPI_STORE = 0, EPI_ACCUM = 1, EPI_SWIGLU = 2, EPI_SWIGLU_BWD = 3 };
+// EPI_CE: C is not written; the products are logits, and each 128-column tile
+// tn of row i leaves ce_part[(i * tiles + tn) * 2 + {0, 1}] = (max, sum of
+// exp(z - max)) over its columns, and the tile holding column ce_targets[i]
+// leaves that logit in ce_zt[i] (the head GEMM with the loss folded in; see
+// gemm_ce_tiles and launch_ce_combine).
+enum Epilogue : int { EPI_STORE = 0, EPI_ACCUM = 1, EPI_SWIGLU = 2, EPI_SWIGLU_BWD = 3,
+                      EPI_CE = 4 };
 
 struct GemmDesc {
     const float *a = nullptr;
@@ -112,6 +135,10 @@ struct GemmDesc {
     // otherwise by the rope kernel after the product. Same bits either way.
     const float *rope_cos = nullptr, *rope_sin = nullptr;
     int64_t rope_seq = 0, rope_hd = 0, rope_cols = 0;
+    // EPI_CE (batch 1, the 128x128 kernel only): targets [m] on the device,
+    // partials [m, gemm_ce_tiles, 2] and target logits [m] out.
+    const int32_t *ce_targets = nullptr;
+    float *ce_part = nullptr, *ce_zt = nullptr;
 };
 
 void gemm(Context &ctx, const GemmDesc &d);
@@ -121,6 +148,9 @@ struct GemmFusion {
     bool norm = false, rope = false;
 };
 GemmFusion gemm_fusion(const Context &ctx, const GemmDesc &d);
+// Column tiles of an EPI_CE product of d's shape (the partials per row), or 0
+// when the loss cannot fold into it (the small-shape kernels, batches).
+int64_t gemm_ce_tiles(const Context &ctx, const GemmDesc &d);
 // TFLOP/s of an fp32 MFMA issue-rate probe (register operands, no memory
 // traffic) over the whole chip; uses the context's scratch and its events.
 double mfma_peak_tflops(Context &ctx);
@@ -140,6 +170,11 @@ void launch_rope(Context &ctx, const float *x, int64_t bh, int64_t t, int64_t hd
 // Row losses then their f64 mean; loss_dev receives one float.
 void launch_cross_entropy(Context &ctx, const float *logits, const int32_t *targets_dev,
                           int64_t n, int64_t v, float *row_loss, float *loss_dev);
+// The loss from the partials of an EPI_CE head GEMM: each row's (max, sum)
+// pairs merged over its tiles, row loss = max + ln(sum) - z[target], then the
+// f64 mean as launch_cross_entropy.
+void launch_ce_combine(Context &ctx, const float *part, int64_t tiles, const float *zt,
+                       int64_t n, float *row_loss, float *loss_dev);
 void launch_pack_cols(Context &ctx, const float *src, int64_t rows, int64_t cols, float *dst,
                       int64_t ld_dst, int64_t col_off);
 void launch_pack_gate_up(Context &ctx, const float *wg, const float *wu, int64_t rows,

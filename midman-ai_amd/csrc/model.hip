@@ -232,7 +232,8 @@ struct Model {
     int64_t cap = 0;
     float *act = nullptr;
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *cb = nullptr, *h = nullptr,
-          *logits = nullptr, *row_loss = nullptr, *loss = nullptr;
+          *logits = nullptr, *row_loss = nullptr, *loss = nullptr, *ce_part = nullptr,
+          *ce_zt = nullptr;
     int32_t *ids = nullptr, *tgt = nullptr;
     int64_t staged_n = 0;
     bool staged_targets = false;
@@ -314,19 +315,23 @@ struct Model {
         }
         const int64_t d = cfg.d;
         auto al = [](int64_t v) { return (v + 63) / 64 * 64; };
-        const int64_t sizes[] = {al(n * d), al(n * d), al(n * qkv_cols()), al(n * d),
-                                 al(n * cfg.ff), al(n * cfg.vocab), al(n), 64, al(n), al(n)};
+        // the loss folded into the head GEMM: (max, sum) per row and 128-column tile
+        const int64_t ce_tiles = (cfg.vocab + 127) / 128;
+        const int64_t sizes[] = {al(n * d),     al(n * d),         al(n * qkv_cols()),
+                                 al(n * d),     al(n * cfg.ff),    al(n * cfg.vocab),
+                                 al(n),         64,                al(n * ce_tiles * 2),
+                                 al(n),         al(n),             al(n)};
         int64_t total = 0;
         for (int64_t s : sizes) total += s;
         check_hip(hipMalloc(&act, (size_t)total * 4), "activation alloc");
         float *p = act;
-        float **slots[] = {&x, &xn, &qkv, &cb, &h, &logits, &row_loss, &loss};
-        for (int i = 0; i < 8; ++i) {
+        float **slots[] = {&x, &xn, &qkv, &cb, &h, &logits, &row_loss, &loss, &ce_part, &ce_zt};
+        for (int i = 0; i < 10; ++i) {
             *slots[i] = p;
             p += sizes[i];
         }
         ids = reinterpret_cast<int32_t *>(p);
-        p += sizes[8];
+        p += sizes[10];
         tgt = reinterpret_cast<int32_t *>(p);
         cap = n;
         staged_n = 0;
@@ -404,8 +409,11 @@ struct Model {
     }
 
     // model.rs:127-165 on the staged ids, then model.rs:174-183 when with_loss.
-    // Queued on the context stream; nothing waits.
-    void enqueue(int64_t batch, int64_t seq, bool with_loss, Prof *prof = nullptr) {
+    // Without want_logits the loss folds into the head GEMM where it can
+    // (EPI_CE) and the logits are never written. Queued on the context
+    // stream; nothing waits.
+    void enqueue(int64_t batch, int64_t seq, bool with_loss, bool want_logits,
+                 Prof *prof = nullptr) {
         const int64_t n = batch * seq;
         if (n != staged_n || n > cap)
             fail(MMH_ERR_ARGUMENT, "no tokens staged for batch " + std::to_string(batch) +
@@ -458,6 +466,17 @@ struct Model {
             hg.b = lm_head();
             hg.ldb = V;
         }
+        const int64_t ce_tiles = with_loss && !want_logits ? gemm_ce_tiles(c, hg) : 0;
+        if (ce_tiles > 0) {
+            hg.epi = EPI_CE;
+            hg.ce_targets = tgt;
+            hg.ce_part = ce_part;
+            hg.ce_zt = ce_zt;
+            timed(prof, MMH_PROF_GEMM_HEAD, [&] { gemm(c, hg); });
+            timed(prof, MMH_PROF_LOSS,
+                  [&] { launch_ce_combine(c, ce_part, ce_tiles, ce_zt, n, row_loss, loss); });
+            return;
+        }
         timed(prof, MMH_PROF_GEMM_HEAD, [&] { gemm(c, hg); });
         if (with_loss)
             timed(prof, MMH_PROF_LOSS,
@@ -474,7 +493,7 @@ struct Model {
             return;
         }
         if (!(warm_b == batch && warm_t == seq && warm_act == act)) {
-            enqueue(batch, seq, true);
+            enqueue(batch, seq, true, false);
             warm_b = batch;
             warm_t = seq;
             warm_act = act;
@@ -483,7 +502,7 @@ struct Model {
         drop_graph();
         check_hip(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "capture");
         try {
-            enqueue(batch, seq, true);
+            enqueue(batch, seq, true, false);
         } catch (...) {
             hipGraph_t g = nullptr;
             (void)hipStreamEndCapture(ctx->stream, &g);
@@ -501,7 +520,7 @@ struct Model {
     void run(const int32_t *inputs, const int32_t *targets, int64_t batch, int64_t seq,
              float *logits_out, float *loss_out) {
         stage(inputs, loss_out ? targets : nullptr, batch, seq);
-        enqueue(batch, seq, loss_out != nullptr);
+        enqueue(batch, seq, loss_out != nullptr, logits_out != nullptr);
         Context &c = *ctx;
         if (loss_out)
             check_hip(hipMemcpyAsync(loss_out, loss, 4, hipMemcpyDeviceToHost, c.stream),
@@ -1101,7 +1120,7 @@ int32_t mmh_model_profile(mmh_handle model_h, int64_t batch, int64_t seq, float 
             }
         } cleanup{prof};
         check_hip(hipStreamSynchronize(m.ctx->stream), "profile sync");
-        m.enqueue(batch, seq, true, &prof);
+        m.enqueue(batch, seq, true, false, &prof);
         check_hip(hipStreamSynchronize(m.ctx->stream), "profile sync");
         for (int i = 0; i < MMH_PROF_CLASSES; ++i) {
             class_ms[i] = 0.0f;

@@ -188,20 +188,6 @@ __global__ __launch_bounds__(256) void rope_kernel(const float *__restrict__ x, 
 // and adds the chunk's 16 exponentials; (max, sum) pairs then merge across the
 // workgroup. The row term is formed as the reference forms it,
 // (max + ln(sum)) - z[target], in f32.
-__device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2) {
-    if (m2 == -INFINITY) return;
-    if (m == -INFINITY) {
-        m = m2;
-        s = s2;
-        return;
-    }
-    if (m2 > m) {
-        s = s * expf(m - m2) + s2;
-        m = m2;
-    } else {
-        s = s + s2 * expf(m2 - m);
-    }
-}
 
 __global__ __launch_bounds__(256) void ce_rows_kernel(const float *__restrict__ logits,
                                                       const int32_t *__restrict__ targets,
@@ -259,6 +245,30 @@ __global__ __launch_bounds__(256) void ce_rows_kernel(const float *__restrict__ 
         const float lse = __fadd_rn(M, logf(S));
         row_loss[row] = __fsub_rn(lse, z[targets[row]]);
     }
+}
+
+// The row terms from the head GEMM's per-tile partials (EPI_CE): one wave per
+// row; lane l merges tiles l, l + 64, ... in order, then the lanes merge in a
+// fixed tree; the row term is (max + ln(sum)) - z[target] as in ce_rows_kernel.
+__global__ __launch_bounds__(256) void ce_combine_kernel(const float *__restrict__ part,
+                                                         int64_t tiles,
+                                                         const float *__restrict__ zt,
+                                                         int64_t n, float *__restrict__ row_loss) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    const float2 *pr = reinterpret_cast<const float2 *>(part) + row * tiles;
+    float m = -INFINITY, s = 0.0f;
+    for (int64_t j = lane; j < tiles; j += 64) {
+        const float2 q = pr[j];
+        lse_merge(m, s, q.x, q.y);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, 64), s2 = __shfl_xor(s, off, 64);
+        lse_merge(m, s, m2, s2);
+    }
+    if (lane == 0) row_loss[row] = __fsub_rn(__fadd_rn(m, logf(s)), zt[row]);
 }
 
 // Mean of the row terms in f64 (ops_reduce.rs:258-259), fixed reduction order.
@@ -381,6 +391,17 @@ void launch_cross_entropy(Context &ctx, const float *logits, const int32_t *targ
     hipLaunchKernelGGL(ce_rows_kernel, dim3((unsigned)n), dim3(256), 0, ctx.stream, logits,
                        targets_dev, n, v, row_loss, vec);
     check_hip(hipGetLastError(), "cross_entropy launch");
+    hipLaunchKernelGGL(mean_f64_kernel, dim3(1), dim3(256), 0, ctx.stream, row_loss, n,
+                       loss_dev);
+    check_hip(hipGetLastError(), "loss mean launch");
+}
+
+void launch_ce_combine(Context &ctx, const float *part, int64_t tiles, const float *zt,
+                       int64_t n, float *row_loss, float *loss_dev) {
+    if (n > 0x1ffffffff) fail(MMH_ERR_SHAPE, "cross_entropy: too many rows");
+    hipLaunchKernelGGL(ce_combine_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, ctx.stream,
+                       part, tiles, zt, n, row_loss);
+    check_hip(hipGetLastError(), "loss combine launch");
     hipLaunchKernelGGL(mean_f64_kernel, dim3(1), dim3(256), 0, ctx.stream, row_loss, n,
                        loss_dev);
     check_hip(hipGetLastError(), "loss mean launch");

@@ -27,21 +27,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
-__device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2) {
-    if (m2 == -INFINITY) return;
-    if (m == -INFINITY) {
-        m = m2;
-        s = s2;
-        return;
-    }
-    if (m2 > m) {
-        s = s * expf(m - m2) + s2;
-        m = m2;
-    } else {
-        s = s + s2 * expf(m2 - m);
-    }
-}
-
 // ---- cross entropy forward + backward ----------------------------------------
 // row_loss[row] = max + ln(sum) - z[t]; then z[j] <- exp(z[j] - max) / sum * scale,
 // minus scale at the target (ops_reduce.rs:263-272, scale = g / N).
