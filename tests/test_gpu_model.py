@@ -124,6 +124,37 @@ def test_small_width_forwards_against_oracle(ctx, cfg, batch, seq):
         m.close()
 
 
+@pytest.mark.parametrize("cfg,batch,seq", [
+    # enough rows x 128-column tiles (>= the CU count) for the 128x128 head
+    # kernel, which folds the loss in when only the loss is asked for; the
+    # vocabularies end in a partial column tile
+    ([3000, 64, 1, 4, 2, 96, 1024, 10000.0, 1e-5, 1], 2, 1024),
+    ([4133, 96, 1, 3, 3, 128, 512, 10000.0, 1e-5, 0], 4, 500),
+])
+def test_loss_folded_into_the_head_gemm(ctx, cfg, batch, seq):
+    print(f"\n[model] loss-only forward {cfg[:7]} B{batch} T{seq}", flush=True)
+    c = oracle_config(cfg)
+    w = O.init_weights(c, O.rng(23), std=0.2)
+    r = np.random.default_rng(seq + cfg[0])
+    x = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    y = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    m = mh.Model.from_weights(ctx, cfg, w)
+    try:
+        folded = float(m.loss(x, y, batch, seq))
+        with_logits, logits = m.forward_loss(x, y, batch, seq)
+        ref_loss = float(O.forward_loss(c, w, x, y, batch, seq, want_logits=False)[0])
+        L = logits.reshape(-1, cfg[0]).astype(np.float64)
+        mx = L.max(1, keepdims=True)
+        f64 = float(np.mean(np.log(np.exp(L - mx).sum(1)) + mx[:, 0] - L[np.arange(len(y)), y]))
+        print(f"  folded {folded:.7f} separate {with_logits:.7f} float64 CE of the logits "
+              f"{f64:.7f} oracle {ref_loss:.7f}", flush=True)
+        assert abs(folded - f64) <= 2e-6 * f64
+        assert abs(folded - with_logits) <= 2e-6 * with_logits
+        assert abs(folded - ref_loss) <= 1e-4 * ref_loss
+    finally:
+        m.close()
+
+
 def test_untied_head_against_oracle(ctx):
     cfg = [13, 16, 2, 4, 2, 24, 8, 10000.0, 1e-5, 0]
     c = oracle_config(cfg)
