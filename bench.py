@@ -404,6 +404,8 @@ def main():
                     help="skip timing training and evaluation fed from token shard files")
     ap.add_argument("--train-steps", type=int, default=5,
                     help="large-preset training steps to time after the forward (0: none)")
+    ap.add_argument("--no-bandwidth", action="store_true",
+                    help="skip the back-to-back timing of the op-level bandwidth kernels")
     ap.add_argument("--no-mfma-probe", action="store_true",
                     help="skip the fp32 MFMA issue-rate probe (the measured ceiling)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -478,9 +480,11 @@ def main():
         log(f"fp32 MFMA issue-rate probe (no memory traffic): {ceiling:.1f} TFLOP/s; "
             f"the GEMMs reach {achieved / ceiling:.1%} of it")
 
-    bandwidth = time_bandwidth(mh, ctx)
-    log("bandwidth kernels (back-to-back launches): " + ", ".join(
-        f"{k} {v['gbs']:.0f} GB/s ({v['frac_of_hbm']:.0%})" for k, v in bandwidth.items()))
+    bandwidth = None
+    if not a.no_bandwidth:
+        bandwidth = time_bandwidth(mh, ctx)
+        log("bandwidth kernels (back-to-back launches): " + ", ".join(
+            f"{k} {v['gbs']:.0f} GB/s ({v['frac_of_hbm']:.0%})" for k, v in bandwidth.items()))
 
     sweep = None
     if not a.no_sweep:
