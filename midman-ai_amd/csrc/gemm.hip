@@ -830,14 +830,19 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
 // x * w feeds the MFMAs, the sums of squares of x are gathered per lane and
 // combined over the lane halves and then the waves, and each row's 1/rms
 // scales the summed results.
-// MODE: 2 when K is a multiple of 32 and the A rows (and the norm weights)
+// MODE: 2 when the K range of every split is a multiple of 32 and the
+// k-contiguous operands (A rows when !TA, B rows when TB, the norm weights)
 // are 16-byte aligned: float4 reads, no predicates; 1 when only the rows are
-// aligned: a lane whose 16 k values all lie below K reads them as float4,
+// aligned: a lane whose 16 k values all lie in range reads them as float4,
 // the lanes of the partial last step one predicated value at a time; 0
 // otherwise: every read predicated. (Keeping the predicated path out of mode
 // 2 keeps its registers low; a separate tail step measured slower than the
-// per-lane test of mode 1.)
-template <int EPI, bool NORM, int NW, int MODE>
+// per-lane test of mode 1.) Operands stored k-major (A when TA, B when !TB)
+// are read one value per k, coalesced across the 32 lanes of a half.
+// Split K (grid z > 1): each split covers k_per_split values and writes its
+// partial tile; splitk_reduce sums the splits in order and applies the
+// epilogue.
+template <bool TA, bool TB, int EPI, bool NORM, int NW, int MODE>
 __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     __shared__ float part[NW][16][64];
     __shared__ float sm_ss[NW][32];
@@ -846,21 +851,25 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     const int lr = lane & 31, lk = lane >> 5;
     const int tm = (int)blockIdx.x / p.tiles_n, tn = (int)blockIdx.x - tm * p.tiles_n;
     const int64_t m0 = (int64_t)tm * 32, n0 = (int64_t)tn * 32;
-    const int64_t M = p.m, N = p.n, K = p.k;
-    const int nsteps = (int)((K + 31) / 32);
+    const int64_t M = p.m, N = p.n;
+    const int split = blockIdx.z;
+    const int64_t kbeg = (int64_t)split * p.k_per_split;
+    const int64_t kend = min(p.k, kbeg + p.k_per_split);
+    const int nsteps = (int)((kend - kbeg + 31) / 32);
     // rows and columns past the edge read the last one; their results are not stored
-    const float *arow = p.a + min(m0 + lr, M - 1) * p.lda;
-    const float *bcol = p.b + min(n0 + lr, N - 1);
+    const int64_t am = min(m0 + lr, M - 1), bn = min(n0 + lr, N - 1);
+    const float *arow = TA ? p.a + am : p.a + am * p.lda;    // then + k * (TA ? lda : 1)
+    const float *bcol = TB ? p.b + bn * p.ldb : p.b + bn;    // then + k * (TB ? 1 : ldb)
 
     floatx16 acc;
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
     float ss = 0.0f;
     for (int st = wave; st < nsteps; st += NW) {
-        const int64_t kb = (int64_t)st * 32 + 16 * lk;  // this lane's first k of the step
-        const bool whole = MODE == 2 || (MODE == 1 && kb + 16 <= K);
+        const int64_t kb = kbeg + (int64_t)st * 32 + 16 * lk;  // this lane's first k of the step
+        const bool whole = MODE == 2 || (MODE == 1 && kb + 16 <= kend);
         float a[16], b[16];
-        if (whole) {
+        if (!TA && whole) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float4 v = reinterpret_cast<const float4 *>(arow + kb)[i];
@@ -871,10 +880,23 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) a[j] = kb + j < K ? arow[kb + j] : 0.0f;
+            for (int j = 0; j < 16; ++j)
+                a[j] = (whole || kb + j < kend) ? arow[(kb + j) * (TA ? p.lda : 1)] : 0.0f;
         }
+        if (TB && whole) {
 #pragma unroll
-        for (int j = 0; j < 16; ++j) b[j] = (whole || kb + j < K) ? bcol[(kb + j) * p.ldb] : 0.0f;
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = reinterpret_cast<const float4 *>(bcol + kb)[i];
+                b[4 * i + 0] = v.x;
+                b[4 * i + 1] = v.y;
+                b[4 * i + 2] = v.z;
+                b[4 * i + 3] = v.w;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                b[j] = (whole || kb + j < kend) ? bcol[(kb + j) * (TB ? 1 : p.ldb)] : 0.0f;
+        }
         if (NORM) {
             float w[16];
             if (whole) {
@@ -888,7 +910,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
                 }
             } else {
 #pragma unroll
-                for (int j = 0; j < 16; ++j) w[j] = kb + j < K ? p.norm_w[kb + j] : 0.0f;
+                for (int j = 0; j < 16; ++j) w[j] = kb + j < kend ? p.norm_w[kb + j] : 0.0f;
             }
 #pragma unroll
             for (int j = 0; j < 16; ++j) {
@@ -913,7 +935,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
             float t = sm_ss[0][tid];
 #pragma unroll
             for (int w = 1; w < NW; ++w) t = __fadd_rn(t, sm_ss[w][tid]);
-            const float mean = __fmul_rn(t, __fdiv_rn(1.0f, (float)K));  // norm.rs:21-39
+            const float mean = __fmul_rn(t, __fdiv_rn(1.0f, (float)p.k));  // norm.rs:21-39
             sm_inv[tid] = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, p.norm_eps)));
         }
         __syncthreads();
@@ -928,39 +950,45 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
         for (int w = 1; w < NW; ++w) v = __fadd_rn(v, part[w][r][lane]);
         const int rl = 8 * (r >> 2) + 4 * lk + (r & 3);
         if (NORM) v = __fmul_rn(v, sm_inv[rl]);
-        block32_epilogue<EPI>(p, C, R, m0 + rl, col, lr, v);
+        if (p.splits > 1) {
+            if (m0 + rl < M && col < N) p.partial[((int64_t)split * M + m0 + rl) * N + col] = v;
+        } else {
+            block32_epilogue<EPI>(p, C, R, m0 + rl, col, lr, v);
+        }
     }
 }
 
-template <int EPI, bool NORM, int MODE>
+template <bool TA, bool TB, int EPI, bool NORM, int MODE>
 void launch_ksplit_mode(Context &ctx, const KParams &p, dim3 grid, int nw) {
     if (nw == 4)
-        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 4, MODE>), grid, dim3(256), 0, ctx.stream, p);
+        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<TA, TB, EPI, NORM, 4, MODE>), grid, dim3(256), 0,
+                           ctx.stream, p);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<EPI, NORM, 8, MODE>), grid, dim3(512), 0, ctx.stream, p);
+        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<TA, TB, EPI, NORM, 8, MODE>), grid, dim3(512), 0,
+                           ctx.stream, p);
 }
 
-template <int EPI, bool NORM>
-void launch_ksplit_nw(Context &ctx, const KParams &p, dim3 grid, bool vec, int nw) {
-    if (vec && p.k % 32 == 0)
-        launch_ksplit_mode<EPI, NORM, 2>(ctx, p, grid, nw);
-    else if (vec)
-        launch_ksplit_mode<EPI, NORM, 1>(ctx, p, grid, nw);
+template <bool TA, bool TB, int EPI, bool NORM>
+void launch_ksplit_nw(Context &ctx, const KParams &p, dim3 grid, int mode, int nw) {
+    if (mode == 2)
+        launch_ksplit_mode<TA, TB, EPI, NORM, 2>(ctx, p, grid, nw);
+    else if (mode == 1)
+        launch_ksplit_mode<TA, TB, EPI, NORM, 1>(ctx, p, grid, nw);
     else
-        launch_ksplit_mode<EPI, NORM, 0>(ctx, p, grid, nw);
+        launch_ksplit_mode<TA, TB, EPI, NORM, 0>(ctx, p, grid, nw);
 }
 
-// Four waves up to four K steps (one step each), eight beyond.
-template <int EPI>
-void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, bool vec) {
-    const int nw = (p.k + 31) / 32 <= 4 ? 4 : 8;
-    if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
+// Four waves up to four K steps of a split (one step each), eight beyond.
+template <bool TA, bool TB, int EPI>
+void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, int mode) {
+    const int nw = (p.k_per_split + 31) / 32 <= 4 ? 4 : 8;
+    if constexpr (!TA && !TB && (EPI == EPI_STORE || EPI == EPI_SWIGLU)) {
         if (p.norm_w) {
-            launch_ksplit_nw<EPI, true>(ctx, p, grid, vec, nw);
+            launch_ksplit_nw<false, false, EPI, true>(ctx, p, grid, mode, nw);
             return;
         }
     }
-    launch_ksplit_nw<EPI, false>(ctx, p, grid, vec, nw);
+    launch_ksplit_nw<TA, TB, EPI, false>(ctx, p, grid, mode, nw);
 }
 
 // ---- fp32 MFMA issue-rate probe ---------------------------------------------------
@@ -1058,15 +1086,28 @@ bool use_small(const Context &ctx, const GemmDesc &d) {
     return d.force_splits == 0 && big_tiles < cus_of(ctx) && d.k <= 1024;
 }
 
-// The K-split kernel for the small nn shapes of one matrix whose K is at most
-// 15 steps of 32, with the store, accumulate and SwiGLU epilogues, while the
-// 64x64 tiles number under two per CU (beyond that the small kernel's grid is
-// deep enough and its tiles share their operands through LDS).
-bool use_ksplit(const Context &ctx, const GemmDesc &d) {
+// When the K-split kernel runs: 1 for the small nn shapes of one matrix whose
+// K is at most 15 steps of 32 (one split; the store, accumulate and SwiGLU
+// epilogues, with the RMSNorm and RoPE folds) while the 64x64 tiles number
+// under two per CU (beyond that the small kernel's grid is deep enough and its
+// tiles share their operands through LDS); 2 for the other products of one
+// matrix whose 128x128 tiles would not give every CU one and of at most 2^28
+// multiply-adds (any form but tt, store or accumulate), split along K across
+// workgroups: on the BASELINE sweep it wins at 0.27 GFLOP (dA, dB at K = N =
+// 256: 27 -> 37 and 13 -> 23 TFLOP/s) and loses from 1 GFLOP up, where the
+// other kernels' operand reuse through LDS pays; 0 otherwise.
+int ksplit_kind(const Context &ctx, const GemmDesc &d) {
+    const int cus = cus_of(ctx);
+    const bool plain = d.epi == EPI_STORE || d.epi == EPI_ACCUM;
     const int64_t small_tiles = ((d.m + SBM - 1) / SBM) * ((d.n + SBN - 1) / SBN);
-    return use_small(ctx, d) && !d.ta && !d.tb && d.batch == 1 && d.k <= 480 &&
-           small_tiles < 2 * cus_of(ctx) &&
-           (d.epi == EPI_STORE || d.epi == EPI_ACCUM || d.epi == EPI_SWIGLU);
+    if (use_small(ctx, d) && !d.ta && !d.tb && d.batch == 1 && d.k <= 480 &&
+        small_tiles < 2 * cus && (plain || d.epi == EPI_SWIGLU))
+        return 1;
+    const int64_t big_tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN);
+    if (d.batch == 1 && d.force_splits == 0 && !(d.ta && d.tb) && plain && !d.norm_w &&
+        !d.rope_cos && big_tiles < cus && d.m * d.n * d.k <= (int64_t(1) << 28))
+        return 2;
+    return 0;
 }
 
 bool vec_a_of(const GemmDesc &d, const float *a, int64_t lda) {
@@ -1127,7 +1168,8 @@ void gemm(Context &ctx, const GemmDesc &d) {
     }
     const int cus = cus_of(ctx);
     const bool small = use_small(ctx, d);
-    const bool ksplit = use_ksplit(ctx, d);
+    const int kind = ksplit_kind(ctx, d);
+    const bool ksplit = kind != 0;
     const GemmFusion fuse = gemm_fusion(ctx, d);
     p.tiles_m = (int)(ksplit ? (d.m + 31) / 32 : small ? (d.m + SBM - 1) / SBM : (d.m + BM - 1) / BM);
     p.tiles_n = (int)(ksplit ? (d.n + 31) / 32 : small ? (d.n + SBN - 1) / SBN : (d.n + BN - 1) / BN);
@@ -1156,11 +1198,17 @@ void gemm(Context &ctx, const GemmDesc &d) {
     }
 
     const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
-    const int64_t ktiles = (d.k + (small ? SBK : BK) - 1) / (small ? SBK : BK);
+    const int64_t kstep = ksplit ? 32 : small ? SBK : BK;
+    const int64_t ktiles = (d.k + kstep - 1) / kstep;
     int splits = 1;
     if (d.force_splits > 0) {
         splits = d.force_splits;
-    } else if (d.batch == 1 && d.epi != EPI_SWIGLU && d.epi != EPI_SWIGLU_BWD) {
+    } else if (kind == 2) {
+        // Up to two workgroups per CU, each split keeping >= 4 steps of 32
+        // (a step per wave at least).
+        while (tiles * splits < 2 * (int64_t)cus && splits < 64 && ktiles / (splits * 2) >= 4)
+            splits *= 2;
+    } else if (!ksplit && d.batch == 1 && d.epi != EPI_SWIGLU && d.epi != EPI_SWIGLU_BWD) {
         if (small) {
             // Split only while a split keeps >= 8 steps of 32 (the reduce
             // launch costs about what 8 steps do) and the grid is below a
@@ -1175,9 +1223,8 @@ void gemm(Context &ctx, const GemmDesc &d) {
         }
     }
     if (d.batch > 1 || d.epi == EPI_SWIGLU || d.epi == EPI_SWIGLU_BWD || d.epi == EPI_CE ||
-        p.norm_w || ksplit)
+        p.norm_w || kind == 1)
         splits = 1;
-    const int64_t kstep = small ? SBK : BK;
     const int64_t kt_per = (ktiles + splits - 1) / splits;
     p.k_per_split = kt_per * kstep;
     splits = (int)((ktiles + kt_per - 1) / kt_per);
@@ -1203,14 +1250,23 @@ void gemm(Context &ctx, const GemmDesc &d) {
     dim3 grid((unsigned)tiles, (unsigned)d.batch, (unsigned)splits);
     const int epi = splits > 1 ? EPI_STORE : d.epi;
     if (ksplit) {
-        // vec_a holds lda % 4 == 0 and a 16-byte aligned A
-        const bool vec = p.vec_a && (!p.norm_w || aligned16(p.norm_w));
+        // The k-contiguous operands (A when !ta, B when tb, the norm weights)
+        // decide between vector and predicated reads (vec_a / vec_b hold
+        // ld % 4 == 0 and a 16-byte aligned base).
+        const bool vec = (d.ta || p.vec_a) && (!d.tb || p.vec_b) &&
+                         (!p.norm_w || aligned16(p.norm_w));
+        const int mode = !vec ? 0 : d.k % 32 == 0 ? 2 : 1;
         if (epi == EPI_SWIGLU)
-            launch_ksplit<EPI_SWIGLU>(ctx, p, grid, vec);
-        else if (epi == EPI_ACCUM)
-            launch_ksplit<EPI_ACCUM>(ctx, p, grid, vec);
+            launch_ksplit<false, false, EPI_SWIGLU>(ctx, p, grid, mode);
+        else if (!d.ta && !d.tb)
+            (epi == EPI_ACCUM ? launch_ksplit<false, false, EPI_ACCUM>
+                              : launch_ksplit<false, false, EPI_STORE>)(ctx, p, grid, mode);
+        else if (!d.ta)
+            (epi == EPI_ACCUM ? launch_ksplit<false, true, EPI_ACCUM>
+                              : launch_ksplit<false, true, EPI_STORE>)(ctx, p, grid, mode);
         else
-            launch_ksplit<EPI_STORE>(ctx, p, grid, vec);
+            (epi == EPI_ACCUM ? launch_ksplit<true, false, EPI_ACCUM>
+                              : launch_ksplit<true, false, EPI_STORE>)(ctx, p, grid, mode);
     } else if (epi == EPI_CE) {
         if (d.tb)
             hipLaunchKernelGGL((gemm_f32_mfma<false, true, EPI_CE>), grid, dim3(256), 0,
