@@ -19,11 +19,11 @@
 //
 // K advances 16 at a time through two LDS stages, software-pipelined: at the
 // top of iteration t, tile t+1 moves from registers into the free stage and
-// tile t+2's global loads are issued; then the 32 MFMAs per wave of tile t run
-// while those loads are in flight. One barrier per tile. Interior tiles take a
-// path with no
-// load predicates and 32-bit offsets from uniform base pointers; edge tiles
-// zero-fill outside [M, N, K).
+// tile t+4's global loads are issued into the register slot it freed (a ring
+// of three slots); then the 32 MFMAs per wave of tile t run while the loads
+// of three tiles are in flight. One barrier per tile. Interior tiles take a
+// path with no load predicates and 32-bit offsets from uniform base
+// pointers; edge tiles zero-fill outside [M, N, K) and keep one slot.
 //
 // Workgroup -> tile mapping is XCD-aware: the dispatcher hands workgroup w to
 // XCD w % 8, so w is renumbered to make each XCD's share a contiguous run of
@@ -35,6 +35,8 @@
 // so the result is deterministic.
 #include "mmh_internal.h"
 
+#include <utility>
+
 namespace mmh {
 namespace {
 
@@ -42,6 +44,11 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int GROUP_M = 8;
+// Register slots of the 128x128 kernel's load ring on interior tiles: tile
+// t+KSLOTS's global loads are issued while tile t's MFMAs run. Edge tiles
+// (predicated loads, few per grid) keep one slot, which holds the kernel's
+// registers to what the interior path needs.
+constexpr int KSLOTS = 3;
 // Raw buffer descriptor: byte range (interior tiles stay below 2^31 bytes from
 // their base, checked on the host) and the gfx9-family dword-3 flags.
 constexpr int kBufferRange = 0x7fffffff;
@@ -85,6 +92,13 @@ struct LdsB {
     static constexpr int S = BN + (TB ? 2 : 4);
 };
 
+// Calls f(integral_constant<int, i>) for i = 0..n-1, so that i is a
+// compile-time constant in each call (register-slot indices stay static).
+template <class F, int... Is>
+__device__ __forceinline__ void unroll_seq(F &&f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+
 // Reductions over each 32-lane half of a wave with DPP moves (quad permutes,
 // then rotations within a 16-lane row) and one swizzle across the two rows of
 // the half. For the max every lane ends with the result; for the sum the
@@ -118,7 +132,7 @@ __device__ __forceinline__ float half_sum32(float v) {
 }
 
 // The K loop of one 128x128 tile; see the file comment.
-template <bool TA, bool TB, bool FAST>
+template <bool TA, bool TB, bool FAST, int SLOTS>
 __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__restrict__ A,
                                               const float *__restrict__ B, int64_t m0, int64_t n0,
                                               int64_t kbeg, int64_t kend,
@@ -149,7 +163,8 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                          : (uint32_t)(idx >> 5) * ldb + (idx & 31) * 4);
     }
 
-    float4 ra[NL], rb[NL];
+    constexpr int NS = FAST ? SLOTS : 1;
+    float4 ra[NS][NL], rb[NS][NL];
 
     auto load_a_edge = [&](int idx, int64_t k0) __attribute__((always_inline)) -> float4 {
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -197,7 +212,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
         }
         return w;
     };
-    auto load = [&](int64_t k0) __attribute__((always_inline)) {
+    auto load = [&](int sl, int64_t k0) __attribute__((always_inline)) {
         if (FAST) {
             // Buffer loads: the tile's base in a scalar descriptor, the
             // per-thread byte offset in one loop-invariant VGPR.
@@ -209,46 +224,46 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                 const_cast<float *>(bk), (short)0, kBufferRange, kBufferFlags);
 #pragma unroll
             for (int i = 0; i < NL; ++i)
-                ra[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsa, ao[i], 0, 0));
+                ra[sl][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsa, ao[i], 0, 0));
 #pragma unroll
             for (int i = 0; i < NL; ++i)
-                rb[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsb, bo[i], 0, 0));
+                rb[sl][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsb, bo[i], 0, 0));
         } else {
 #pragma unroll
-            for (int i = 0; i < NL; ++i) ra[i] = load_a_edge(tid + 256 * i, k0);
+            for (int i = 0; i < NL; ++i) ra[sl][i] = load_a_edge(tid + 256 * i, k0);
 #pragma unroll
-            for (int i = 0; i < NL; ++i) rb[i] = load_b_edge(tid + 256 * i, k0);
+            for (int i = 0; i < NL; ++i) rb[sl][i] = load_b_edge(tid + 256 * i, k0);
         }
     };
-    auto store = [&](int buf) __attribute__((always_inline)) {
+    auto store = [&](int sl, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
             const int idx = tid + 256 * i;
             if (!TA) {
                 const int row = idx / RQ, kq = (idx % RQ) * 4;
-                As[buf][kq + 0][row] = ra[i].x;
-                As[buf][kq + 1][row] = ra[i].y;
-                As[buf][kq + 2][row] = ra[i].z;
-                As[buf][kq + 3][row] = ra[i].w;
+                As[buf][kq + 0][row] = ra[sl][i].x;
+                As[buf][kq + 1][row] = ra[sl][i].y;
+                As[buf][kq + 2][row] = ra[sl][i].z;
+                As[buf][kq + 3][row] = ra[sl][i].w;
             } else {
                 float *dst = &As[buf][idx >> 5][(idx & 31) * 4];
-                dst[0] = ra[i].x;
-                dst[1] = ra[i].y;
-                dst[2] = ra[i].z;
-                dst[3] = ra[i].w;
+                dst[0] = ra[sl][i].x;
+                dst[1] = ra[sl][i].y;
+                dst[2] = ra[sl][i].z;
+                dst[3] = ra[sl][i].w;
             }
             if (!TB) {
                 float *dst = &Bs[buf][idx >> 5][(idx & 31) * 4];
-                dst[0] = rb[i].x;
-                dst[1] = rb[i].y;
-                dst[2] = rb[i].z;
-                dst[3] = rb[i].w;
+                dst[0] = rb[sl][i].x;
+                dst[1] = rb[sl][i].y;
+                dst[2] = rb[sl][i].z;
+                dst[3] = rb[sl][i].w;
             } else {
                 const int col = idx / RQ, kq = (idx % RQ) * 4;
-                Bs[buf][kq + 0][col] = rb[i].x;
-                Bs[buf][kq + 1][col] = rb[i].y;
-                Bs[buf][kq + 2][col] = rb[i].z;
-                Bs[buf][kq + 3][col] = rb[i].w;
+                Bs[buf][kq + 0][col] = rb[sl][i].x;
+                Bs[buf][kq + 1][col] = rb[sl][i].y;
+                Bs[buf][kq + 2][col] = rb[sl][i].z;
+                Bs[buf][kq + 3][col] = rb[sl][i].w;
             }
         }
     };
@@ -278,29 +293,49 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
         }
     };
 
-    // Pipeline: stage t%2 holds tile t and the registers hold tile t+1 when
-    // iteration t starts. Tile t+1 first goes into the other stage (last read
-    // in iteration t-1, before its barrier), the global loads of tile t+2 are
-    // issued into the freed registers, and then the MFMAs of tile t run: the
-    // loads have a whole tile of MFMAs to land. One barrier per iteration.
+    // Pipeline: when iteration t starts, LDS stage t%2 holds tile t and
+    // register slot (t+j)%NS holds tile t+j for j = 1..NS (loads in flight;
+    // NS = SLOTS on interior tiles, 1 on edge tiles). Tile t+1 goes into the other stage
+    // (last read in iteration t-1, before its barrier), tile t+1+NS's global
+    // loads are issued into the slot that freed, and then the MFMAs of tile t
+    // run: a load has NS tiles of MFMAs to land, which covers HBM latency
+    // when the operands are in no cache (a layer's weights). One barrier per
+    // iteration. The loop is unrolled by the period of (stage, slot) so every
+    // slot index is a constant, and every step issues its loads
+    // unconditionally (tiles past the end reload the last one, which nothing
+    // reads): with the same loads on every path the compiler waits for
+    // exactly the oldest slot instead of draining all of them.
     const int nk = (int)((kend - kbeg + BK - 1) / BK);
-    if (nk > 0) {
-        load(kbeg);
-        store(0);
-    }
-    if (nk > 1) load(kbeg + BK);
-    __syncthreads();
-    for (int it = 0; it < nk; ++it) {
-        const int cur = it & 1;
-        if (it + 1 < nk) store(cur ^ 1);
-        if (it + 2 < nk) load(kbeg + (int64_t)(it + 2) * BK);
-        compute(cur);
+    if (nk <= 0) return;
+    constexpr int U = NS % 2 == 0 ? NS : 2 * NS;
+    auto tile_k = [&](int t) __attribute__((always_inline)) {
+        return kbeg + (int64_t)min(t, nk - 1) * BK;
+    };
+    auto step = [&](auto uc, int it) __attribute__((always_inline)) {
+        constexpr int u = decltype(uc)::value;
+        store((u + 1) % NS, (u + 1) % 2);
+        load((u + 1) % NS, tile_k(it + 1 + NS));
+        compute(u % 2);
         __syncthreads();
-    }
+    };
+    load(0, kbeg);
+    store(0, 0);
+    unroll_seq([&](auto jc) __attribute__((always_inline)) {
+        constexpr int j = decltype(jc)::value + 1;
+        load(j % NS, tile_k(j));
+    }, std::make_integer_sequence<int, NS>{});
+    __syncthreads();
+    int base = 0;
+    for (; base + U <= nk; base += U)
+        unroll_seq([&](auto uc) __attribute__((always_inline)) { step(uc, base + uc); },
+                   std::make_integer_sequence<int, U>{});
+    unroll_seq([&](auto uc) __attribute__((always_inline)) {
+        if (base + uc < nk) step(uc, base + uc);
+    }, std::make_integer_sequence<int, U>{});
 }
 
 template <bool TA, bool TB, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
+__global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
     __shared__ __attribute__((aligned(16))) float As[2][BK][LdsA<TA>::S];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK][LdsB<TB>::S];
 
@@ -340,10 +375,12 @@ __global__ __launch_bounds__(256, 2) void gemm_f32_mfma(KParams p) {
 
     const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
                       (kend - kbeg) % BK == 0;
+    // the loss epilogue's registers leave room for two slots at 3 workgroups per CU
+    constexpr int slots = EPI == EPI_CE ? 2 : KSLOTS;
     if (fast)
-        gemm_mainloop<TA, TB, true>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+        gemm_mainloop<TA, TB, true, slots>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
     else
-        gemm_mainloop<TA, TB, false>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+        gemm_mainloop<TA, TB, false, 1>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
 
     // ---- epilogue: block (i, j) register r of lane l is C[row][col] with
     // row = base_row + 2*(8*(r/4) + 4*(l/32) + r%4) + i, col = base_col + 2*(l%32) + j.
