@@ -7,7 +7,7 @@ reference init, uniform token ids, all in f32, with the weights and the token
 ids resident in HBM when the timed region starts. One step = one forward +
 loss over the batch (mmh_model_run_staged). Also reported: the large-preset
 training step (forward + loss + backward + clip + AdamW), the tiny preset
-(B8 T256), the BASELINE GEMM sweep (M=2048, K,N in {256,1024,4096}, forward
+(B8 T256), the benchmark GEMM sweep (M=2048, K,N in {256,1024,4096}, forward
 C=A.B and backward dA=dC.B^T, dB=A^T.dC), a per-kernel-class breakdown from
 HIP events, the roofline of the dominant kernel (the fp32 MFMA GEMM) and the
 CPU baseline (the oracle, a C restatement of the reference CPU path, on one
@@ -225,7 +225,7 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
 
 
 def time_block(mh, ctx, hkv, reps=20):
-    """DecoderBlock::forward alone at the BASELINE block config: d 1024, 16
+    """DecoderBlock::forward alone at the benchmark block config: d 1024, 16
     heads x 64, SwiGLU 2816, B8 T1024, x ~ N(0,1), W ~ N(0,0.02) seeded.
     HIP events around `reps` calls after 3 warmups (weights packed per call,
     as the op-level entry point does)."""
@@ -399,7 +399,7 @@ def main():
     ap.add_argument("--no-checkpoint", action="store_true",
                     help="skip timing the large model's safetensors save/load")
     ap.add_argument("--no-block", action="store_true",
-                    help="skip timing the BASELINE single-block config")
+                    help="skip timing the benchmark single-block config")
     ap.add_argument("--no-shards", action="store_true",
                     help="skip timing training and evaluation fed from token shard files")
     ap.add_argument("--train-steps", type=int, default=5,

@@ -11,7 +11,9 @@
 // The wave's two row blocks take the even and the odd rows of its 64 (and the
 // two column blocks the even and odd columns), so one 8-byte LDS read gives a
 // lane its operand for both blocks, at an immediate offset from one base
-// address, and the epilogue writes column pairs.
+// address, and the epilogue writes column pairs. For the QKV product with
+// RoPE in the epilogue the column blocks instead hold columns c and c + hd/2
+// of a head (hd 64 or 128), so each rotation pair sits in one lane.
 //
 // MFMA 32x32x2 f32 operand layout (wave64): lane l supplies A[i=l%32][k=l/32]
 // and B[k=l/32][j=l%32]; accumulator register r of lane l holds
@@ -132,7 +134,12 @@ __device__ __forceinline__ float half_sum32(float v) {
 }
 
 // The K loop of one 128x128 tile; see the file comment.
-template <bool TA, bool TB, bool FAST, int SLOTS>
+// CL: the columns of a wave's two MFMA column blocks: 0 the even and odd
+// columns of its 64 (one 8-byte operand read), 1 its two halves of 32, 2
+// columns c and c + 64 of the tile (wave wn takes c = 32*wn .. +31), so the
+// RoPE pair (c, c + hd/2) of a head of 64 (CL 1) or 128 (CL 2) columns sits
+// in one lane.
+template <bool TA, bool TB, bool FAST, int SLOTS, int CL>
 __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__restrict__ A,
                                               const float *__restrict__ B, int64_t m0, int64_t n0,
                                               int64_t kbeg, int64_t kend,
@@ -275,14 +282,19 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     // One tile's MFMAs from LDS stage `buf`: all operand reads are issued
     // first (for each k-pair kk the float2 holds the operand of row or column
     // block 0 and of block 1); the MFMAs consume them in order as they land.
+    constexpr int cstep = CL == 0 ? 1 : CL == 1 ? 32 : 64;  // block 1's column offset
+    const int cbase = CL == 0 ? wn * 64 + 2 * lr : CL == 1 ? wn * 64 + lr : wn * 32 + lr;
     auto compute = [&](int buf) __attribute__((always_inline)) {
         const float *pa = &As[buf][lk][wm * 64 + 2 * lr];
-        const float *pb = &Bs[buf][lk][wn * 64 + 2 * lr];
+        const float *pb = &Bs[buf][lk][cbase];
         float2 a[BK / 2], b[BK / 2];
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) {
             a[kk] = *reinterpret_cast<const float2 *>(pa + 2 * kk * LdsA<TA>::S);
-            b[kk] = *reinterpret_cast<const float2 *>(pb + 2 * kk * LdsB<TB>::S);
+            if constexpr (CL == 0)
+                b[kk] = *reinterpret_cast<const float2 *>(pb + 2 * kk * LdsB<TB>::S);
+            else
+                b[kk] = make_float2(pb[2 * kk * LdsB<TB>::S], pb[2 * kk * LdsB<TB>::S + cstep]);
         }
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) {
@@ -334,8 +346,9 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     }, std::make_integer_sequence<int, U>{});
 }
 
-template <bool TA, bool TB, int EPI>
+template <bool TA, bool TB, int EPI, int CL = 0>
 __global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
+    static_assert(CL == 0 || EPI == EPI_STORE, "the RoPE column layouts store plain values");
     __shared__ __attribute__((aligned(16))) float As[2][BK][LdsA<TA>::S];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK][LdsB<TB>::S];
 
@@ -372,22 +385,53 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
     const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
                       (kend - kbeg) % BK == 0;
     // the loss epilogue's registers leave room for two slots at 3 workgroups per CU
     constexpr int slots = EPI == EPI_CE ? 2 : KSLOTS;
     if (fast)
-        gemm_mainloop<TA, TB, true, slots>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+        gemm_mainloop<TA, TB, true, slots, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
     else
-        gemm_mainloop<TA, TB, false, 1>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+        gemm_mainloop<TA, TB, false, 1, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
 
     // ---- epilogue: block (i, j) register r of lane l is C[row][col] with
-    // row = base_row + 2*(8*(r/4) + 4*(l/32) + r%4) + i, col = base_col + 2*(l%32) + j.
+    // row = base_row + 2*(8*(r/4) + 4*(l/32) + r%4) + i, col = base_col + 2*(l%32) + j
+    // (CL 0; the other layouts below).
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, lk = lane >> 5;
     const int64_t col = n0 + wn * 64 + 2 * lr;
+    if constexpr (CL != 0) {
+        // Column block j of lane lr is column c0 + j*half of C (half = 32 for
+        // CL 1, 64 for CL 2), c0 the lane's column in the first half of its
+        // head: RoPE (rope.rs:28-32) rotates the pair in registers, with the
+        // rope kernel's arithmetic, on the q and k heads (columns below
+        // rope_cols); the v heads are stored as they are.
+        constexpr int half = CL == 1 ? 32 : 64;
+        const int hc = CL == 1 ? lr : wn * 32 + lr;
+        const int64_t c0 = CL == 1 ? n0 + wn * 64 + lr : n0 + wn * 32 + lr;
+        const bool rot = p.rope_cos != nullptr && c0 < p.rope_cols;
+        float *C = p.c + batch * p.stride_c;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
+                if (row >= M) continue;
+                float x1 = acc[i][0][r], x2 = acc[i][1][r];
+                if (rot) {
+                    const int64_t t = (row % p.rope_seq) * half + hc;
+                    const float cs = p.rope_cos[t], sn = p.rope_sin[t];
+                    const float y1 = x1 * cs - x2 * sn;
+                    const float y2 = x2 * cs + x1 * sn;
+                    x1 = y1;
+                    x2 = y2;
+                }
+                if (c0 < N) C[row * p.ldc + c0] = x1;
+                if (c0 + half < N) C[row * p.ldc + c0 + half] = x2;
+            }
+        return;
+    }
     if (p.splits > 1) {
         float *P = p.partial + (int64_t)split * M * N;
 #pragma unroll
@@ -1093,6 +1137,18 @@ void launch(Context &ctx, const KParams &p, dim3 grid, bool small) {
             return;
         }
     }
+    if constexpr (!TA && !TB && EPI == EPI_STORE) {
+        // RoPE in the 128x128 kernel's epilogue (heads of 64 or 128 columns)
+        if (!small && p.rope_cos) {
+            if (p.rope_hd == 64)
+                hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI, 1>), grid, dim3(256), 0,
+                                   ctx.stream, p);
+            else
+                hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI, 2>), grid, dim3(256), 0,
+                                   ctx.stream, p);
+            return;
+        }
+    }
     if (small)
         hipLaunchKernelGGL((gemm_f32_mfma_small<TA, TB, EPI, false>), grid, dim3(256), 0,
                            ctx.stream, p);
@@ -1130,7 +1186,7 @@ bool use_small(const Context &ctx, const GemmDesc &d) {
 // tiles share their operands through LDS); 2 for the other products of one
 // matrix whose 128x128 tiles would not give every CU one and of at most 2^28
 // multiply-adds (any form but tt, store or accumulate), split along K across
-// workgroups: on the BASELINE sweep it wins at 0.27 GFLOP (dA, dB at K = N =
+// workgroups: on the benchmark sweep it wins at 0.27 GFLOP (dA, dB at K = N =
 // 256: 27 -> 37 and 13 -> 23 TFLOP/s) and loses from 1 GFLOP up, where the
 // other kernels' operand reuse through LDS pays; 0 otherwise.
 int ksplit_kind(const Context &ctx, const GemmDesc &d) {
@@ -1158,11 +1214,21 @@ bool vec_a_of(const GemmDesc &d, const float *a, int64_t lda) {
 GemmFusion gemm_fusion(const Context &ctx, const GemmDesc &d) {
     GemmFusion f;
     const bool small = use_small(ctx, d);
-    f.norm = small && !d.ta && !d.tb && d.batch == 1 && d.k <= 256 && d.k % 4 == 0 &&
-             vec_a_of(d, d.a, d.lda) && aligned16(d.norm_w) &&
-             (d.epi == EPI_STORE || d.epi == EPI_SWIGLU);
-    f.rope = small && d.batch == 1 && d.epi == EPI_STORE && d.rope_hd > 0 &&
-             d.rope_hd <= 32 && 32 % d.rope_hd == 0;
+    const bool nn = !d.ta && !d.tb && d.batch == 1 && d.k % 4 == 0 &&
+                    vec_a_of(d, d.a, d.lda) && aligned16(d.norm_w) &&
+                    (d.epi == EPI_STORE || d.epi == EPI_SWIGLU);
+    if (small) {
+        f.norm = nn && d.k <= 256;
+        f.rope = d.batch == 1 && d.epi == EPI_STORE && d.rope_hd > 0 && d.rope_hd <= 32 &&
+                 32 % d.rope_hd == 0;
+    } else {
+        // the 128x128 kernel rotates heads of 64 or 128 columns in registers;
+        // the norm stays a kernel of its own (in this kernel's loads it costs
+        // the registers of a ring slot, and the GEMM loses more than the norm
+        // kernel takes)
+        f.rope = !d.ta && !d.tb && d.batch == 1 && d.epi == EPI_STORE &&
+                 (d.rope_hd == 64 || d.rope_hd == 128);
+    }
     return f;
 }
 

@@ -101,9 +101,10 @@ Config parse_config(const double *v) {
 // One pre-norm block (block.rs:77-81) on packed weights: x += attn(rms(x)),
 // then x += mlp(rms(x)), the residual adds fused into the O and down GEMMs,
 // SwiGLU into the gate/up GEMM, and the two norms and the q, k rotation
-// handed to the QKV and gate/up GEMMs (which fold them in for small widths
-// and run them as kernels of their own otherwise). timed(class, launch)
-// wraps each launch.
+// handed to the QKV and gate/up GEMMs, which fold them in where they can
+// (the norms at small widths; the rotation for heads of up to 32 columns on
+// the small tiles and of 64 or 128 on the 128x128 tiles) and run them as
+// kernels of their own otherwise. timed(class, launch) wraps each launch.
 struct BlockRun {
     const float *attn_norm = nullptr, *wqkv = nullptr, *wo = nullptr;
     const float *mlp_norm = nullptr, *wgu = nullptr, *wd = nullptr;

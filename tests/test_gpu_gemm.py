@@ -1,5 +1,5 @@
 """GPU parity of the fp32 MFMA GEMM seam (kernels.rs:49-108) and the matmul
-backward (ops_matmul.rs:62-74) against the oracle, on the BASELINE sweep:
+backward (ops_matmul.rs:62-74) against the oracle, on the benchmark sweep:
 M = 2048, K, N in {256, 1024, 4096}, A ~ N(0,1) from Rng(1), B ~ N(0,0.02)
 from Rng(2), dC ~ N(0,1) from Rng(3).
 

@@ -2,7 +2,7 @@
 mmh_model_*: seeded weights and tokens bit-exact, the reference's native
 golden losses, and logits/loss against the oracle on identical inputs.
 
-Tolerances: loss <= 1e-4 relative; logits: per row,
+Tolerances (the stated target): loss <= 1e-4 relative; logits: per row,
 max|gpu - oracle| <= 1e-3 * max|oracle row|.
 """
 import math
@@ -170,7 +170,7 @@ def test_untied_head_against_oracle(ctx):
 
 
 def test_large_preset_full_size_invariants(ctx):
-    # Full large preset at the BASELINE shape B4 T1024: size-independent checks.
+    # Full large preset at the benchmark shape B4 T1024: size-independent checks.
     print("\n[model] large preset B4 T1024 (init ~ a few seconds)", flush=True)
     m = mh.Model.new(ctx, mh.PRESETS["large"], 0)
     assert m.num_parameters() == 1_009_338_368

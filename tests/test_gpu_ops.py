@@ -159,8 +159,13 @@ def test_attention_forward(ctx, B, T, d, H, Hkv):
 
 @pytest.mark.parametrize("B,T,d,H,Hkv,ff", [
     (2, 12, 16, 2, 1, 24), (2, 64, 256, 4, 2, 176), (1, 100, 128, 1, 1, 344),
-    # the BASELINE block config, both kv-head counts
-    (8, 1024, 1024, 16, 16, 2816), (8, 1024, 1024, 16, 8, 2816)])
+    # the benchmark's block config (d 1024, 16 heads of 64, SwiGLU 2816, B8
+    # T1024), both kv-head counts; heads of 64 columns rotated in the 128x128
+    # GEMM's epilogue
+    (8, 1024, 1024, 16, 16, 2816), (8, 1024, 1024, 16, 8, 2816),
+    # heads of 128 (the large preset's), QKV at 512 tiles of 128x128: rotated
+    # in the epilogue, with no K split
+    (2, 1024, 2048, 16, 8, 512)])
 def test_block_forward(ctx, B, T, d, H, Hkv, ff):
     """DecoderBlock::forward (block.rs:77-81) against the oracle's block."""
     print(f"\n[block_forward] B={B} T={T} d={d} H={H} Hkv={Hkv} ff={ff}", flush=True)
