@@ -79,6 +79,21 @@ def model_bytes(cfg, B, T):
     }
 
 
+def warm_up(ctx, fn, ms=50.0):
+    """Runs fn until at least `ms` of device time has passed (and 3 times at
+    least): the chip's clock climbs for some tens of milliseconds after an
+    idle spell (the host-side setup of each case), so a few launches of a
+    short kernel would time a partly ramped clock."""
+    t0 = time.perf_counter()
+    n = 0
+    while n < 3 or (time.perf_counter() - t0) * 1000 < ms:
+        fn()
+        n += 1
+        if n % 8 == 0:
+            ctx.synchronize()
+    ctx.synchronize()
+
+
 def time_train(mh, m, B, T, steps, warmup):
     """Training steps on the model's own weights (Lab::step_once /
     Trainer::update on the device): forward + loss + backward + f64 global
@@ -227,7 +242,7 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
 def time_block(mh, ctx, hkv, reps=20):
     """DecoderBlock::forward alone at the benchmark block config: d 1024, 16
     heads x 64, SwiGLU 2816, B8 T1024, x ~ N(0,1), W ~ N(0,0.02) seeded.
-    HIP events around `reps` calls after 3 warmups (weights packed per call,
+    HIP events around `reps` calls after 50 ms of warmup (weights packed per call,
     as the op-level entry point does)."""
     import numpy as np
 
@@ -243,9 +258,7 @@ def time_block(mh, ctx, hkv, reps=20):
     dw = ctx.to_device(w)
     out = ctx.empty((B, T, d))
     tabs = mh.RotaryTables(ctx, hd, T, 10000.0)
-    for _ in range(3):
-        mh.block_forward(ctx, x, dw, H, hkv, ff, 1e-5, tabs, out=out)
-    ctx.synchronize()
+    warm_up(ctx, lambda: mh.block_forward(ctx, x, dw, H, hkv, ff, 1e-5, tabs, out=out))
     ctx.timer_start()
     for _ in range(reps):
         mh.block_forward(ctx, x, dw, H, hkv, ff, 1e-5, tabs, out=out)
@@ -275,9 +288,7 @@ def gemm_sweep(mh, ctx, reps=10):
             for form, fn in (("fwd_nn", lambda: mh.gemm(ctx, "nn", A, B, C, M, k, n)),
                              ("dA_nt", lambda: mh.matmul_backward(ctx, A, B, DC, M, k, n, da=DA)),
                              ("dB_tn", lambda: mh.matmul_backward(ctx, A, B, DC, M, k, n, db=DB))):
-                for _ in range(3):
-                    fn()
-                ctx.synchronize()
+                warm_up(ctx, fn)
                 ctx.timer_start()
                 for _ in range(reps):
                     fn()
@@ -298,9 +309,7 @@ def time_bandwidth(mh, ctx, reps=20):
     rng = np.random.default_rng(0)
 
     def timed(fn):
-        for _ in range(3):
-            fn()
-        ctx.synchronize()
+        warm_up(ctx, fn)
         ctx.timer_start()
         for _ in range(reps):
             fn()

@@ -6,12 +6,14 @@
 // kernels.rs:68-73): each operand is read in its stored layout and written into
 // LDS k-major, the layout the MFMA operand reads want.
 //
-// Tiling: a 256-thread workgroup (4 wave64s, 2x2) owns a 128x128 tile of C;
-// each wave owns 64x64 as 2x2 MFMA 32x32 blocks (64 accumulators per lane).
-// The wave's two row blocks take the even and the odd rows of its 64 (and the
-// two column blocks the even and odd columns), so one 8-byte LDS read gives a
-// lane its operand for both blocks, at an immediate offset from one base
-// address, and the epilogue writes column pairs. For the QKV product with
+// Tiling: a 512-thread workgroup (8 wave64s, 4 along M x 2 along N) owns a
+// 128x128 tile of C; each wave owns 32 rows x 64 columns as two MFMA 32x32
+// blocks (32 accumulators per lane), whose columns are the even and the odd
+// columns of its 64: one 4-byte A read and one 8-byte B read from LDS give a
+// lane its operands for both blocks, and the epilogue writes column pairs.
+// Eight small waves rather than four of 64x64 keep four waves on every SIMD
+// when a grid has only two tiles per CU (the O and down projections of the
+// large preset: 512 tiles), at under 110 registers. For the QKV product with
 // RoPE in the epilogue the column blocks instead hold columns c and c + hd/2
 // of a head (hd 64 or 128), so each rotation pair sits in one lane.
 //
@@ -22,7 +24,7 @@
 // K advances 16 at a time through two LDS stages, software-pipelined: at the
 // top of iteration t, tile t+1 moves from registers into the free stage and
 // tile t+4's global loads are issued into the register slot it freed (a ring
-// of three slots); then the 32 MFMAs per wave of tile t run while the loads
+// of three slots); then the 16 MFMAs per wave of tile t run while the loads
 // of three tiles are in flight. One barrier per tile. Interior tiles take a
 // path with no load predicates and 32-bit offsets from uniform base
 // pointers; edge tiles zero-fill outside [M, N, K) and keep one slot.
@@ -45,6 +47,7 @@ namespace {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 128, BN = 128, BK = 16;
+constexpr int NT = 512;  // threads of the 128x128 kernel: 8 waves
 constexpr int GROUP_M = 8;
 // Register slots of the 128x128 kernel's load ring on interior tiles: tile
 // t+KSLOTS's global loads are issued while tile t's MFMAs run. Edge tiles
@@ -145,14 +148,15 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                                               int64_t kbeg, int64_t kend,
                                               float (*As)[BK][LdsA<TA>::S],
                                               float (*Bs)[BK][LdsB<TB>::S],
-                                              floatx16 (&acc)[2][2]) {
+                                              floatx16 (&acc)[2]) {
     const int tid = threadIdx.x;
     const int64_t M = p.m, N = p.n;
     // A K-tile of each operand is 128 x BK floats = 32*BK float4; thread tid
-    // moves float4 idx = tid + 256*i, i < BK/8.
+    // moves float4 idx = tid + NT*i, i < NL.
     // Row-major-in-k operands (A for nn/nt, B for nt): row idx/(BK/4), k (idx%(BK/4))*4.
     // k-major operands (A for tn, B for nn/tn): k idx/32, column (idx%32)*4.
-    constexpr int NL = BK / 8;
+    constexpr int NL = 32 * BK / NT;
+    static_assert(NL >= 1 && 32 * BK % NT == 0, "a K-tile must split evenly over the threads");
     constexpr int RQ = BK / 4;  // float4 per row of a row-major-in-k tile
     // Uniform bases (moved by the tile's k) and loop-invariant 32-bit byte
     // offsets per thread, so each load is one SGPR base + VGPR offset
@@ -163,7 +167,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     uint32_t ao[NL], bo[NL];
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
-        const int idx = tid + 256 * i;
+        const int idx = tid + NT * i;
         ao[i] = 4u * (TA ? (uint32_t)(idx >> 5) * lda + (idx & 31) * 4
                          : (uint32_t)(idx / RQ) * lda + (idx % RQ) * 4);
         bo[i] = 4u * (TB ? (uint32_t)(idx / RQ) * ldb + (idx % RQ) * 4
@@ -237,15 +241,15 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
                 rb[sl][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rsb, bo[i], 0, 0));
         } else {
 #pragma unroll
-            for (int i = 0; i < NL; ++i) ra[sl][i] = load_a_edge(tid + 256 * i, k0);
+            for (int i = 0; i < NL; ++i) ra[sl][i] = load_a_edge(tid + NT * i, k0);
 #pragma unroll
-            for (int i = 0; i < NL; ++i) rb[sl][i] = load_b_edge(tid + 256 * i, k0);
+            for (int i = 0; i < NL; ++i) rb[sl][i] = load_b_edge(tid + NT * i, k0);
         }
     };
     auto store = [&](int sl, int buf) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < NL; ++i) {
-            const int idx = tid + 256 * i;
+            const int idx = tid + NT * i;
             if (!TA) {
                 const int row = idx / RQ, kq = (idx % RQ) * 4;
                 As[buf][kq + 0][row] = ra[sl][i].x;
@@ -280,17 +284,19 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     const int lr = lane & 31, lk = lane >> 5;
 
     // One tile's MFMAs from LDS stage `buf`: all operand reads are issued
-    // first (for each k-pair kk the float2 holds the operand of row or column
-    // block 0 and of block 1); the MFMAs consume them in order as they land.
+    // first (for each k-pair kk the A value of the lane's row and the B
+    // values of its two column blocks); the MFMAs consume them in order as
+    // they land.
     constexpr int cstep = CL == 0 ? 1 : CL == 1 ? 32 : 64;  // block 1's column offset
     const int cbase = CL == 0 ? wn * 64 + 2 * lr : CL == 1 ? wn * 64 + lr : wn * 32 + lr;
     auto compute = [&](int buf) __attribute__((always_inline)) {
-        const float *pa = &As[buf][lk][wm * 64 + 2 * lr];
+        const float *pa = &As[buf][lk][wm * 32 + lr];
         const float *pb = &Bs[buf][lk][cbase];
-        float2 a[BK / 2], b[BK / 2];
+        float a[BK / 2];
+        float2 b[BK / 2];
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) {
-            a[kk] = *reinterpret_cast<const float2 *>(pa + 2 * kk * LdsA<TA>::S);
+            a[kk] = pa[2 * kk * LdsA<TA>::S];
             if constexpr (CL == 0)
                 b[kk] = *reinterpret_cast<const float2 *>(pb + 2 * kk * LdsB<TB>::S);
             else
@@ -298,10 +304,8 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
         }
 #pragma unroll
         for (int kk = 0; kk < BK / 2; ++kk) {
-            acc[0][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].x, b[kk].x, acc[0][0], 0, 0, 0);
-            acc[0][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].x, b[kk].y, acc[0][1], 0, 0, 0);
-            acc[1][0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].y, b[kk].x, acc[1][0], 0, 0, 0);
-            acc[1][1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk].y, b[kk].y, acc[1][1], 0, 0, 0);
+            acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], b[kk].x, acc[0], 0, 0, 0);
+            acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk], b[kk].y, acc[1], 0, 0, 0);
         }
     };
 
@@ -347,7 +351,7 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
 }
 
 template <bool TA, bool TB, int EPI, int CL = 0>
-__global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
+__global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     static_assert(CL == 0 || EPI == EPI_STORE, "the RoPE column layouts store plain values");
     __shared__ __attribute__((aligned(16))) float As[2][BK][LdsA<TA>::S];
     __shared__ __attribute__((aligned(16))) float Bs[2][BK][LdsB<TB>::S];
@@ -378,29 +382,28 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
     const int64_t kend = min(p.k, kbeg + p.k_per_split);
     const int64_t M = p.m, N = p.n;
 
-    floatx16 acc[2][2];
+    floatx16 acc[2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
     const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
                       (kend - kbeg) % BK == 0;
-    // the loss epilogue's registers leave room for two slots at 3 workgroups per CU
-    constexpr int slots = EPI == EPI_CE ? 2 : KSLOTS;
     if (fast)
-        gemm_mainloop<TA, TB, true, slots, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+        gemm_mainloop<TA, TB, true, KSLOTS, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
     else
         gemm_mainloop<TA, TB, false, 1, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
 
-    // ---- epilogue: block (i, j) register r of lane l is C[row][col] with
-    // row = base_row + 2*(8*(r/4) + 4*(l/32) + r%4) + i, col = base_col + 2*(l%32) + j
-    // (CL 0; the other layouts below).
+    // ---- epilogue: block j register r of lane l is C[row][col] with
+    // row = m0 + 32*wm + 8*(r/4) + 4*(l/32) + r%4 and, for CL 0,
+    // col = n0 + 64*wn + 2*(l%32) + j (the other layouts below).
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, lk = lane >> 5;
     const int64_t col = n0 + wn * 64 + 2 * lr;
+    auto row_local = [&](int r) __attribute__((always_inline)) {
+        return wm * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
+    };
     if constexpr (CL != 0) {
         // Column block j of lane lr is column c0 + j*half of C (half = 32 for
         // CL 1, 64 for CL 2), c0 the lane's column in the first half of its
@@ -413,73 +416,67 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
         const bool rot = p.rope_cos != nullptr && c0 < p.rope_cols;
         float *C = p.c + batch * p.stride_c;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-                if (row >= M) continue;
-                float x1 = acc[i][0][r], x2 = acc[i][1][r];
-                if (rot) {
-                    const int64_t t = (row % p.rope_seq) * half + hc;
-                    const float cs = p.rope_cos[t], sn = p.rope_sin[t];
-                    const float y1 = x1 * cs - x2 * sn;
-                    const float y2 = x2 * cs + x1 * sn;
-                    x1 = y1;
-                    x2 = y2;
-                }
-                if (c0 < N) C[row * p.ldc + c0] = x1;
-                if (c0 + half < N) C[row * p.ldc + c0 + half] = x2;
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + row_local(r);
+            if (row >= M) continue;
+            float x1 = acc[0][r], x2 = acc[1][r];
+            if (rot) {
+                const int64_t t = (row % p.rope_seq) * half + hc;
+                const float cs = p.rope_cos[t], sn = p.rope_sin[t];
+                const float y1 = x1 * cs - x2 * sn;
+                const float y2 = x2 * cs + x1 * sn;
+                x1 = y1;
+                x2 = y2;
             }
+            if (c0 < N) C[row * p.ldc + c0] = x1;
+            if (c0 + half < N) C[row * p.ldc + c0 + half] = x2;
+        }
         return;
     }
     if (p.splits > 1) {
         float *P = p.partial + (int64_t)split * M * N;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-                if (row < M) {
-                    if (col < N) P[row * N + col] = acc[i][0][r];
-                    if (col + 1 < N) P[row * N + col + 1] = acc[i][1][r];
-                }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + row_local(r);
+            if (row < M) {
+                if (col < N) P[row * N + col] = acc[0][r];
+                if (col + 1 < N) P[row * N + col + 1] = acc[1][r];
             }
+        }
         return;
     }
     if constexpr (EPI == EPI_CE) {
         // Cross-entropy partials of this tile's columns (ops_reduce.rs:236-259
         // split by column tiles): per row, the max of the logits and the sum of
         // exp(z - max) over the lane's two columns, over the 32 lanes of its
-        // half by xor exchanges, then over the two waves sharing the rows
-        // through LDS. The lane holding a row's target column keeps its logit.
+        // half by DPP moves, then over the two waves sharing the rows through
+        // LDS. The lane holding a row's target column keeps its logit.
         __shared__ float ce_m[2][BM], ce_s[2][BM];
         __shared__ int ce_t[BM];
         if (tid < BM) ce_t[tid] = m0 + tid < M ? p.ce_targets[m0 + tid] : -1;
         __syncthreads();
         constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int rl = wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-                const int64_t row = m0 + rl;
-                const float v0 = acc[i][0][r], v1 = acc[i][1][r];
-                const float x0 = col < N ? v0 : -INFINITY, x1 = col + 1 < N ? v1 : -INFINITY;
-                const float mx = half_max32(fmaxf(x0, x1));
-                // exp(z - max) through the hardware's exp2 (no flush concern: the
-                // terms that matter are within a few hundred of 1)
-                const float e = half_sum32(
-                    mx == -INFINITY ? 0.0f
-                                    : __builtin_amdgcn_exp2f((x0 - mx) * kLog2e) +
-                                          __builtin_amdgcn_exp2f((x1 - mx) * kLog2e));
-                if (lr == 0) {
-                    ce_m[wn][rl] = mx;
-                    ce_s[wn][rl] = e;
-                }
-                const int t = ce_t[rl];
-                if (t == col) p.ce_zt[row] = v0;
-                if (t == col + 1) p.ce_zt[row] = v1;
+        for (int r = 0; r < 16; ++r) {
+            const int rl = row_local(r);
+            const int64_t row = m0 + rl;
+            const float v0 = acc[0][r], v1 = acc[1][r];
+            const float x0 = col < N ? v0 : -INFINITY, x1 = col + 1 < N ? v1 : -INFINITY;
+            const float mx = half_max32(fmaxf(x0, x1));
+            // exp(z - max) through the hardware's exp2 (no flush concern: the
+            // terms that matter are within a few hundred of 1)
+            const float e = half_sum32(
+                mx == -INFINITY ? 0.0f
+                                : __builtin_amdgcn_exp2f((x0 - mx) * kLog2e) +
+                                      __builtin_amdgcn_exp2f((x1 - mx) * kLog2e));
+            if (lr == 0) {
+                ce_m[wn][rl] = mx;
+                ce_s[wn][rl] = e;
             }
+            const int t = ce_t[rl];
+            if (t == col) p.ce_zt[row] = v0;
+            if (t == col + 1) p.ce_zt[row] = v1;
+        }
         __syncthreads();
         if (tid < BM && m0 + tid < M) {
             float m = ce_m[0][tid], sum = ce_s[0][tid];
@@ -494,66 +491,59 @@ __global__ __launch_bounds__(256, 3) void gemm_f32_mfma(KParams p) {
         // Packed columns interleave gate and up: column 2f is gate f, 2f+1 up f.
         const int64_t f = col >> 1;
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-                if (row >= M) continue;
-                if (p.aux && col + 1 < N)
-                    *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) =
-                        make_float2(acc[i][0][r], acc[i][1][r]);
-                if (f < p.swiglu_ff)
-                    C[row * p.ldc + f] = __fmul_rn(silu_f(acc[i][0][r]), acc[i][1][r]);
-            }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + row_local(r);
+            if (row >= M) continue;
+            if (p.aux && col + 1 < N)
+                *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) =
+                    make_float2(acc[0][r], acc[1][r]);
+            if (f < p.swiglu_ff) C[row * p.ldc + f] = __fmul_rn(silu_f(acc[0][r]), acc[1][r]);
+        }
         return;
     }
     if (EPI == EPI_SWIGLU_BWD) {
         // acc is dh[row][col, col+1]; their (g, u) pairs sit at aux columns
         // 2*col .. 2*col+3 and the (dg, du) pairs go to the same columns of C.
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-                if (row >= M) continue;
-                const float *gu = p.aux + row * p.ldaux + 2 * col;
-                float *dst = C + row * p.ldc + 2 * col;
-                if (col + 1 < N) {
-                    const float4 v = *reinterpret_cast<const float4 *>(gu);
-                    const float2 a = swiglu_bwd_f(acc[i][0][r], v.x, v.y);
-                    const float2 b2 = swiglu_bwd_f(acc[i][1][r], v.z, v.w);
-                    *reinterpret_cast<float4 *>(dst) = make_float4(a.x, a.y, b2.x, b2.y);
-                } else if (col < N) {
-                    const float2 a = swiglu_bwd_f(acc[i][0][r], gu[0], gu[1]);
-                    dst[0] = a.x;
-                    dst[1] = a.y;
-                }
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + row_local(r);
+            if (row >= M) continue;
+            const float *gu = p.aux + row * p.ldaux + 2 * col;
+            float *dst = C + row * p.ldc + 2 * col;
+            if (col + 1 < N) {
+                const float4 v = *reinterpret_cast<const float4 *>(gu);
+                const float2 a = swiglu_bwd_f(acc[0][r], v.x, v.y);
+                const float2 b2 = swiglu_bwd_f(acc[1][r], v.z, v.w);
+                *reinterpret_cast<float4 *>(dst) = make_float4(a.x, a.y, b2.x, b2.y);
+            } else if (col < N) {
+                const float2 a = swiglu_bwd_f(acc[0][r], gu[0], gu[1]);
+                dst[0] = a.x;
+                dst[1] = a.y;
             }
+        }
         return;
     }
     const float *R = p.resid ? p.resid + batch * p.stride_c : C;
     const bool pair = p.vec_c && col + 1 < N;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + wm * 64 + 2 * (8 * (r >> 2) + 4 * lk + (r & 3)) + i;
-            if (row >= M) continue;
-            float *dst = C + row * p.ldc + col;
-            const float *src = R + row * p.ldc + col;
-            float v0 = acc[i][0][r], v1 = acc[i][1][r];
-            if (pair) {
-                if (EPI == EPI_ACCUM) {
-                    const float2 o = *reinterpret_cast<const float2 *>(src);
-                    v0 = __fadd_rn(o.x, v0);
-                    v1 = __fadd_rn(o.y, v1);
-                }
-                *reinterpret_cast<float2 *>(dst) = make_float2(v0, v1);
-            } else {
-                if (col < N) dst[0] = EPI == EPI_ACCUM ? __fadd_rn(src[0], v0) : v0;
-                if (col + 1 < N) dst[1] = EPI == EPI_ACCUM ? __fadd_rn(src[1], v1) : v1;
+    for (int r = 0; r < 16; ++r) {
+        const int64_t row = m0 + row_local(r);
+        if (row >= M) continue;
+        float *dst = C + row * p.ldc + col;
+        const float *src = R + row * p.ldc + col;
+        float v0 = acc[0][r], v1 = acc[1][r];
+        if (pair) {
+            if (EPI == EPI_ACCUM) {
+                const float2 o = *reinterpret_cast<const float2 *>(src);
+                v0 = __fadd_rn(o.x, v0);
+                v1 = __fadd_rn(o.y, v1);
             }
+            *reinterpret_cast<float2 *>(dst) = make_float2(v0, v1);
+        } else {
+            if (col < N) dst[0] = EPI == EPI_ACCUM ? __fadd_rn(src[0], v0) : v0;
+            if (col + 1 < N) dst[1] = EPI == EPI_ACCUM ? __fadd_rn(src[1], v1) : v1;
         }
+    }
 }
 
 // ---- small-tile GEMM ---------------------------------------------------------
@@ -1141,10 +1131,10 @@ void launch(Context &ctx, const KParams &p, dim3 grid, bool small) {
         // RoPE in the 128x128 kernel's epilogue (heads of 64 or 128 columns)
         if (!small && p.rope_cos) {
             if (p.rope_hd == 64)
-                hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI, 1>), grid, dim3(256), 0,
+                hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI, 1>), grid, dim3(NT), 0,
                                    ctx.stream, p);
             else
-                hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI, 2>), grid, dim3(256), 0,
+                hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI, 2>), grid, dim3(NT), 0,
                                    ctx.stream, p);
             return;
         }
@@ -1153,7 +1143,7 @@ void launch(Context &ctx, const KParams &p, dim3 grid, bool small) {
         hipLaunchKernelGGL((gemm_f32_mfma_small<TA, TB, EPI, false>), grid, dim3(256), 0,
                            ctx.stream, p);
     else
-        hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI>), grid, dim3(256), 0, ctx.stream, p);
+        hipLaunchKernelGGL((gemm_f32_mfma<TA, TB, EPI>), grid, dim3(NT), 0, ctx.stream, p);
 }
 
 template <int EPI>
@@ -1372,10 +1362,10 @@ void gemm(Context &ctx, const GemmDesc &d) {
                               : launch_ksplit<true, false, EPI_STORE>)(ctx, p, grid, mode);
     } else if (epi == EPI_CE) {
         if (d.tb)
-            hipLaunchKernelGGL((gemm_f32_mfma<false, true, EPI_CE>), grid, dim3(256), 0,
+            hipLaunchKernelGGL((gemm_f32_mfma<false, true, EPI_CE>), grid, dim3(NT), 0,
                                ctx.stream, p);
         else
-            hipLaunchKernelGGL((gemm_f32_mfma<false, false, EPI_CE>), grid, dim3(256), 0,
+            hipLaunchKernelGGL((gemm_f32_mfma<false, false, EPI_CE>), grid, dim3(NT), 0,
                                ctx.stream, p);
     } else if (epi == EPI_SWIGLU) {
         if (d.ta || d.tb) fail(MMH_ERR_ARGUMENT, "gemm: swiglu epilogue needs the nn form");
