@@ -37,9 +37,9 @@ PEAK_HBM_GBS = 8000.0
 # rocprofv3 passes over this same bench (--pmc FETCH_SIZE, then --pmc
 # WRITE_SIZE, --steps 1 --warmup 0 --train-steps 0 --copy-probe), each scaled by
 # what the counter reads for the add kernel's known traffic (FETCH x 2.0,
-# WRITE x 1.0): (45,797,122 + 4,439,363) KiB over 81 launches. The counters
+# WRITE x 1.0): (48,516,468 + 4,438,255) KiB over 81 launches. The counters
 # cannot be read from inside this process; see profiles/large_forward_hbm_traffic.md.
-GEMM_TRAFFIC_BYTES_PER_LAUNCH = 635.1e6
+GEMM_TRAFFIC_BYTES_PER_LAUNCH = 669.5e6
 
 
 def log(msg):

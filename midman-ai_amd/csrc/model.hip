@@ -668,7 +668,14 @@ struct Model {
             float *gu = tr.gu + l * cap * ffp2, *hl = tr.h + l * cap * cfg.ff;
             float *xnext = tr.xs + (l + 1) * cap * d;
             launch_rms_norm(c, x, attn_norm(l), n, d, cfg.eps, xn1);
-            gemm(c, desc(xn1, false, d, wqkv(l), false, qc, qkvl, qc, n, d, qc));
+            // q, k rotated by the QKV GEMM (in its epilogue or right after it)
+            GemmDesc q = desc(xn1, false, d, wqkv(l), false, qc, qkvl, qc, n, d, qc);
+            q.rope_cos = cos_t;
+            q.rope_sin = sin_t;
+            q.rope_seq = seq;
+            q.rope_hd = hd;
+            q.rope_cols = d + kv;
+            gemm(c, q);
             AttnDesc a{};
             a.q = qkvl;
             a.k = qkvl + d;
@@ -685,8 +692,6 @@ struct Model {
             a.hkv = cfg.kv_heads;
             a.t = seq;
             a.hd = hd;
-            a.cos_t = cos_t;
-            a.sin_t = sin_t;
             a.lse = tr.lse + l * lse_rows(cap);
             attention(c, a);
             GemmDesc o = desc(cbl, false, d, wo(l), false, d, hres, d, n, d, d);
