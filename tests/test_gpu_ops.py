@@ -164,8 +164,9 @@ def test_attention_forward(ctx, B, T, d, H, Hkv):
     # GEMM's epilogue
     (8, 1024, 1024, 16, 16, 2816), (8, 1024, 1024, 16, 8, 2816),
     # heads of 128 (the large preset's), QKV at 512 tiles of 128x128: rotated
-    # in the epilogue, with no K split
-    (2, 1024, 2048, 16, 8, 512)])
+    # in the epilogue, with no K split; then 2049 rows (a last row tile of
+    # one row, ragged sequences)
+    (2, 1024, 2048, 16, 8, 512), (3, 683, 2048, 16, 8, 512)])
 def test_block_forward(ctx, B, T, d, H, Hkv, ff):
     """DecoderBlock::forward (block.rs:77-81) against the oracle's block."""
     print(f"\n[block_forward] B={B} T={T} d={d} H={H} Hkv={Hkv} ff={ff}", flush=True)
