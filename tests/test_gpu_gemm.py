@@ -77,6 +77,10 @@ def test_sweep_forward_and_backward(ctx, k, n):
 @pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (12, 16, 32), (33, 17, 65),
                                    (129, 250, 131), (64, 4097, 40), (300, 8, 1000),
                                    (2048, 128, 4096),
+                                   # the 128x128 kernel's load ring (3 slots, unrolled by 6)
+                                   # with 1, 3, 6 and 7 K-tiles, the last with ragged edges
+                                   (2048, 16, 4096), (2048, 48, 4096), (2048, 96, 4096),
+                                   (2050, 112, 4100),
                                    # short-K shapes of the tiny preset and its edges
                                    (2048, 128, 384), (2048, 352, 128), (2047, 480, 97),
                                    (2000, 481, 50), (65, 33, 700)])
