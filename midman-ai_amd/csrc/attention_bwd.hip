@@ -454,6 +454,238 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
     }
 }
 
+// ---- small grids ----------------------------------------------------------
+// When the 128-row blocks leave CUs idle and the head is at most 64 wide (the
+// tiny preset: 4 heads x 8 sequences of 256 rows give 64 workgroups), each
+// workgroup owns one 32-row strip (dq: queries; dkv: keys) and its 4 waves
+// take the key tiles (dq) or query tiles (dkv) round-robin, reading every
+// operand straight from memory into the MFMA layouts (no LDS staging, no
+// barrier per tile). The products, the masks and the arithmetic are those of
+// the kernels above; the 4 partial accumulators are then summed through LDS
+// in wave order (deterministic) and written as rows.
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_bwd_dq_split_kernel(BwdP p) {
+    constexpr int NS = HD / 2, NDB = (HD + 31) / 32, OS = HD + 1;
+    __shared__ float red[3][NDB * 16][64];
+    __shared__ float Os[32 * OS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int head = blockIdx.x, b = blockIdx.y;
+    const int T = p.t;
+    const int nstrips = (T + 31) / 32;
+    const int strip = nstrips - 1 - (int)blockIdx.z;  // longest rows first
+    const int kvh = head / (p.h / p.hkv);
+    const int q0 = strip * 32;
+    const int ntiles = strip + 1;  // key tiles 0 .. strip
+    const int qi = q0 + lq;
+    const int qc = min(qi, T - 1);
+
+    const float *Q = p.q + b * p.sqb + head * p.sqh;
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+    const float *O = p.o + b * p.sob + head * p.soh;
+    const float *dO = p.dout + b * p.sob + head * p.soh;
+    const int64_t rows = ((int64_t)b * p.h + head) * T;
+
+    const float sc = p.scale * 1.4426950408889634f;
+    float qr[NS], gr[NS];
+    load_run<NS>(qr, Q + (int64_t)qc * p.sqt + lh * NS);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qr[s] *= sc;
+    load_run<NS>(gr, dO + (int64_t)qc * p.sot + lh * NS);
+    float dsum = 0.0f;
+    {
+        const float *orow = O + (int64_t)qc * p.sot + lh * NS;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dsum += gr[s] * orow[s];
+    }
+    dsum += __shfl_xor(dsum, 32, 64);
+    const float Dq = dsum;
+    const float L2 = p.lse[rows + qc];
+    if (wave == 0 && lh == 0 && qi < T) p.dvec[rows + qi] = Dq;
+
+    floatx16 dq[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) dq[db][r] = 0.0f;
+    for (int kt = wave; kt < ntiles; kt += 4) {
+        const int k0 = kt * 32;
+        // keys past T read row T-1 (finite values whose P is 0)
+        const int key_l = min(k0 + lq, T - 1);
+        floatx16 s0, s1, g0, g1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = 0.0f;
+            s1[r] = 0.0f;
+            g0[r] = 0.0f;
+            g1[r] = 0.0f;
+        }
+        dot_chains<NS>(K + (int64_t)key_l * p.skt + lh * NS, qr, s0, s1);
+        dot_chains<NS>(V + (int64_t)key_l * p.svt + lh * NS, gr, g0, g1);
+        const bool full = k0 + 31 <= q0 && k0 + 31 < T;
+        float ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+            const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - L2);
+            const float pr = (full || (key <= qi && key < T)) ? e : 0.0f;
+            ds[r] = pr * ((g0[r] + g1[r]) - Dq);
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int key = min(k0 + 8 * (s >> 2) + 4 * lh + (s & 3), T - 1);
+            float a[NDB];
+            read_dims<HD, NDB>(a, K + (int64_t)key * p.skt, lq);
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) dq[db] = mfma(a[db], ds[s], dq[db]);
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) red[wave - 1][db * 16 + r][lane] = dq[db][r];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                float v = dq[db][r];
+#pragma unroll
+                for (int w = 0; w < 3; ++w) v += red[w][db * 16 + r][lane];
+                const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+                const int d = NDB * i + db;
+                if (d < HD) Os[lq * OS + d] = v * p.scale;
+            }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < 32 * HD; idx += 256) {
+        const int j = idx / HD, c = idx - j * HD;
+        const int q = q0 + j;
+        if (q < T) p.dq[b * p.sqb + head * p.sqh + (int64_t)q * p.sqt + c] = Os[j * OS + c];
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_split_kernel(BwdP p) {
+    constexpr int NS = HD / 2, NDB = (HD + 31) / 32, OS = HD + 1;
+    __shared__ float red[3][NDB * 16][64];
+    __shared__ float Os[32 * OS];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int lq = lane & 31, lh = lane >> 5;
+    const int groups = p.h / p.hkv;
+    const int kvh = blockIdx.x, b = blockIdx.y;
+    const int kstrip = blockIdx.z;  // strip 0 sees the most queries and starts first
+    const int T = p.t;
+    const int k0 = kstrip * 32;
+    const int kj = k0 + lq;
+    const int kc = min(kj, T - 1);
+    const int nqt = (T + 31) / 32;
+    const int per_head = nqt - kstrip;  // query tiles at or after the keys
+    const int total = groups * per_head;
+
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+    const float sc = p.scale * 1.4426950408889634f;
+    float kr[NS], vr[NS];
+    load_run<NS>(kr, K + (int64_t)kc * p.skt + lh * NS);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) kr[s] *= sc;
+    load_run<NS>(vr, V + (int64_t)kc * p.svt + lh * NS);
+
+    floatx16 dk[NDB], dv[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            dk[db][r] = 0.0f;
+            dv[db][r] = 0.0f;
+        }
+    for (int it = wave; it < total; it += 4) {
+        const int g = it / per_head;
+        const int qt = kstrip + (it - g * per_head);
+        const int head = kvh * groups + g;
+        const float *Qh = p.q + b * p.sqb + head * p.sqh;
+        const float *Gh = p.dout + b * p.sob + head * p.soh;
+        // rows past T read row T-1 (finite; their P is 0)
+        const int qrow = min(qt * 32 + lq, T - 1);
+        // lanes 0-31 hold the tile's log-sum-exps, 32-63 its D values
+        const float lreg = ((lh != 0) ? p.dvec : p.lse)[((int64_t)b * p.h + head) * T + qrow];
+        floatx16 s0, s1, g0, g1;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            s0[r] = 0.0f;
+            s1[r] = 0.0f;
+            g0[r] = 0.0f;
+            g1[r] = 0.0f;
+        }
+        dot_chains<NS>(Qh + (int64_t)qrow * p.sqt + lh * NS, kr, s0, s1);
+        dot_chains<NS>(Gh + (int64_t)qrow * p.sot + lh * NS, vr, g0, g1);
+        const bool full = qt * 32 >= k0 + 31 && qt * 32 + 31 < T && k0 + 31 < T;
+        float pv[16], ds[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
+            const int q = qt * 32 + row;
+            const float lrow = __shfl(lreg, row, 64), drow = __shfl(lreg, 32 + row, 64);
+            const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - lrow);
+            const float pr = (full || (kj <= q && q < T && kj < T)) ? e : 0.0f;
+            pv[r] = pr;
+            ds[r] = pr * ((g0[r] + g1[r]) - drow);
+        }
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const int q = min(qt * 32 + 8 * (s >> 2) + 4 * lh + (s & 3), T - 1);
+            float ag[NDB], aq[NDB];
+            read_dims<HD, NDB>(ag, Gh + (int64_t)q * p.sot, lq);
+            read_dims<HD, NDB>(aq, Qh + (int64_t)q * p.sqt, lq);
+#pragma unroll
+            for (int db = 0; db < NDB; ++db) {
+                dv[db] = mfma(ag[db], pv[s], dv[db]);
+                dk[db] = mfma(aq[db], ds[s], dk[db]);
+            }
+        }
+    }
+    // dK = scale * dK^T and dV = dV^T: the waves' partials summed in wave
+    // order, through LDS as [key][d], then rows.
+    for (int which = 0; which < 2; ++which) {
+        if (wave > 0) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r)
+                    red[wave - 1][db * 16 + r][lane] = which == 0 ? dk[db][r] : dv[db][r];
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int db = 0; db < NDB; ++db)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float v = which == 0 ? dk[db][r] : dv[db][r];
+#pragma unroll
+                    for (int w = 0; w < 3; ++w) v += red[w][db * 16 + r][lane];
+                    const int i = 8 * (r >> 2) + 4 * lh + (r & 3);
+                    const int d = NDB * i + db;
+                    if (d < HD) Os[lq * OS + d] = which == 0 ? v * p.scale : v;
+                }
+        }
+        __syncthreads();
+        float *dst = which == 0 ? p.dk + b * p.skb + kvh * p.skh : p.dv + b * p.svb + kvh * p.svh;
+        const int64_t st = which == 0 ? p.skt : p.svt;
+        for (int idx = tid; idx < 32 * HD; idx += 256) {
+            const int j = idx / HD, c = idx - j * HD;
+            const int key = k0 + j;
+            if (key < T) dst[(int64_t)key * st + c] = Os[j * OS + c];
+        }
+        __syncthreads();
+    }
+}
+
 // dK, dV of kv head j = the sum of its group's partials in head order.
 // One thread per 4 consecutive dims of one (batch, kv head, key).
 __global__ __launch_bounds__(256) void dkv_group_sum_kernel(const float *__restrict__ part, int b,
@@ -533,12 +765,26 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
     p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
     // GQA: per-query-head partials when the caller gave room for them and the
     // head is wide enough for the float4 sum (hd >= 4 always holds).
-    p.part = d.h > d.hkv && d.scratch ? d.scratch : nullptr;
+    // small grids (fewer 128-row blocks than CUs, heads up to 64 wide): the
+    // strip kernels, which need no partials (a group's heads are summed in
+    // one workgroup)
+    const int cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
+    const bool split = d.hd <= 64 && d.b * d.h * p.nqb < cus;
+    p.part = !split && d.h > d.hkv && d.scratch ? d.scratch : nullptr;
     const dim3 gq((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
     const dim3 gk((unsigned)(p.part ? d.h : d.hkv), (unsigned)d.b, (unsigned)p.nkb);
+    const unsigned strips = (unsigned)((d.t + 31) / 32);
+    const dim3 sq((unsigned)d.h, (unsigned)d.b, strips), sk((unsigned)d.hkv, (unsigned)d.b, strips);
     const dim3 blk(256);
 #define MMH_BWD_CASE(HD)                                                                   \
     case HD:                                                                               \
+        if constexpr (HD <= 64) {                                                          \
+            if (split) {                                                                   \
+                hipLaunchKernelGGL((attn_bwd_dq_split_kernel<HD>), sq, blk, 0, ctx.stream, p); \
+                hipLaunchKernelGGL((attn_bwd_dkv_split_kernel<HD>), sk, blk, 0, ctx.stream, p); \
+                break;                                                                     \
+            }                                                                              \
+        }                                                                                  \
         hipLaunchKernelGGL((attn_bwd_dq_kernel<HD>), gq, blk, 0, ctx.stream, p);           \
         hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD>), gk, blk, 0, ctx.stream, p);          \
         break;

@@ -86,6 +86,9 @@ def test_backward_matches_oracle(ctx, name):
 ATTN_SHAPES = [  # B, H, Hkv, T, hd
     (1, 2, 1, 33, 4), (2, 4, 2, 70, 8), (1, 2, 2, 64, 16), (2, 4, 1, 100, 32),
     (1, 4, 2, 130, 64), (1, 2, 1, 200, 128), (1, 1, 1, 1, 64), (2, 2, 2, 257, 128),
+    # grids of at least one 128-row block per CU take the block kernels (the
+    # shapes above, the strip kernels) also for heads of 64 and 32
+    (4, 16, 8, 512, 64), (8, 8, 8, 512, 32),
 ]
 
 
