@@ -8,6 +8,8 @@
 // operation rounds exactly where the reference's does; that makes the
 // embedding, RoPE and add bit-exact, and leaves RMSNorm and the loss differing
 // from the reference only by summation order.
+#include <algorithm>
+
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -286,33 +288,58 @@ __global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__
     if (threadIdx.x == 0) out[0] = (float)(part[0] / (double)n);
 }
 
-// ---- weight packing (model creation) ------------------------------------------
+// ---- weight packing (model creation, after every optimizer step) -------------
+// A workgroup row of the grid (blockIdx.y, striding by gridDim.y) walks whole
+// rows; its threads walk the row in float4s where the layout allows (vec),
+// else in single floats. Bit-exact copies.
 __global__ __launch_bounds__(256) void pack_cols_kernel(const float *__restrict__ src,
                                                         int64_t rows, int64_t cols,
                                                         float *__restrict__ dst, int64_t ld_dst,
-                                                        int64_t col_off) {
-    const int64_t total = rows * cols;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / cols, c = i - r * cols;
-        dst[r * ld_dst + col_off + c] = src[i];
+                                                        int64_t col_off, int vec) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float *s = src + r * cols;
+        float *d = dst + r * ld_dst + col_off;
+        if (vec) {
+            for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < cols / 4; q += step)
+                reinterpret_cast<float4 *>(d)[q] = reinterpret_cast<const float4 *>(s)[q];
+        } else {
+            for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += step)
+                d[c] = s[c];
+        }
     }
 }
 
 // dst [rows, 2*ff_pad]: column 2f is gate column f and column 2f+1 is up
-// column f; columns of f >= ff are zero.
+// column f; columns of f >= ff are zero. A thread moves 4 columns f of both.
 __global__ __launch_bounds__(256) void pack_gate_up_kernel(const float *__restrict__ wg,
                                                            const float *__restrict__ wu,
                                                            int64_t rows, int64_t ff,
                                                            int64_t ff_pad,
-                                                           float *__restrict__ dst) {
-    const int64_t cols = 2 * ff_pad, total = rows * cols;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / cols, c2 = i - r * cols;
-        const int64_t f = c2 >> 1;
-        const float *src = (c2 & 1) ? wu : wg;
-        dst[i] = f < ff ? src[r * ff + f] : 0.0f;
+                                                           float *__restrict__ dst, int vec) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float *g = wg + r * ff, *u = wu + r * ff;
+        float4 *d = reinterpret_cast<float4 *>(dst + r * 2 * ff_pad);
+        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < ff_pad / 4; q += step) {
+            const int64_t f = 4 * q;
+            float4 a, b;
+            if (vec && f + 3 < ff) {
+                a = reinterpret_cast<const float4 *>(g)[q];
+                b = reinterpret_cast<const float4 *>(u)[q];
+            } else {
+                a.x = f + 0 < ff ? g[f + 0] : 0.0f;
+                a.y = f + 1 < ff ? g[f + 1] : 0.0f;
+                a.z = f + 2 < ff ? g[f + 2] : 0.0f;
+                a.w = f + 3 < ff ? g[f + 3] : 0.0f;
+                b.x = f + 0 < ff ? u[f + 0] : 0.0f;
+                b.y = f + 1 < ff ? u[f + 1] : 0.0f;
+                b.z = f + 2 < ff ? u[f + 2] : 0.0f;
+                b.w = f + 3 < ff ? u[f + 3] : 0.0f;
+            }
+            d[2 * q] = make_float4(a.x, b.x, a.y, b.y);
+            d[2 * q + 1] = make_float4(a.z, b.z, a.w, b.w);
+        }
     }
 }
 
@@ -407,17 +434,27 @@ void launch_ce_combine(Context &ctx, const float *part, int64_t tiles, const flo
     check_hip(hipGetLastError(), "loss mean launch");
 }
 
+// Grid of the row-walking copy kernels: enough threads for a row's units in
+// x, rows (at most 65535 at a time) in y.
+dim3 rows_grid(int64_t rows, int64_t units) {
+    const int64_t x = std::max<int64_t>(1, std::min<int64_t>((units + 255) / 256, 64));
+    return dim3((unsigned)x, (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, 65535)));
+}
+
 void launch_pack_cols(Context &ctx, const float *src, int64_t rows, int64_t cols, float *dst,
                       int64_t ld_dst, int64_t col_off) {
-    hipLaunchKernelGGL(pack_cols_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, ctx.stream,
-                       src, rows, cols, dst, ld_dst, col_off);
+    const int vec = cols % 4 == 0 && ld_dst % 4 == 0 && col_off % 4 == 0 && al16(src) && al16(dst);
+    hipLaunchKernelGGL(pack_cols_kernel, rows_grid(rows, vec ? cols / 4 : cols), dim3(256), 0,
+                       ctx.stream, src, rows, cols, dst, ld_dst, col_off, vec);
     check_hip(hipGetLastError(), "pack launch");
 }
 
 void launch_pack_gate_up(Context &ctx, const float *wg, const float *wu, int64_t rows,
                          int64_t ff, int64_t ff_pad, float *dst) {
-    hipLaunchKernelGGL(pack_gate_up_kernel, dim3(grid_for(rows * 2 * ff_pad)), dim3(256), 0,
-                       ctx.stream, wg, wu, rows, ff, ff_pad, dst);
+    if (ff_pad % 4 || !al16(dst)) fail(MMH_ERR_ARGUMENT, "pack: padded rows must be float4s");
+    const int vec = ff % 4 == 0 && al16(wg) && al16(wu);
+    hipLaunchKernelGGL(pack_gate_up_kernel, rows_grid(rows, ff_pad / 4), dim3(256), 0, ctx.stream,
+                       wg, wu, rows, ff, ff_pad, dst, vec);
     check_hip(hipGetLastError(), "pack launch");
 }
 

@@ -16,6 +16,8 @@
 //     parameter; nothing is written when the loss or the norm is not finite.
 // Element-wise arithmetic uses explicitly rounded intrinsics, so the update is
 // the reference's operation order with no contraction.
+#include <algorithm>
+
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -339,28 +341,48 @@ __global__ __launch_bounds__(256) void fill_kernel(float *__restrict__ x, int64_
 __global__ __launch_bounds__(256) void unpack_cols_kernel(const float *__restrict__ src,
                                                           int64_t ld_src, int64_t col_off,
                                                           int64_t rows, int64_t cols,
-                                                          float *__restrict__ dst) {
-    const int64_t total = rows * cols;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / cols, c = i - r * cols;
-        dst[i] = src[r * ld_src + col_off + c];
+                                                          float *__restrict__ dst, int vec) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float *s = src + r * ld_src + col_off;
+        float *d = dst + r * cols;
+        if (vec) {
+            for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < cols / 4; q += step)
+                reinterpret_cast<float4 *>(d)[q] = reinterpret_cast<const float4 *>(s)[q];
+        } else {
+            for (int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; c < cols; c += step)
+                d[c] = s[c];
+        }
     }
 }
 
-// src [rows, 2*ff_pad] interleaved (2f gate, 2f+1 up) -> wg, wu [rows, ff].
+// src [rows, 2*ff_pad] interleaved (2f gate, 2f+1 up) -> wg, wu [rows, ff];
+// a thread moves 4 columns f of both.
 __global__ __launch_bounds__(256) void unpack_gate_up_kernel(const float *__restrict__ src,
                                                              int64_t rows, int64_t ff,
                                                              int64_t ff_pad,
                                                              float *__restrict__ wg,
-                                                             float *__restrict__ wu) {
-    const int64_t total = rows * ff;
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        const int64_t r = i / ff, f = i - r * ff;
-        const float2 v = *reinterpret_cast<const float2 *>(src + r * 2 * ff_pad + 2 * f);
-        wg[i] = v.x;
-        wu[i] = v.y;
+                                                             float *__restrict__ wu, int vec) {
+    const int64_t step = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t r = blockIdx.y; r < rows; r += gridDim.y) {
+        const float *s = src + r * 2 * ff_pad;
+        float *g = wg + r * ff, *u = wu + r * ff;
+        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < (ff + 3) / 4;
+             q += step) {
+            const int64_t f = 4 * q;
+            const float4 a = reinterpret_cast<const float4 *>(s)[2 * q];
+            const float4 b = reinterpret_cast<const float4 *>(s)[2 * q + 1];
+            if (vec) {
+                reinterpret_cast<float4 *>(g)[q] = make_float4(a.x, a.z, b.x, b.z);
+                reinterpret_cast<float4 *>(u)[q] = make_float4(a.y, a.w, b.y, b.w);
+            } else {
+                const float gv[4] = {a.x, a.z, b.x, b.z}, uv[4] = {a.y, a.w, b.y, b.w};
+                for (int j = 0; j < 4 && f + j < ff; ++j) {
+                    g[f + j] = gv[j];
+                    u[f + j] = uv[j];
+                }
+            }
+        }
     }
 }
 
@@ -564,15 +586,24 @@ void launch_fill(Context &ctx, float *x, int64_t n, float v) {
 
 void launch_unpack_cols(Context &ctx, const float *src, int64_t ld_src, int64_t col_off,
                         int64_t rows, int64_t cols, float *dst) {
-    hipLaunchKernelGGL(unpack_cols_kernel, dim3(grid_for(rows * cols)), dim3(256), 0, ctx.stream,
-                       src, ld_src, col_off, rows, cols, dst);
+    const int vec = cols % 4 == 0 && ld_src % 4 == 0 && col_off % 4 == 0 && al16(src) && al16(dst);
+    const int64_t units = vec ? cols / 4 : cols;
+    const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>((units + 255) / 256, 64)),
+                    (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, 65535)));
+    hipLaunchKernelGGL(unpack_cols_kernel, grid, dim3(256), 0, ctx.stream, src, ld_src, col_off,
+                       rows, cols, dst, vec);
     check_hip(hipGetLastError(), "unpack launch");
 }
 
 void launch_unpack_gate_up(Context &ctx, const float *src, int64_t rows, int64_t ff,
                            int64_t ff_pad, float *wg, float *wu) {
-    hipLaunchKernelGGL(unpack_gate_up_kernel, dim3(grid_for(rows * ff)), dim3(256), 0,
-                       ctx.stream, src, rows, ff, ff_pad, wg, wu);
+    if (ff_pad % 4 || ff_pad < ff || !al16(src))
+        fail(MMH_ERR_ARGUMENT, "unpack: padded rows must be float4s");
+    const int vec = ff % 4 == 0 && al16(wg) && al16(wu);
+    const dim3 grid((unsigned)std::max<int64_t>(1, std::min<int64_t>(((ff + 3) / 4 + 255) / 256, 64)),
+                    (unsigned)std::max<int64_t>(1, std::min<int64_t>(rows, 65535)));
+    hipLaunchKernelGGL(unpack_gate_up_kernel, grid, dim3(256), 0, ctx.stream, src, rows, ff,
+                       ff_pad, wg, wu, vec);
     check_hip(hipGetLastError(), "unpack launch");
 }
 
