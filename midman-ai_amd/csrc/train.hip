@@ -454,43 +454,68 @@ __global__ __launch_bounds__(256) void adamw_kernel(float *__restrict__ w,
                                                     int64_t n, const int64_t *__restrict__ ranges,
                                                     int nranges, AdamArgs a,
                                                     const float *__restrict__ loss,
-                                                    const float *__restrict__ norm) {
+                                                    const float *__restrict__ norm, bool vec) {
     const float ln = loss[0], nv = norm[0];
     if (!(isfinite(ln) && isfinite(nv))) return;  // a failed step changes nothing
     const bool clip = nv > a.clip_norm;
     const float factor = __fdiv_rn(a.clip_norm, __fadd_rn(nv, 1e-6f));  // clip.rs:52
     const int64_t c0 = (int64_t)blockIdx.x * ADAM_CHUNK;
     const int64_t c1 = min(n, c0 + ADAM_CHUNK);
+    // The undecayed ranges that meet this chunk, found by all threads at
+    // once (their order in the list does not matter: membership is an OR).
     __shared__ int64_t lo[ADAM_MAX_RANGES], hi[ADAM_MAX_RANGES];
     __shared__ int cnt;
-    if (threadIdx.x == 0) {
-        int k = 0;
-        for (int r = 0; r < nranges; ++r) {
-            const int64_t s = ranges[2 * r], e = ranges[2 * r + 1];
-            if (s < c1 && e > c0 && k < ADAM_MAX_RANGES) {
-                lo[k] = s;
-                hi[k] = e;
-                ++k;
+    if (threadIdx.x == 0) cnt = 0;
+    __syncthreads();
+    for (int r = threadIdx.x; r < nranges; r += 256) {
+        const int64_t s = ranges[2 * r], e = ranges[2 * r + 1];
+        if (s < c1 && e > c0) {
+            const int slot = atomicAdd(&cnt, 1);
+            if (slot < ADAM_MAX_RANGES) {
+                lo[slot] = s;
+                hi[slot] = e;
             }
         }
-        cnt = k;
     }
     __syncthreads();
-    const int k = cnt;
+    const int k = min(cnt, ADAM_MAX_RANGES);
     const float one_b1 = __fsub_rn(1.0f, a.beta1), one_b2 = __fsub_rn(1.0f, a.beta2);
     const float decay = __fsub_rn(1.0f, __fmul_rn(a.lr, a.weight_decay));
-    for (int64_t i = c0 + threadIdx.x; i < c1; i += 256) {
+    auto update = [&](int64_t i, float grad, float x, float m0, float v0, float &mi, float &vi)
+        __attribute__((always_inline)) {
         bool rank1 = false;
         for (int r = 0; r < k; ++r) rank1 |= (i >= lo[r] && i < hi[r]);
-        float grad = g[i];
         if (clip) grad = __fmul_rn(grad, factor);
-        float x = w[i];
         if (!rank1) x = __fmul_rn(x, decay);
-        const float mi = __fadd_rn(__fmul_rn(a.beta1, m[i]), __fmul_rn(one_b1, grad));
-        const float vi =
-            __fadd_rn(__fmul_rn(a.beta2, v[i]), __fmul_rn(__fmul_rn(one_b2, grad), grad));
+        mi = __fadd_rn(__fmul_rn(a.beta1, m0), __fmul_rn(one_b1, grad));
+        vi = __fadd_rn(__fmul_rn(a.beta2, v0), __fmul_rn(__fmul_rn(one_b2, grad), grad));
         const float den = __fadd_rn(__fdiv_rn(__fsqrt_rn(vi), a.bias2_sqrt), a.eps);
-        x = __fsub_rn(x, __fdiv_rn(__fmul_rn(a.step_size, mi), den));
+        return __fsub_rn(x, __fdiv_rn(__fmul_rn(a.step_size, mi), den));
+    };
+    int64_t i0 = c0;
+    if (vec) {
+        // whole float4 groups of the chunk; chunks start at multiples of 4
+        const int64_t q1 = c0 + ((c1 - c0) & ~int64_t(3));
+#pragma unroll 4
+        for (int64_t i = c0 + 4 * threadIdx.x; i < q1; i += 4 * 256) {
+            const float4 g4 = *reinterpret_cast<const float4 *>(g + i);
+            const float4 w4 = *reinterpret_cast<const float4 *>(w + i);
+            const float4 m4 = *reinterpret_cast<const float4 *>(m + i);
+            const float4 v4 = *reinterpret_cast<const float4 *>(v + i);
+            float4 wo, mo, vo;
+            wo.x = update(i + 0, g4.x, w4.x, m4.x, v4.x, mo.x, vo.x);
+            wo.y = update(i + 1, g4.y, w4.y, m4.y, v4.y, mo.y, vo.y);
+            wo.z = update(i + 2, g4.z, w4.z, m4.z, v4.z, mo.z, vo.z);
+            wo.w = update(i + 3, g4.w, w4.w, m4.w, v4.w, mo.w, vo.w);
+            *reinterpret_cast<float4 *>(m + i) = mo;
+            *reinterpret_cast<float4 *>(v + i) = vo;
+            *reinterpret_cast<float4 *>(w + i) = wo;
+        }
+        i0 = q1;
+    }
+    for (int64_t i = i0 + threadIdx.x; i < c1; i += 256) {
+        float mi, vi;
+        const float x = update(i, g[i], w[i], m[i], v[i], mi, vi);
         m[i] = mi;
         v[i] = vi;
         w[i] = x;
@@ -636,8 +661,9 @@ void launch_adamw(Context &ctx, float *w, const float *g, float *m, float *v, in
         fail(MMH_ERR_ARGUMENT, "adamw: too many undecayed parameters in one chunk");
     const int64_t blocks = (n + ADAM_CHUNK - 1) / ADAM_CHUNK;
     if (blocks > 0x7fffffff) fail(MMH_ERR_SHAPE, "adamw: too many parameters");
+    const bool vec = al16(w) && al16(g) && al16(m) && al16(v);
     hipLaunchKernelGGL(adamw_kernel, dim3((unsigned)blocks), dim3(256), 0, ctx.stream, w, g, m,
-                       v, n, ranges_dev, nranges, a, loss_dev, norm_dev);
+                       v, n, ranges_dev, nranges, a, loss_dev, norm_dev, vec);
     check_hip(hipGetLastError(), "adamw launch");
 }
 
