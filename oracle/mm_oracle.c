@@ -68,19 +68,29 @@ double mmo_rng_next_f64(mmo_rng *r) {
     return (double)(mmo_rng_next_u64(r) >> 11) * (1.0 / 9007199254740992.0);
 }
 
+/* rng.rs:78-83: one Box-Muller pair from two consecutive draws, u1 = 1 -
+ * next_f64, u2 = next_f64; *c is the value returned, *s the cached spare. */
+static void box_muller(uint64_t x1, uint64_t x2, float *c, float *s) {
+    const double u1 = 1.0 - (double)(x1 >> 11) * (1.0 / 9007199254740992.0);
+    const double u2 = (double)(x2 >> 11) * (1.0 / 9007199254740992.0);
+    const double radius = sqrt(-2.0 * log(u1));
+    const double theta = 6.283185307179586 * u2; /* std::f64::consts::TAU */
+    *s = (float)(radius * sin(theta));
+    *c = (float)(radius * cos(theta));
+}
+
 /* rng.rs:74-84, Box-Muller with a cached spare that persists across calls. */
 float mmo_rng_normal(mmo_rng *r) {
     if (r->has_spare) {
         r->has_spare = 0;
         return r->spare;
     }
-    const double u1 = 1.0 - mmo_rng_next_f64(r);
-    const double u2 = mmo_rng_next_f64(r);
-    const double radius = sqrt(-2.0 * log(u1));
-    const double theta = 6.283185307179586 * u2; /* std::f64::consts::TAU */
-    r->spare = (float)(radius * sin(theta));
+    const uint64_t x1 = mmo_rng_next_u64(r);
+    const uint64_t x2 = mmo_rng_next_u64(r);
+    float c;
+    box_muller(x1, x2, &c, &r->spare);
     r->has_spare = 1;
-    return (float)(radius * cos(theta));
+    return c;
 }
 
 /* rng.rs:91-105, Lemire's nearly-divisionless method. */
@@ -176,13 +186,89 @@ int32_t mmo_preset(int32_t which, mmo_config *out) {
     return MMO_OK;
 }
 
+/* Splits [0, n) into nthreads contiguous ranges run on pthreads. */
+typedef void (*range_fn)(void *ctx, int64_t lo, int64_t hi);
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    int64_t lo, hi;
+} range_task;
+
+static void *range_thread(void *arg) {
+    range_task *t = (range_task *)arg;
+    if (t->lo < t->hi) t->fn(t->ctx, t->lo, t->hi);
+    return NULL;
+}
+
+static void parallel_for(int64_t n, int32_t nthreads, range_fn fn, void *ctx) {
+    if (nthreads <= 1 || n < 2) {
+        fn(ctx, 0, n);
+        return;
+    }
+    if (nthreads > 64) nthreads = 64;
+    if (nthreads > n) nthreads = (int32_t)n;
+    pthread_t th[64];
+    range_task tasks[64];
+    for (int32_t i = 0; i < nthreads; i++) {
+        tasks[i].fn = fn;
+        tasks[i].ctx = ctx;
+        tasks[i].lo = n * i / nthreads;
+        tasks[i].hi = n * (i + 1) / nthreads;
+    }
+    for (int32_t i = 1; i < nthreads; i++) pthread_create(&th[i], NULL, range_thread, &tasks[i]);
+    range_thread(&tasks[0]);
+    for (int32_t i = 1; i < nthreads; i++) pthread_join(th[i], NULL);
+}
+
 /* ------------------------------------------------------------------------ */
 /* Init: model.rs:51-83, init.rs:33-40, tensor.rs:158-162                    */
 /* ------------------------------------------------------------------------ */
 
 /* Tensor::randn: each value is std * normal() as an f32 product. */
-static void randn(float *dst, int64_t n, float std, mmo_rng *r) {
+static void randn_seq(float *dst, int64_t n, float std, mmo_rng *r) {
     for (int64_t i = 0; i < n; i++) dst[i] = std * mmo_rng_normal(r);
+}
+
+/* The same values with the transcendental work spread over threads: the
+ * draws are taken from the stream in order (a chunk at a time), and pair j of
+ * a chunk turns draws 2j, 2j+1 into values 2j, 2j+1, exactly what the
+ * sequential loop computes for them; a cached spare is used first and an odd
+ * last value comes from mmo_rng_normal, which caches its pair's spare. */
+typedef struct {
+    const uint64_t *draws;
+    float *out;
+    float std;
+} randn_chunk;
+
+static void randn_pairs(void *ctx, int64_t lo, int64_t hi) {
+    const randn_chunk *k = (const randn_chunk *)ctx;
+    for (int64_t j = lo; j < hi; j++) {
+        float c, s;
+        box_muller(k->draws[2 * j], k->draws[2 * j + 1], &c, &s);
+        k->out[2 * j] = k->std * c;
+        k->out[2 * j + 1] = k->std * s;
+    }
+}
+
+static int32_t g_init_threads = 1; /* set by mmo_init_weights_mt for its call */
+
+static void randn(float *dst, int64_t n, float std, mmo_rng *r) {
+    if (g_init_threads <= 1 || n < (1 << 16)) {
+        randn_seq(dst, n, std, r);
+        return;
+    }
+    int64_t i = 0;
+    if (r->has_spare) dst[i++] = std * mmo_rng_normal(r);
+    const int64_t pairs = (n - i) / 2, chunk = (int64_t)1 << 20;
+    uint64_t *draws = (uint64_t *)malloc((size_t)(pairs < chunk ? pairs : chunk) * 2 * 8 + 16);
+    for (int64_t base = 0; base < pairs; base += chunk) {
+        const int64_t cnt = pairs - base < chunk ? pairs - base : chunk;
+        for (int64_t j = 0; j < 2 * cnt; j++) draws[j] = mmo_rng_next_u64(r);
+        randn_chunk k = {draws, dst + i + 2 * base, std};
+        parallel_for(cnt, g_init_threads, randn_pairs, &k);
+    }
+    free(draws);
+    if ((n - i) & 1) dst[n - 1] = std * mmo_rng_normal(r);
 }
 
 void mmo_randn(mmo_rng *r, float *dst, int64_t n, float std) { randn(dst, n, std, r); }
@@ -221,6 +307,16 @@ int32_t mmo_init_weights(const mmo_config *c, float std, mmo_rng *r, float *w, i
     return (p - w == total) ? MMO_OK : MMO_ERR_SHAPE;
 }
 
+/* mmo_init_weights with the normals' arithmetic on nthreads threads: the same
+ * bits (the draw order is unchanged). Not reentrant across threads. */
+int32_t mmo_init_weights_mt(const mmo_config *c, float std, mmo_rng *r, float *w, int64_t n,
+                            int32_t nthreads) {
+    g_init_threads = nthreads;
+    const int32_t st = mmo_init_weights(c, std, r, w, n);
+    g_init_threads = 1;
+    return st;
+}
+
 /* lab.rs:194-203 */
 void mmo_lab_tokens(mmo_rng *r, int64_t vocab, int64_t batch, int64_t seq, int32_t *inputs,
                     int32_t *targets) {
@@ -236,39 +332,6 @@ void mmo_lab_tokens(mmo_rng *r, int64_t vocab, int64_t batch, int64_t seq, int32
 /* ------------------------------------------------------------------------ */
 /* Threads: split [0, n) into contiguous ranges                              */
 /* ------------------------------------------------------------------------ */
-
-typedef void (*range_fn)(void *ctx, int64_t lo, int64_t hi);
-typedef struct {
-    range_fn fn;
-    void *ctx;
-    int64_t lo, hi;
-} range_task;
-
-static void *range_thread(void *arg) {
-    range_task *t = (range_task *)arg;
-    if (t->lo < t->hi) t->fn(t->ctx, t->lo, t->hi);
-    return NULL;
-}
-
-static void parallel_for(int64_t n, int32_t nthreads, range_fn fn, void *ctx) {
-    if (nthreads <= 1 || n < 2) {
-        fn(ctx, 0, n);
-        return;
-    }
-    if (nthreads > 64) nthreads = 64;
-    if (nthreads > n) nthreads = (int32_t)n;
-    pthread_t th[64];
-    range_task tasks[64];
-    for (int32_t i = 0; i < nthreads; i++) {
-        tasks[i].fn = fn;
-        tasks[i].ctx = ctx;
-        tasks[i].lo = n * i / nthreads;
-        tasks[i].hi = n * (i + 1) / nthreads;
-    }
-    for (int32_t i = 1; i < nthreads; i++) pthread_create(&th[i], NULL, range_thread, &tasks[i]);
-    range_thread(&tasks[0]);
-    for (int32_t i = 1; i < nthreads; i++) pthread_join(th[i], NULL);
-}
 
 /* ------------------------------------------------------------------------ */
 /* GEMM: kernels.rs:49-108 (scalar) and kernels_avx.rs:177-204 (4x16 tile)   */

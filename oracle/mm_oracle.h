@@ -115,6 +115,10 @@ int32_t mmo_preset(int32_t which, mmo_config *out);
  *   o [d,d], mlp_norm [d], gate [d,ff], up [d,ff], down [ff,d];
  *   final_norm [d]; lm_head [d,V] only when untied. */
 int32_t mmo_init_weights(const mmo_config *c, float std, mmo_rng *r, float *w, int64_t n);
+/* The same weights with the Box-Muller arithmetic spread over nthreads
+ * threads (draws still taken in stream order): identical bits. */
+int32_t mmo_init_weights_mt(const mmo_config *c, float std, mmo_rng *r, float *w, int64_t n,
+                            int32_t nthreads);
 /* Lab::new token scheme (crates/midman-api/src/lab.rs:194-203). */
 void mmo_lab_tokens(mmo_rng *r, int64_t vocab, int64_t batch, int64_t seq,
                     int32_t *inputs, int32_t *targets);

@@ -84,6 +84,7 @@ def lib():
             "mmo_param_count": (_i64, [C]),
             "mmo_preset": (_i32, [_i32, C]),
             "mmo_init_weights": (_i32, [C, ctypes.c_float, R, _f32p, _i64]),
+            "mmo_init_weights_mt": (_i32, [C, ctypes.c_float, R, _f32p, _i64, _i32]),
             "mmo_lab_tokens": (None, [R, _i64, _i64, _i64, _i32p, _i32p]),
             "mmo_gemm_nn": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i32]),
             "mmo_gemm_nt": (None, [_f32p, _f32p, _f32p, _i64, _i64, _i64, _i32]),
@@ -198,10 +199,16 @@ def param_count(c):
     return lib().mmo_param_count(ctypes.byref(c))
 
 
-def init_weights(c, r, std=0.02):
+def init_weights(c, r, std=0.02, threads=None):
+    """MidManModel::with_init_std's draws (model.rs:51-83); threads > 1 spreads
+    the Box-Muller arithmetic over threads (same bits, tested)."""
     n = param_count(c)
     w = np.empty(n, np.float32)
-    st = lib().mmo_init_weights(ctypes.byref(c), std, ctypes.byref(r), fp(w), n)
+    threads = threads or default_threads()
+    if threads > 1:
+        st = lib().mmo_init_weights_mt(ctypes.byref(c), std, ctypes.byref(r), fp(w), n, threads)
+    else:
+        st = lib().mmo_init_weights(ctypes.byref(c), std, ctypes.byref(r), fp(w), n)
     if st != OK:
         raise ValueError(f"mmo_init_weights status {st}")
     return w
@@ -214,10 +221,10 @@ def lab_tokens(r, vocab, batch, seq):
     return inputs, targets
 
 
-def lab_setup(c, seed, batch, seq, std=0.02):
+def lab_setup(c, seed, batch, seq, std=0.02, threads=None):
     """Lab::new / overfit.rs memorize: weights then tokens from one stream."""
     r = rng(seed)
-    w = init_weights(c, r, std)
+    w = init_weights(c, r, std, threads)
     inputs, targets = lab_tokens(r, c.vocab_size, batch, seq)
     return w, inputs, targets
 

@@ -169,6 +169,45 @@ def test_untied_head_against_oracle(ctx):
     m.close()
 
 
+def test_large_preset_full_depth_against_oracle(ctx):
+    # The whole large preset (20 layers, d 2048, 16 heads of 128, 8 kv heads,
+    # ff 5632, V 32000; presets.rs:63-70) from Rng(0) against the oracle's
+    # forward (model.rs:103-183) at B1 T1024: every weight bit-exact, then the
+    # loss within 1e-4 and each row's logits within 1e-3 of the row's
+    # magnitude, so error growth over the 20 blocks is measured against the
+    # CPU path. The oracle runs on 16 host threads (its row split keeps every
+    # element's summation order).
+    import time
+    t0 = time.time()
+    cfg = mh.PRESETS["large"]
+    print("\n[model] large preset, 20 layers, B1 T1024 vs the oracle", flush=True)
+    m = mh.Model.new(ctx, cfg, 0)
+    try:
+        c = oracle_config(cfg)
+        w_ref, x_ref, y_ref = O.lab_setup(c, 0, 1, 1024, threads=16)
+        print(f"  init: device + oracle {time.time() - t0:.1f}s", flush=True)
+        w = m.weights()
+        assert w.size == 1_009_338_368
+        assert np.array_equal(w.view(np.uint32), w_ref.view(np.uint32))
+        del w
+        x, y = m.lab_tokens(1, 1024)
+        assert np.array_equal(x, x_ref) and np.array_equal(y, y_ref)
+        loss, logits = m.forward_loss(x, y, 1, 1024)
+        t1 = time.time()
+        ref_loss, ref_logits = O.forward_loss(c, w_ref, x, y, 1, 1024, threads=16)
+        print(f"  oracle forward {time.time() - t1:.1f}s; loss gpu {loss:.7f} oracle "
+              f"{ref_loss:.7f} (rel {abs(loss - ref_loss) / ref_loss:.2e})", flush=True)
+        assert abs(loss - ref_loss) / ref_loss <= 1e-4
+        check_logits(logits, ref_logits, "large preset logits, 20 layers")
+        # the loss-only forward (the head GEMM with the loss folded in)
+        folded = m.loss(x, y, 1, 1024)
+        assert abs(folded - ref_loss) / ref_loss <= 1e-4
+        assert abs(folded - loss) <= 2e-6 * loss
+        print(f"  total {time.time() - t0:.1f}s", flush=True)
+    finally:
+        m.close()
+
+
 def test_large_preset_full_size_invariants(ctx):
     # Full large preset at the benchmark shape B4 T1024: size-independent checks.
     print("\n[model] large preset B4 T1024 (init ~ a few seconds)", flush=True)
@@ -196,6 +235,18 @@ def test_large_preset_full_size_invariants(ctx):
     losses = [m.loss(x[i * 1024:(i + 1) * 1024], y[i * 1024:(i + 1) * 1024], 1, 1024)
               for i in range(4)]
     assert abs(np.mean(losses) - loss) / loss < 1e-5
+    # The benchmark's timed path at its shape: the loss-only forward (the loss
+    # folded into the head GEMM over 250 column tiles of 128, EPI_CE), eager
+    # (mmh_model_loss) and staged (run 1 eager, run 2 captured into a HIP
+    # graph, runs 3-4 replays), against the logits path's loss.
+    folded = m.loss(x, y, 4, 1024)
+    print(f"  loss-only forward {folded:.7f} vs logits path {loss:.7f}", flush=True)
+    assert abs(folded - loss) <= 2e-6 * loss
+    assert abs(folded - f64) <= 2e-6 * f64
+    m.stage(x, y, 4, 1024)
+    for i in range(4):
+        m.run_staged(4, 1024)
+        assert m.read_loss() == folded, i
     m.close()
 
 

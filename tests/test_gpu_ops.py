@@ -93,6 +93,7 @@ ATTN_CASES = [
     (8, 4, 4, 256, 32),
     (2, 16, 16, 100, 64),
     (1, 16, 8, 1024, 128),
+    (1, 16, 8, 2048, 128),  # the large preset's max_seq_len
     (2, 16, 8, 77, 128),
     (3, 6, 3, 1, 64),
     # odd counts of 128-row query blocks (the middle one has no partner)

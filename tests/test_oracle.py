@@ -118,6 +118,24 @@ def test_init_draw_order_and_scales():
         assert abs(s - want) / want < 0.1, (name, s, want)
 
 
+@pytest.mark.parametrize("cfg", [
+    # an untied head, a vocabulary and widths that are not powers of two, and
+    # (below) tensors past the 2^20-pair chunk
+    (257, 1118, 1, 13, 1, 301, 16, 10000.0, 1e-5, False),
+    (32000, 2048, 1, 16, 8, 5632, 16, 10000.0, 1e-5, True),
+])
+def test_threaded_init_equals_sequential(cfg):
+    c = O.config(*cfg)
+    seq = O.init_weights(c, O.rng(5), threads=1)
+    r = O.rng(5)
+    par = O.init_weights(c, r, threads=8)
+    assert np.array_equal(seq.view(np.uint32), par.view(np.uint32))
+    # the stream continues identically afterwards (spare included)
+    r1 = O.rng(5)
+    O.init_weights(c, r1, threads=1)
+    assert np.array_equal(O.normals(r1, 7), O.normals(r, 7))
+
+
 # ---- GEMM: ops_matmul.rs:137-156, the reference's own C twin, brute force -------
 
 def test_gemm_hand_calculation(goldens):
