@@ -110,6 +110,23 @@ int32_t mmh_gemm_nt(mmh_handle ctx, const float *a, const float *b, float *c, in
 /* kernels.rs:78 gemm_tn: C[m,n] (+)= A[k,m]^T B[k,n] */
 int32_t mmh_gemm_tn(mmh_handle ctx, const float *a, const float *b, float *c, int64_t m,
                     int64_t k, int64_t n, int32_t accumulate);
+/* mmh_gemm_nn / _nt / _tn (form MMH_GEMM_NN, _NT, _TN) without any device
+ * allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The same kernels and split choices as the
+ * three entry points above, so the same bits; the split-K partials live in a
+ * fixed 32 MiB device array per GPU instead of the context's workspace. A
+ * product whose partials need more (splits x m x n x 4 bytes; split-K is
+ * chosen only when the output tiles cannot fill the chip, and every product of
+ * the benchmark sweep fits) is refused with MMH_ERR_SHAPE before anything
+ * runs. The array is shared by every call on a
+ * GPU: calls that overlap on one GPU (other streams, contexts or threads) race
+ * on it. */
+#define MMH_GEMM_NN 0
+#define MMH_GEMM_NT 1
+#define MMH_GEMM_TN 2
+int32_t mmh_gemm_noalloc(mmh_handle ctx, int32_t form, const float *a, const float *b,
+                         float *c, int64_t m, int64_t k, int64_t n, int32_t accumulate);
 /* ops_matmul.rs:87-96, batched form: C[i] = A[i] B[i] for i < batch, each
  * [m,k] x [k,n], contiguous. */
 int32_t mmh_matmul_batched(mmh_handle ctx, const float *a, const float *b, float *c,

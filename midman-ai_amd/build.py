@@ -21,7 +21,7 @@ LIB = os.path.join(HERE, "libmidman_hip.so")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "rowops.hip", "attention.hip", "attention_bwd.hip",
-               "train.hip", "checkpoint.hip", "data.hip", "model.hip"]
+               "train.hip", "checkpoint.hip", "data.hip", "model.hip", "noalloc.hip"]
 HOST_SOURCES = ["host_math.cpp", "host_sha256.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

@@ -1322,7 +1322,20 @@ void gemm(Context &ctx, const GemmDesc &d) {
     p.k_per_split = kt_per * kstep;
     splits = (int)((ktiles + kt_per - 1) / kt_per);
     p.splits = splits;
-    if (splits > 1) p.partial = static_cast<float *>(ctx.get_scratch((size_t)splits * d.m * d.n * 4));
+    if (splits > 1) {
+        const size_t need_bytes = (size_t)splits * d.m * d.n * 4;
+        if (d.scratch) {
+            if (need_bytes > d.scratch_bytes)
+                fail(MMH_ERR_SHAPE, "gemm: the split-K partials of a " + std::to_string(d.m) +
+                                        " x " + std::to_string(d.n) + " product (" +
+                                        std::to_string(splits) + " splits) need " +
+                                        std::to_string(need_bytes) + " bytes; the scratch holds " +
+                                        std::to_string(d.scratch_bytes));
+            p.partial = d.scratch;
+        } else {
+            p.partial = static_cast<float *>(ctx.get_scratch(need_bytes));
+        }
+    }
 
     // RoPE in the small kernel's epilogue when a head fits 32 columns.
     const bool rope = d.rope_cos != nullptr;

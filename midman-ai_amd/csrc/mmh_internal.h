@@ -139,6 +139,11 @@ struct GemmDesc {
     // partials [m, gemm_ce_tiles, 2] and target logits [m] out.
     const int32_t *ce_targets = nullptr;
     float *ce_part = nullptr, *ce_zt = nullptr;
+    // Device memory for the split-K partials supplied by the caller (null: the
+    // context's growable workspace). gemm() fails with MMH_ERR_SHAPE when the
+    // partials of the split it chooses need more than scratch_bytes.
+    float *scratch = nullptr;
+    size_t scratch_bytes = 0;
 };
 
 void gemm(Context &ctx, const GemmDesc &d);

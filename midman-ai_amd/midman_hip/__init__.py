@@ -92,6 +92,7 @@ _SIGNATURES = {
     "mmh_gemm_nn": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
     "mmh_gemm_nt": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
     "mmh_gemm_tn": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
+    "mmh_gemm_noalloc": [_h, _i32, _vp, _vp, _vp, _i64, _i64, _i64, _i32],
     "mmh_matmul_batched": [_h, _vp, _vp, _vp, _i64, _i64, _i64, _i64],
     "mmh_matmul_backward": [_h, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64],
     "mmh_embedding": [_h, _vp, _i64, _i64, _i32p, _i64, _vp],
