@@ -229,6 +229,14 @@ int32_t mmh_model_forward_loss(mmh_handle model, const int32_t *inputs_host,
                                const int32_t *targets_host, int64_t batch, int64_t seq,
                                float *logits_host, float *loss_host);
 int32_t mmh_model_destroy(mmh_handle model);
+/* Diagnostic with no reference counterpart (the guard-band checks of
+ * kernels_avx.rs:368-390, on the device): the model's activation and training
+ * buffers are carved into slots separated by guard words of 0x7FC0DEAD, set
+ * when the buffers are allocated; this waits for queued work and counts the
+ * guard words that no longer hold that value (0 unless a kernel wrote outside
+ * its output: the logits, the loss partials of the head GEMM, the saved
+ * gate/up pairs, ...). */
+int32_t mmh_model_check_guards(mmh_handle model, uint64_t *broken_words);
 
 /* Device-resident steps (no reference counterpart: the reference has no
  * device; these split model.rs:174's loss into upload / run / read so a caller

@@ -83,6 +83,11 @@ struct KParams {
     // EPI_CE (128x128 kernel): targets in, per-tile (max, sum) pairs and target logits out
     const int32_t *ce_targets;
     float *ce_part, *ce_zt;
+    // The value the sums of products start from: +0 (a product, as the
+    // reference's fresh zeroed C), or -0 when the sum is added into C (the
+    // seam's accumulate: C's own value starts the reference's sum, so a -0 in
+    // C with all products -0 must stay -0; -0 is the identity of IEEE addition)
+    float acc_init;
 };
 
 // Row strides (floats) of the k-major LDS stages: even, so the 8-byte operand
@@ -177,8 +182,11 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     constexpr int NS = FAST ? SLOTS : 1;
     float4 ra[NS][NL], rb[NS][NL];
 
+    // Values outside [M, N, K) read as zeros; A's are -0, so a product of two
+    // of them is -0, the identity of IEEE addition (a +0 would turn an exact
+    // -0 sum into +0).
     auto load_a_edge = [&](int idx, int64_t k0) __attribute__((always_inline)) -> float4 {
-        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 v = make_float4(-0.f, -0.f, -0.f, -0.f);
         if (!TA) {
             const int64_t gm = m0 + idx / RQ, gk = k0 + (idx % RQ) * 4;
             if (gm < M) {
@@ -386,7 +394,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[j][r] = 0.0f;
+        for (int r = 0; r < 16; ++r) acc[j][r] = p.acc_init;
     const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
                       (kend - kbeg) % BK == 0;
     if (fast)
@@ -603,7 +611,8 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int idx = tid + 256 * i;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f), w = v;
+            // padding: A -0, B +0, so a padded product is -0 (see load_a_edge)
+            float4 v = make_float4(-0.f, -0.f, -0.f, -0.f), w = make_float4(0.f, 0.f, 0.f, 0.f);
             if (!TA) {
                 const int64_t gm = m0 + (idx >> 3), gk = k0 + (idx & 7) * 4;
                 const float *src = A + gm * p.lda + gk;
@@ -810,7 +819,7 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
 
     floatx16 acc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < 16; ++r) acc[r] = p.acc_init;
     // NORM: sums of squares of this thread's two A rows (the loads give
     // thread tid rows tid/8 and 32 + tid/8 at every K-step), gathered as the
     // values pass through the LDS stores.
@@ -934,7 +943,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
 
     floatx16 acc;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < 16; ++r) acc[r] = p.acc_init;
     float ss = 0.0f;
     for (int st = wave; st < nsteps; st += NW) {
         const int64_t kb = kbeg + (int64_t)st * 32 + 16 * lk;  // this lane's first k of the step
@@ -952,7 +961,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
         } else {
 #pragma unroll
             for (int j = 0; j < 16; ++j)
-                a[j] = (whole || kb + j < kend) ? arow[(kb + j) * (TA ? p.lda : 1)] : 0.0f;
+                a[j] = (whole || kb + j < kend) ? arow[(kb + j) * (TA ? p.lda : 1)] : -0.0f;
         }
         if (TB && whole) {
 #pragma unroll
@@ -1252,6 +1261,9 @@ void gemm(Context &ctx, const GemmDesc &d) {
     p.ce_targets = d.ce_targets;
     p.ce_part = d.ce_part;
     p.ce_zt = d.ce_zt;
+    if (d.accumulate_into_c && (d.epi != EPI_ACCUM || d.resid))
+        fail(MMH_ERR_ARGUMENT, "gemm: accumulate_into_c takes EPI_ACCUM into C itself");
+    p.acc_init = d.accumulate_into_c ? -0.0f : 0.0f;
     if (d.epi == EPI_SWIGLU_BWD || (d.epi == EPI_SWIGLU && d.aux)) {
         if (!d.aux || d.ldaux < (d.epi == EPI_SWIGLU ? d.n : 2 * d.n) || d.ldaux % 4 ||
             !aligned16(d.aux) ||

@@ -144,6 +144,11 @@ struct GemmDesc {
     // partials of the split it chooses need more than scratch_bytes.
     float *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // EPI_ACCUM with the GEMM seam's rule (kernels.rs:48, C += A.B): C's own
+    // value starts the sum. Without it EPI_ACCUM is a residual add of a fresh
+    // product (block.rs:79-80: x + matmul(..), the product summed from +0).
+    // The two differ only in the sign of an exact zero.
+    bool accumulate_into_c = false;
 };
 
 void gemm(Context &ctx, const GemmDesc &d);

@@ -218,6 +218,37 @@ void enqueue_block(Context &c, const BlockRun &r, Timed &&timed) {
     timed(MMH_PROF_GEMM_DOWN, [&] { gemm(c, dn); });
 }
 
+// Activation blocks are carved into slots with a guard band of kGuardFloats
+// words before the first slot, between slots and after the last, set to
+// kGuardBits when the block is allocated; mmh_model_check_guards counts the
+// words that no longer hold it (a kernel that wrote past its output).
+constexpr int64_t kGuardFloats = 64;
+constexpr uint32_t kGuardBits = 0x7FC0DEADu;
+
+// Allocates sum(sizes) floats plus the bands, writes each slot's base into
+// bases[i] and the bands' addresses into bands.
+float *alloc_guarded(Context &c, const int64_t *sizes, int nslots, float **bases,
+                     std::vector<float *> &bands, const char *what) {
+    int64_t total = (nslots + 1) * kGuardFloats;
+    for (int i = 0; i < nslots; ++i) total += sizes[i];
+    float *mem = nullptr;
+    check_hip(hipMalloc(&mem, (size_t)total * 4), what);
+    bands.clear();
+    float *p = mem;
+    for (int i = 0; i < nslots; ++i) {
+        bands.push_back(p);
+        p += kGuardFloats;
+        bases[i] = p;
+        p += sizes[i];
+    }
+    bands.push_back(p);
+    for (float *b : bands)
+        check_hip(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(b), (int)kGuardBits,
+                                    (size_t)kGuardFloats, c.stream),
+                  "guard fill");
+    return mem;
+}
+
 struct Model {
     mmh_handle ctx_handle = 0;
     Context *ctx = nullptr;
@@ -232,6 +263,7 @@ struct Model {
     // Activations for up to cap rows.
     int64_t cap = 0;
     float *act = nullptr;
+    std::vector<float *> act_bands, tr_bands;  // guard bands of act and tr.mem
     float *x = nullptr, *xn = nullptr, *qkv = nullptr, *cb = nullptr, *h = nullptr,
           *logits = nullptr, *row_loss = nullptr, *loss = nullptr, *ce_part = nullptr,
           *ce_zt = nullptr;
@@ -322,18 +354,12 @@ struct Model {
                                  al(n * d),     al(n * cfg.ff),    al(n * cfg.vocab),
                                  al(n),         64,                al(n * ce_tiles * 2),
                                  al(n),         al(n),             al(n)};
-        int64_t total = 0;
-        for (int64_t s : sizes) total += s;
-        check_hip(hipMalloc(&act, (size_t)total * 4), "activation alloc");
-        float *p = act;
+        float *base[12];
+        act = alloc_guarded(*ctx, sizes, 12, base, act_bands, "activation alloc");
         float **slots[] = {&x, &xn, &qkv, &cb, &h, &logits, &row_loss, &loss, &ce_part, &ce_zt};
-        for (int i = 0; i < 10; ++i) {
-            *slots[i] = p;
-            p += sizes[i];
-        }
-        ids = reinterpret_cast<int32_t *>(p);
-        p += sizes[10];
-        tgt = reinterpret_cast<int32_t *>(p);
+        for (int i = 0; i < 10; ++i) *slots[i] = base[i];
+        ids = reinterpret_cast<int32_t *>(base[10]);
+        tgt = reinterpret_cast<int32_t *>(base[11]);
         cap = n;
         staged_n = 0;
     }
@@ -573,25 +599,18 @@ struct Model {
             al(global_norm_scratch_bytes() / 4),  // norm_scratch (doubles)
             al(n), al(n + 1), al(n),        // uniq, start, order (int32)
         };
-        int64_t total = 0;
-        for (int64_t s : sizes) total += s;
-        check_hip(hipMalloc(&tr.mem, (size_t)total * 4), "training activation alloc");
-        float *p = tr.mem;
+        constexpr int nslots = (int)(sizeof(sizes) / sizeof(sizes[0]));
+        static_assert(nslots == 24, "training slots");
+        float *base[nslots];
+        tr.mem = alloc_guarded(*ctx, sizes, nslots, base, tr_bands, "training activation alloc");
         float **slots[] = {&tr.xs,   &tr.xn1, &tr.qkv,  &tr.cb,   &tr.lse,  &tr.hres, &tr.xn2,
                            &tr.gu,   &tr.h,   &tr.xnf,  &tr.dx,   &tr.dy,   &tr.dxn,  &tr.dctx,
                            &tr.dqkv, &tr.dvec, &tr.wtmp, &tr.rms, &tr.norm, &tr.apart};
-        int i = 0;
-        for (; i < 20; ++i) {
-            *slots[i] = p;
-            p += sizes[i];
-        }
-        tr.norm_scratch = reinterpret_cast<double *>(p);
-        p += sizes[i++];
-        tr.uniq = reinterpret_cast<int32_t *>(p);
-        p += sizes[i++];
-        tr.start = reinterpret_cast<int32_t *>(p);
-        p += sizes[i++];
-        tr.order = reinterpret_cast<int32_t *>(p);
+        for (int i = 0; i < 20; ++i) *slots[i] = base[i];
+        tr.norm_scratch = reinterpret_cast<double *>(base[20]);
+        tr.uniq = reinterpret_cast<int32_t *>(base[21]);
+        tr.start = reinterpret_cast<int32_t *>(base[22]);
+        tr.order = reinterpret_cast<int32_t *>(base[23]);
         tr.cap = n;
         staged_index = false;
     }
@@ -862,6 +881,21 @@ struct Model {
         launch_adamw(*ctx, w, grad, mom1, mom2, n_params, ranges, nranges, ranges_worst, a, loss,
                      tr.norm);
         repack();
+    }
+
+    // Guard words of the activation blocks that no longer hold kGuardBits.
+    uint64_t count_broken_guards() {
+        check_hip(hipStreamSynchronize(ctx->stream), "guard check sync");
+        uint64_t broken = 0;
+        std::vector<uint32_t> host((size_t)kGuardFloats);
+        for (const auto *bands : {&act_bands, &tr_bands})
+            for (float *b : *bands) {
+                check_hip(hipMemcpy(host.data(), b, (size_t)kGuardFloats * 4,
+                                    hipMemcpyDeviceToHost),
+                          "guard download");
+                for (uint32_t v : host) broken += v != kGuardBits;
+            }
+        return broken;
     }
 
     // Reads the loss and the norm; true when both are finite.
@@ -1521,6 +1555,16 @@ int32_t mmh_model_destroy(mmh_handle model_h) {
             m = std::move(g_models[(size_t)model_h - 1]);
         }
         m->release();
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_check_guards(mmh_handle model_h, uint64_t *broken_words) {
+    return guard([&] {
+        if (!broken_words) fail(MMH_ERR_ARGUMENT, "broken_words is a null pointer");
+        Model &m = model(model_h);
+        m.ctx->select();
+        *broken_words = m.count_broken_guards();
         return MMH_OK;
     });
 }

@@ -75,6 +75,7 @@ int32_t mmh_gemm_noalloc(mmh_handle ctx, int32_t form, const float *a, const flo
         d.ldb = tb ? k : n;
         d.ldc = n;
         d.epi = accumulate ? EPI_ACCUM : EPI_STORE;
+        d.accumulate_into_c = accumulate != 0;
         d.scratch = scratch_of(cx);
         d.scratch_bytes = kScratchBytes;
         gemm(cx, d);

@@ -298,6 +298,7 @@ static int32_t gemm_entry(mmh_handle ctx, const float *a, const float *b, float 
         d.ldb = tb ? k : n;
         d.ldc = n;
         d.epi = accumulate ? EPI_ACCUM : EPI_STORE;
+        d.accumulate_into_c = accumulate != 0;
         gemm(cx, d);
         return MMH_OK;
     });

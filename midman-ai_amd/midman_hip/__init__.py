@@ -116,6 +116,7 @@ _SIGNATURES = {
     "mmh_model_loss": [_h, _i32p, _i32p, _i64, _i64, _f32p],
     "mmh_model_forward_loss": [_h, _i32p, _i32p, _i64, _i64, _f32p, _f32p],
     "mmh_model_destroy": [_h],
+    "mmh_model_check_guards": [_h, ctypes.POINTER(ctypes.c_uint64)],
     "mmh_model_stage": [_h, _i32p, _i32p, _i64, _i64],
     "mmh_model_run_staged": [_h, _i64, _i64],
     "mmh_model_read_loss": [_h, _f32p],
@@ -1127,6 +1128,14 @@ class Model:
         check(lib().mmh_model_evaluate(self.handle, data.handle, batch_size, max_batches,
                                        ctypes.byref(loss), ctypes.byref(nb), ctypes.byref(nt)))
         return loss.value, nb.value, nt.value
+
+    def broken_guards(self) -> int:
+        """Guard words around the model's activation slots that a kernel
+        overwrote (mmh_model_check_guards); 0 when every write stayed inside
+        its output."""
+        n = ctypes.c_uint64()
+        check(lib().mmh_model_check_guards(self.handle, ctypes.byref(n)))
+        return n.value
 
     def close(self):
         if self.handle:

@@ -104,6 +104,106 @@ def test_ragged_shapes_and_accumulate(ctx, m, k, n, form):
         x.free()
 
 
+GUARD = 0x7FC0DEAD  # the reference's guard value (kernels_avx.rs:374)
+MIN_POSITIVE = np.float32(1.17549435e-38)
+
+# Shapes that route the seam to each kernel path (gemm.hip's dispatch on a
+# 256-CU MI355X): the 128x128 kernel with interior and edge tiles; the 64x64
+# kernel with a partial K step; the 32x32 K-split kernel in one workgroup
+# (nn; nt and tn of this shape split K across two workgroups); the K-split
+# kernel split across workgroups plus splitk_reduce; the 128x128 kernel split
+# along K plus splitk_reduce.
+SPECIAL_PATHS = [
+    ("128x128 tiles, interior and edges", 1100, 48, 4100),
+    ("64x64 tiles, partial K step", 2048, 500, 1024),
+    ("32x32 K-split tiles", 2048, 344, 128),
+    ("32x32 K-split over 8 workgroups + reduce", 256, 2048, 256),
+    ("128x128 split 8 ways along K + reduce", 1024, 8192, 1024),
+]
+
+
+def special_operands(m, k, n, seed):
+    """Integer-valued A [m,k], B [k,n], C0 [m,n] (every sum exact in f32, so
+    the result does not depend on the summation order) with special values
+    planted: the reference's case a=[0,-0,inf,1,NaN,-2] x b=[-0,0,3,-inf,1,
+    MIN_POSITIVE] (kernels_avx.rs:355-357) in the last two rows, the last
+    three k and the last two columns (edge tiles, the K tail); a row of -0
+    against a positive column (the sum is -0: +0 stored, C's -0 kept when
+    accumulating); a row of subnormal and MIN_POSITIVE multiples; C0 with
+    -0, inf and NaN."""
+    r = np.random.default_rng(seed)
+    a = r.integers(-3, 4, (m, k)).astype(np.float32)
+    b = r.integers(-3, 4, (k, n)).astype(np.float32)
+    c0 = r.integers(-5, 6, (m, n)).astype(np.float32)
+    i0, p0, j0 = m - 2, k - 3, n - 2
+    a[i0:i0 + 2, :] = 0.0
+    b[:, j0:j0 + 2] = 0.0
+    a[i0:i0 + 2, p0:p0 + 3] = np.array([0.0, -0.0, np.inf, 1.0, np.nan, -2.0],
+                                       np.float32).reshape(2, 3)
+    b[p0:p0 + 3, j0:j0 + 2] = np.array([-0.0, 0.0, 3.0, -np.inf, 1.0, MIN_POSITIVE],
+                                       np.float32).reshape(3, 2)
+    # a row of -0 and a column of positives: every product -0
+    i1, j1 = m // 2, 1
+    a[i1, :] = -0.0
+    b[:, j1] = r.integers(1, 4, k).astype(np.float32)
+    c0[i1, j1] = -0.0
+    c0[i1, j1 + 1] = 0.0
+    # tiny values only (no integer to absorb them): subnormal and MIN_POSITIVE
+    # multiples, exact in f32 in any order
+    i2 = 3
+    a[i2, :] = 0.0
+    a[i2, 0] = MIN_POSITIVE / np.float32(4)   # subnormal operand
+    a[i2, k // 2] = MIN_POSITIVE
+    c0[0, 0], c0[0, 1], c0[0, 2] = -0.0, np.inf, np.nan
+    return a, b, c0
+
+
+def same_bits(got, want):
+    g, w = got.view(np.uint32), want.view(np.uint32)
+    return (g == w) | (np.isnan(got) & np.isnan(want))
+
+
+@pytest.mark.parametrize("path,m,k,n", SPECIAL_PATHS, ids=[p[0] for p in SPECIAL_PATHS])
+@pytest.mark.parametrize("form", ["nn", "nt", "tn"])
+def test_special_values_and_guard_bands_on_every_kernel_path(ctx, path, m, k, n, form):
+    # kernels_avx.rs:351-366: special values follow the scalar rules bit for
+    # bit (NaN matches NaN); :368-390: C written between guard values that
+    # must survive. C sits at a 256-byte offset (vector stores) and at a
+    # 4-byte one (element stores) inside a buffer of guards.
+    print(f"\n[gemm special] {path}: {form} m={m} k={k} n={n}", flush=True)
+    a, b, c0 = special_operands(m, k, n, m + k + n)
+    aa = a if form != "tn" else np.ascontiguousarray(a.T)
+    bb = b if form != "nt" else np.ascontiguousarray(b.T)
+    A, B = ctx.to_device(aa), ctx.to_device(bb)
+    G = 64
+    buf = ctx.empty((m * n + 2 * G + 1,))
+    with np.errstate(invalid="ignore"):
+        want_store = O.gemm(form, aa, bb, m, k, n, threads=16)
+        want_acc = O.gemm(form, aa, bb, m, k, n, c=c0, threads=16)
+    nonfinite = int(np.sum(~np.isfinite(want_acc)))
+    negzero = int(np.sum((want_acc == 0) & np.signbit(want_acc)))
+    print(f"  reference: {nonfinite} non-finite, {negzero} -0 in the accumulated result",
+          flush=True)
+    assert nonfinite > 0 and negzero > 0
+    for off in (G, G + 1):
+        for accumulate, want in ((False, want_store), (True, want_acc)):
+            host = np.full(buf.size, 0, np.uint32) + GUARD
+            host = host.view(np.float32)
+            host[off:off + m * n] = c0.ravel()
+            buf.upload(host)
+            mh.gemm(ctx, form, A, B, buf.offset(off), m, k, n, accumulate=accumulate)
+            out = buf.numpy()
+            got = out[off:off + m * n].reshape(m, n)
+            ok = same_bits(got, want)
+            bad = np.argwhere(~ok)
+            assert ok.all(), (off, accumulate, bad[:5].tolist(),
+                              [(float(got[i, j]), float(want[i, j])) for i, j in bad[:5]])
+            guards = np.concatenate([out[:off], out[off + m * n:]]).view(np.uint32)
+            assert np.all(guards == GUARD), (off, accumulate, "a guard value was overwritten")
+    for x in (A, B, buf):
+        x.free()
+
+
 def test_special_values_propagate(ctx):
     # NaN and inf in A reach exactly the rows they touch (kernels_avx.rs:351-366).
     rng = np.random.default_rng(11)

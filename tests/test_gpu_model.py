@@ -155,6 +155,39 @@ def test_loss_folded_into_the_head_gemm(ctx, cfg, batch, seq):
         m.close()
 
 
+@pytest.mark.parametrize("cfg,batch,seq", [
+    # the head GEMM on the 128x128 kernel with the loss folded in (EPI_CE
+    # partials; V 3000 ends in a partial column tile); ff 96 pads the packed
+    # gate/up pairs to 128 columns
+    ([3000, 64, 1, 4, 2, 96, 1024, 10000.0, 1e-5, 1], 2, 1024),
+    # ragged rows, untied head, small tiles and the folded norm/rotation
+    ([97, 128, 2, 4, 2, 96, 96, 10000.0, 1e-5, 0], 3, 37),
+])
+def test_model_buffers_keep_their_guard_bands(ctx, cfg, batch, seq):
+    # Every activation slot of the forward and of the training step is fenced
+    # by guard words (kernels_avx.rs:368-390): the loss-only forward (head
+    # partials), the logits forward, and a training step (saved gate/up pairs,
+    # their gradients in place, the packed weight-gradient tile) leave every
+    # guard word intact.
+    print(f"\n[guards] model {cfg[:7]} B{batch} T{seq}", flush=True)
+    c = oracle_config(cfg)
+    w = O.init_weights(c, O.rng(31), std=0.1)
+    r = np.random.default_rng(seq)
+    x = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    y = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    m = mh.Model.from_weights(ctx, cfg, w)
+    try:
+        m.loss(x, y, batch, seq)
+        m.forward_loss(x, y, batch, seq)
+        assert m.broken_guards() == 0
+        m.set_optimizer(0.9, 0.99, 1e-8, 0.01, 1.0)
+        m.train_step(x, y, batch, seq, 1e-3)
+        m.loss(x, y, batch, seq)
+        assert m.broken_guards() == 0
+    finally:
+        m.close()
+
+
 def test_untied_head_against_oracle(ctx):
     cfg = [13, 16, 2, 4, 2, 24, 8, 10000.0, 1e-5, 0]
     c = oracle_config(cfg)

@@ -268,3 +268,82 @@ def test_mfma_peak_probe_is_a_plausible_ceiling(ctx):
     tf = ctx.mfma_peak_tflops()
     print(f"\n  fp32 MFMA probe: {tf:.1f} TFLOP/s", flush=True)
     assert 50.0 < tf <= 157.3 * 1.02
+
+
+# ---- outputs stay inside their buffers (kernels_avx.rs:368-390 on the device) ----
+
+GUARD = 0x7FC0DEAD
+G = 64
+
+
+class Fenced:
+    """A device buffer of n floats at a given word offset inside a larger one
+    filled with the guard value."""
+
+    def __init__(self, ctx, n, off, init=None):
+        self.n, self.off = n, off
+        self.buf = ctx.empty((n + off + G,))
+        host = (np.zeros(self.buf.size, np.uint32) + GUARD).view(np.float32)
+        if init is not None:
+            host[off:off + n] = np.asarray(init, np.float32).ravel()
+        self.buf.upload(host)
+        self.ptr = self.buf.offset(off)
+
+    def check(self, what):
+        out = self.buf.numpy()
+        guards = np.concatenate([out[:self.off], out[self.off + self.n:]]).view(np.uint32)
+        assert np.all(guards == GUARD), f"{what}: a guard word was overwritten"
+        return out[self.off:self.off + self.n]
+
+
+@pytest.mark.parametrize("off", [G, G + 1])
+def test_op_outputs_stay_inside_their_buffers(ctx, off):
+    print(f"\n[guards] op outputs at word offset {off}", flush=True)
+    L = mh.lib()
+    # rms_norm rows: the vector path (d % 4 == 0) and the generic one
+    for rows, d in ((33, 2048), (7, 1023), (5, 64)):
+        x = O.randn((rows, d), 1.0, O.rng(d))
+        w = O.randn((d,), 1.0, O.rng(d + 1))
+        X, W = ctx.to_device(x), ctx.to_device(w)
+        out = Fenced(ctx, rows * d, off)
+        mh.check(L.mmh_rms_norm(ctx.handle, X.ptr, W.ptr, rows, d, 1e-5, out.ptr))
+        got = out.check(f"rms_norm {rows}x{d}").reshape(rows, d)
+        np.testing.assert_allclose(got, O.rms_norm(x, w, 1e-5), rtol=4e-6, atol=0)
+    # embedding rows: float4 rows and an odd width
+    for V, d, n in ((300, 48, 257), (10, 7, 9)):
+        table = O.randn((V, d), 0.02, O.rng(V))
+        ids = np.random.default_rng(V).integers(0, V, n).astype(np.int32)
+        T = ctx.to_device(table)
+        out = Fenced(ctx, n * d, off)
+        mh.check(L.mmh_embedding(ctx.handle, T.ptr, V, d, mh._ip(ids), n, out.ptr))
+        assert np.array_equal(out.check(f"embedding {V}x{d}").reshape(n, d), table[ids])
+    # attention output: each kernel (paired 128-row blocks at hd 128 and 64,
+    # the key-split kernel at hd 32), ragged T
+    for B, H, Hkv, T, hd in ((1, 4, 2, 300, 128), (2, 4, 4, 77, 64), (4, 4, 4, 130, 32),
+                             (2, 2, 1, 12, 8)):
+        r = O.rng(B * 100 + T)
+        q = O.randn((B, H, T, hd), 1.0, r)
+        k = O.randn((B, Hkv, T, hd), 1.0, r)
+        v = O.randn((B, Hkv, T, hd), 1.0, r)
+        Q, K, Vd = ctx.to_device(q), ctx.to_device(k), ctx.to_device(v)
+        out = Fenced(ctx, B * H * T * hd, off)
+        mh.check(L.mmh_causal_attention(ctx.handle, Q.ptr, K.ptr, Vd.ptr, B, H, Hkv, T, hd,
+                                        out.ptr))
+        got = out.check(f"attention B{B} H{H} T{T} hd{hd}").reshape(B, H, T, hd)
+        want = O.causal_attention(q, k, v)
+        assert np.all(np.abs(got - want) <= 2e-5 * np.max(np.abs(v)) + 1e-5 * np.abs(want))
+    # apply_rope and add
+    tabs = mh.RotaryTables(ctx, 64, 40, 10000.0)
+    cos, sin = O.rope_tables(64, 40, 10000.0)
+    # (device buffers are held in names: a temporary's memory is freed and
+    # reused by the next allocation)
+    x = O.randn((3, 40, 64), 1.0, O.rng(9))
+    X = ctx.to_device(x)
+    out = Fenced(ctx, x.size, off)
+    mh.check(L.mmh_apply_rope(ctx.handle, X.ptr, 3, 40, 64, tabs.cos.ptr, tabs.sin.ptr, out.ptr))
+    assert np.array_equal(out.check("apply_rope").reshape(x.shape), O.apply_rope(x, cos, sin))
+    a, b = O.randn((1001,), 1.0, O.rng(1)), O.randn((1001,), 1.0, O.rng(2))
+    A, B = ctx.to_device(a), ctx.to_device(b)
+    out = Fenced(ctx, 1001, off)
+    mh.check(L.mmh_add(ctx.handle, A.ptr, B.ptr, out.ptr, 1001))
+    assert np.array_equal(out.check("add"), a + b)
