@@ -1,8 +1,9 @@
 """Builds libmidman_hip.so for gfx950 in-tree (midman-ai_amd/libmidman_hip.so).
 
-HIP sources are compiled with hipcc for gfx950 only; the host-side file that
-must match the reference bit for bit (RNG, randn, rotary tables) is compiled
-with g++ -ffp-contract=off. Objects go to midman-ai_amd/_build/.
+HIP sources are compiled with hipcc for gfx950 only; the host-only sources
+(error handling, the RNG and rotary tables that must match the reference bit
+for bit, SHA-256, the safetensors format, token shards and the batcher) are
+compiled with g++ -ffp-contract=off. Objects go to midman-ai_amd/_build/.
 
     python midman-ai_amd/build.py [--jobs N]
 """
@@ -21,8 +22,10 @@ LIB = os.path.join(HERE, "libmidman_hip.so")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "rowops.hip", "attention.hip", "attention_bwd.hip",
-               "train.hip", "checkpoint.hip", "data.hip", "model.hip", "noalloc.hip"]
-HOST_SOURCES = ["host_math.cpp", "host_sha256.cpp"]
+               "train.hip", "checkpoint.hip", "model.hip", "noalloc.hip"]
+# Host code with no HIP in it (also built with the sanitizers: build_sanitized.py)
+HOST_SOURCES = ["host_errors.cpp", "host_math.cpp", "host_sha256.cpp", "host_safetensors.cpp",
+                "host_data.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 HIP_FLAGS = [

@@ -12,7 +12,8 @@
 #include <mutex>
 
 #include "mmh_data.h"
-#include "mmh_internal.h"
+#include "mmh_error.h"
+#include "mmh_host.h"
 
 namespace mmh {
 

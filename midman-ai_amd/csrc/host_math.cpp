@@ -1,6 +1,7 @@
 // Host-side arithmetic that must match the reference bit for bit: the seeded
-// RNG (midman-foundation/src/rng.rs), Tensor::randn (tensor.rs:158-162) and
-// the rotary tables (midman-nn/src/rope.rs:71-79).
+// RNG (midman-foundation/src/rng.rs), Tensor::randn (tensor.rs:158-162), the
+// rotary tables (midman-nn/src/rope.rs:71-79) and the warmup-cosine learning
+// rate (midman-optim/src/schedule.rs:25-66).
 //
 // Built with g++ -ffp-contract=off and glibc's libm, the toolchain the
 // reference's Rust path matches on x86-64 (no FMA contraction; log, sqrt, sin,
@@ -12,6 +13,7 @@
 #include <thread>
 #include <vector>
 
+#include "mmh_error.h"
 #include "mmh_host.h"
 
 namespace mmh {
@@ -153,3 +155,33 @@ void rope_tables_host(int64_t head_dim, int64_t max_seq_len, float theta, float 
 }
 
 }  // namespace mmh
+
+extern "C" {
+
+int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
+                             uint64_t total_steps, uint64_t step, float *lr_out) {
+    return mmh::guard([&] {
+        if (!lr_out) mmh::fail(MMH_ERR_ARGUMENT, "lr is a null pointer");
+        // schedule.rs:25-48
+        if (!(std::isfinite(max_lr) && max_lr > 0.0f))
+            mmh::fail(MMH_ERR_ARGUMENT, "schedule: max_lr must be positive and finite");
+        if (!(std::isfinite(min_lr) && min_lr >= 0.0f && min_lr <= max_lr))
+            mmh::fail(MMH_ERR_ARGUMENT, "schedule: min_lr must be in [0, max_lr]");
+        if (warmup_steps >= total_steps)
+            mmh::fail(MMH_ERR_ARGUMENT, "schedule: warmup_steps must be below total_steps");
+        // schedule.rs:54-66
+        const double mx = (double)max_lr, mn = (double)min_lr;
+        if (step < warmup_steps) {
+            *lr_out = (float)(mx * (double)(step + 1) / (double)warmup_steps);
+        } else if (step >= total_steps) {
+            *lr_out = min_lr;
+        } else {
+            const double progress =
+                (double)(step - warmup_steps) / (double)(total_steps - warmup_steps);
+            *lr_out = (float)(mn + 0.5 * (mx - mn) * (1.0 + std::cos(M_PI * progress)));
+        }
+        return MMH_OK;
+    });
+}
+
+}  // extern "C"

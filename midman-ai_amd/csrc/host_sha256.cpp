@@ -188,6 +188,7 @@ Sha256::Sha256() {
 }
 
 void Sha256::update(const uint8_t *p, size_t n) {
+    if (n == 0) return;  // p may be null for an empty piece
     total += n;
     if (nbuf) {
         const size_t take = n < 64 - nbuf ? n : 64 - nbuf;
@@ -204,7 +205,7 @@ void Sha256::update(const uint8_t *p, size_t n) {
         p += n / 64 * 64;
         n %= 64;
     }
-    std::memcpy(buf, p, n);
+    if (n) std::memcpy(buf, p, n);
     nbuf = n;
 }
 

@@ -1,13 +1,20 @@
-// Safetensors headers and model checkpoints (checkpoint.hip).
+// Safetensors headers and model checkpoints: the format on the host
+// (host_safetensors.cpp) and the streaming between files and HBM
+// (checkpoint.hip). Host-only declarations.
 #pragma once
 
+#include <unistd.h>
+
+#include <cstdint>
 #include <map>
 #include <string>
 #include <vector>
 
-#include "mmh_internal.h"
+#include "mmh_error.h"
 
 namespace mmh {
+
+struct Context;
 namespace st {
 
 // A parsed header value: the restricted JSON of a safetensors header.
@@ -55,6 +62,19 @@ struct ParamSpec {
     std::vector<uint64_t> shape;
     int64_t offset;
     int64_t numel;
+};
+
+// File I/O that fails with MMH_ERR_OTHER and the path and errno text.
+std::string io_error(const std::string &path, const std::string &what);
+void write_all(int fd, const void *p, size_t n, const std::string &path);
+// n bytes at offset off (pread); a short file is an error.
+void read_all(int fd, void *p, size_t n, uint64_t off, const std::string &path);
+// A file descriptor closed when it goes out of scope.
+struct Fd {
+    int fd = -1;
+    ~Fd() {
+        if (fd >= 0) ::close(fd);
+    }
 };
 
 std::vector<ParamSpec> model_param_specs(int64_t vocab, int64_t d, int64_t layers, int64_t kv,

@@ -10,6 +10,7 @@
 #include <vector>
 
 #include "../../include/midman_hip.h"
+#include "mmh_error.h"
 #include "mmh_host.h"
 
 namespace mmh {
@@ -48,13 +49,6 @@ __device__ __forceinline__ void lse_merge(float &m, float &s, float m2, float s2
     }
 }
 
-// An error that the C-ABI boundary turns into a status code + message.
-struct Error {
-    int32_t status;
-    std::string message;
-};
-
-[[noreturn]] void fail(int32_t status, const std::string &message);
 void check_hip(hipError_t e, const char *what);
 
 // One device + one stream + growable workspaces.
@@ -81,13 +75,6 @@ struct Context {
 
 Context &context(mmh_handle h);
 
-// Runs an entry point body: an Error becomes its status and the thread's
-// error message; any other exception becomes MMH_ERR_PANIC.
-int32_t guard_impl(const std::function<int32_t()> &body);
-template <class F>
-int32_t guard(F &&f) {
-    return guard_impl(std::function<int32_t()>(std::forward<F>(f)));
-}
 // Host-side id validation (ops_shape.rs:250-252, ops_reduce.rs:250-252).
 void check_ids(const int32_t *ids, int64_t n, int64_t vocab, const char *what);
 // Destroys the models created on a context (model.hip).

@@ -1379,32 +1379,6 @@ int32_t mmh_model_optimizer_steps(mmh_handle model_h, uint64_t *out) {
     });
 }
 
-int32_t mmh_warmup_cosine_lr(float max_lr, float min_lr, uint64_t warmup_steps,
-                             uint64_t total_steps, uint64_t step, float *lr_out) {
-    return guard([&] {
-        if (!lr_out) fail(MMH_ERR_ARGUMENT, "lr is a null pointer");
-        // schedule.rs:25-48
-        if (!(std::isfinite(max_lr) && max_lr > 0.0f))
-            fail(MMH_ERR_ARGUMENT, "schedule: max_lr must be positive and finite");
-        if (!(std::isfinite(min_lr) && min_lr >= 0.0f && min_lr <= max_lr))
-            fail(MMH_ERR_ARGUMENT, "schedule: min_lr must be in [0, max_lr]");
-        if (warmup_steps >= total_steps)
-            fail(MMH_ERR_ARGUMENT, "schedule: warmup_steps must be below total_steps");
-        // schedule.rs:54-66
-        const double mx = (double)max_lr, mn = (double)min_lr;
-        if (step < warmup_steps) {
-            *lr_out = (float)(mx * (double)(step + 1) / (double)warmup_steps);
-        } else if (step >= total_steps) {
-            *lr_out = min_lr;
-        } else {
-            const double progress =
-                (double)(step - warmup_steps) / (double)(total_steps - warmup_steps);
-            *lr_out = (float)(mn + 0.5 * (mx - mn) * (1.0 + std::cos(M_PI * progress)));
-        }
-        return MMH_OK;
-    });
-}
-
 // ---- checkpoints (midman-checkpoint params.rs) ----------------------------------
 
 namespace {

@@ -1,6 +1,6 @@
-// The C ABI of libmidman_hip.so: status codes and error buffer, handle tables,
-// contexts (one device + one stream), device buffers, timers and the op-level
-// entry points. Boundary rules follow midman-api/src/ffi.rs:5-32, 99-145:
+// The C ABI of libmidman_hip.so: handle tables, contexts (one device + one
+// stream), device buffers, timers and the op-level entry points (the status
+// codes and the error buffer are host_errors.cpp). Boundary rules follow midman-api/src/ffi.rs:5-32, 99-145:
 // handles not pointers, status codes, the last error message per thread, and
 // nothing unwinds across the boundary (every entry point catches everything).
 #include <cmath>
@@ -13,37 +13,13 @@
 namespace mmh {
 
 namespace {
-thread_local std::string g_error;
 std::mutex g_mutex;
 std::vector<std::unique_ptr<Context>> g_contexts;  // handle = index + 1
 }  // namespace
 
-void fail(int32_t status, const std::string &message) { throw Error{status, message}; }
-
 void check_hip(hipError_t e, const char *what) {
     if (e != hipSuccess)
         fail(MMH_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
-}
-
-void set_error(const std::string &m) { g_error = m; }
-
-int32_t guard_impl(const std::function<int32_t()> &body) {
-    g_error.clear();
-    try {
-        return body();
-    } catch (const Error &e) {
-        g_error = e.message;
-        return e.status;
-    } catch (const std::bad_alloc &) {
-        g_error = "out of host memory";
-        return MMH_ERR_OTHER;
-    } catch (const std::exception &e) {
-        g_error = std::string("internal error: ") + e.what();
-        return MMH_ERR_PANIC;
-    } catch (...) {
-        g_error = "internal error: unknown exception";
-        return MMH_ERR_PANIC;
-    }
 }
 
 void *Context::get_scratch(size_t bytes) { return workspace(0, bytes); }
@@ -112,10 +88,6 @@ void positive(int64_t v, const char *what) {
 }  // namespace
 
 extern "C" {
-
-uint32_t mmh_abi_version(void) { return MMH_ABI_VERSION; }
-const char *mmh_error_ptr(void) { return g_error.c_str(); }
-uint32_t mmh_error_len(void) { return (uint32_t)g_error.size(); }
 
 int32_t mmh_context_create(int32_t device, mmh_handle *out_ctx) {
     return guard([&] {

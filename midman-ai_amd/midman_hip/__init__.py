@@ -20,7 +20,9 @@ from typing import Optional, Sequence
 import numpy as np
 
 _PKG_DIR = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-LIB_PATH = os.path.join(_PKG_DIR, "libmidman_hip.so")
+# MMH_LIB_PATH selects another build of the library (the host-only sanitizer
+# build, midman-ai_amd/build_sanitized.py, which has no device entry points).
+LIB_PATH = os.environ.get("MMH_LIB_PATH") or os.path.join(_PKG_DIR, "libmidman_hip.so")
 HEADER_PATH = os.path.join(os.path.dirname(_PKG_DIR), "include", "midman_hip.h")
 
 OK, STOPPED = 0, 1
@@ -211,7 +213,9 @@ def lib():
                 "there is no CPU fallback")
         L = ctypes.CDLL(LIB_PATH)
         for name, args in _SIGNATURES.items():
-            fn = getattr(L, name)
+            fn = getattr(L, name, None)
+            if fn is None:  # only a host-only build lacks symbols; calling one raises
+                continue
             fn.argtypes = args
             fn.restype = _RESTYPES.get(name, _i32)
         _lib = L

@@ -13,7 +13,8 @@ import os
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libmm_oracle.so")
+# MM_ORACLE_LIB selects another build of the same source (the sanitizer build).
+_LIB_PATH = os.environ.get("MM_ORACLE_LIB") or os.path.join(_HERE, "libmm_oracle.so")
 _REF_PATH = os.path.join(_HERE, "_ref", "libmmb_ref.so")
 
 _f32p = ctypes.POINTER(ctypes.c_float)
