@@ -344,7 +344,26 @@ def time_bandwidth(mh, ctx, reps=20):
     return out
 
 
-def cpu_baseline_large():
+def host_cpu():
+    """The host CPU's model name (/proc/cpuinfo) and the cores this process
+    may run on (its affinity mask; nproc counts the same)."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return name, n
+
+
+def cpu_baseline_large(cpu_model, nproc):
     """The oracle (a C restatement of the reference CPU path: 4x16 AVX tile,
     separate multiply and add, glibc libm) on ONE host core, on a bounded
     sample of the large workload: one decoder block at B1 T1024, the final
@@ -379,10 +398,10 @@ def cpu_baseline_large():
             "sample": (f"oracle single-thread AVX restatement: 1 large-preset decoder block at "
                        f"B1 T1024 ({t_block:.1f}s) + final norm + tied head + CE ({t_head:.1f}s), "
                        f"extrapolated to 20 blocks"),
-            "loss_sanity": loss}
+            "host_cpu": cpu_model, "nproc": nproc, "loss_sanity": loss}
 
 
-def cpu_baseline_tiny():
+def cpu_baseline_tiny(cpu_model, nproc):
     import mm_oracle as O
 
     c = O.preset("tiny")
@@ -394,7 +413,8 @@ def cpu_baseline_tiny():
         runs += 1
     dt = (time.perf_counter() - t0) / runs
     return {"value": round(2048 / dt, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": f"oracle single-thread, full tiny forward+loss B8 T256, {runs} runs"}
+            "sample": f"oracle single-thread, full tiny forward+loss B8 T256, {runs} runs",
+            "host_cpu": cpu_model, "nproc": nproc}
 
 
 def main():
@@ -505,10 +525,11 @@ def main():
     cpu = None
     tiny_cpu = None
     if not a.no_cpu:
-        log("CPU baseline (oracle, 1 core) ...")
-        cpu = cpu_baseline_large()
+        cpu_model, nproc = host_cpu()  # before the baseline pins itself to one core
+        log(f"CPU baseline (oracle, 1 core of {nproc}: {cpu_model}) ...")
+        cpu = cpu_baseline_large(cpu_model, nproc)
         log(f"CPU large: {cpu['value']} tok/s")
-        tiny_cpu = cpu_baseline_tiny()
+        tiny_cpu = cpu_baseline_tiny(cpu_model, nproc)
         log(f"CPU tiny: {tiny_cpu['value']} tok/s")
 
     out = {
@@ -524,6 +545,10 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic: reference seeded init (Rng(0)), uniform token ids (Lab scheme)",
+        "value_scope": ("weights and token ids resident in HBM when the timed region starts "
+                        "(staged once, each step replays the forward+loss graph); excludes the "
+                        "ids/targets upload and the loss download, which "
+                        "extra.pcie_inclusive_tokens_per_s includes"),
         "config": {"workload": "large preset forward + cross-entropy loss", "batch": 4,
                    "seq": 1024, "vocab": 32000, "params": 1009338368,
                    "flops_per_step": total_flops},
