@@ -437,6 +437,9 @@ def main():
                     help="skip the back-to-back timing of the op-level bandwidth kernels")
     ap.add_argument("--no-mfma-probe", action="store_true",
                     help="skip the fp32 MFMA issue-rate probe (the measured ceiling)")
+    ap.add_argument("--tiny-only", action="store_true",
+                    help="time only the tiny preset's forward+loss and log it (no JSON line): "
+                         "the command its kernel-trace profile is taken on")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run one add kernel over 2^26 floats (read 512 MiB, write "
                          "256 MiB) to calibrate HBM byte counters")
@@ -459,6 +462,15 @@ def main():
         for b in bufs:
             b.free()
         log("copy probe: add over 2^26 floats done")
+
+    if a.tiny_only:
+        tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup)
+        log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
+            f"loss {tiny['loss']:.5f}")
+        for k, (ms, nl) in tiny["profile"].items():
+            log(f"  {k}: {ms:.4f} ms over {nl} launches (HIP events per launch)")
+        ctx.close()
+        return
 
     large = time_model(mh, ctx, "large", 4, 1024, a.steps, a.warmup, a.train_steps,
                        checkpoint=not a.no_checkpoint, shards=not a.no_shards)
