@@ -13,9 +13,15 @@
 // then the final norm, the tied head x . E^T (read as the nt form, E^T never
 // exists) and the loss (row log-sum-exp + f64 mean).
 //
-// Weights keep the reference parameter order in one device buffer; the QKV
-// and gate/up matrices are additionally packed once at creation (and again
-// after every optimizer step).
+// Weights live in one device buffer in a device layout that differs from the
+// reference parameter order only inside a block: per block attn_norm, Wqkv
+// (the q|k|v columns side by side, so QKV is one GEMM), Wo, mlp_norm, Wgu
+// (gate column f at 2f and up column f at 2f+1, zero columns up to ff_pad, so
+// the SwiGLU epilogue finds g and u in one lane) and Wd. Gradients and the
+// AdamW moments use the same layout, so a training step writes the weight
+// gradients of the packed matrices in place and updates them with no copies;
+// the reference order exists only at the boundary (creation, downloads,
+// checkpoints), converted on the device.
 //
 // Training (Lab::step_once, lab.rs:263-283; Trainer::update, trainer.rs:185-205)
 // runs the same forward with every value the backward reads kept per layer
@@ -254,9 +260,9 @@ struct Model {
     Context *ctx = nullptr;
     Config cfg;
     int64_t n_params = 0;
-    float *w = nullptr;        // reference parameter order
-    float *packed = nullptr;   // per layer: Wqkv [d, d+2kv] then Wgu [d, 2*ff_pad]
-    int64_t ff_pad = 0;
+    float *w = nullptr;        // the device layout, n_dev floats
+    int64_t n_dev = 0;
+    int64_t ff_pad = 0;        // ff rounded up to a multiple of 32
     float *cos_t = nullptr, *sin_t = nullptr;
     HostRng rng{};
     bool has_rng = false;
@@ -285,7 +291,7 @@ struct Model {
         float *xs = nullptr, *xn1 = nullptr, *qkv = nullptr, *cb = nullptr, *lse = nullptr,
               *hres = nullptr, *xn2 = nullptr, *gu = nullptr, *h = nullptr, *xnf = nullptr,
               *dx = nullptr, *dy = nullptr, *dxn = nullptr, *dctx = nullptr, *dqkv = nullptr,
-              *dvec = nullptr, *wtmp = nullptr, *rms = nullptr, *norm = nullptr,
+              *dvec = nullptr, *rms = nullptr, *norm = nullptr,
               *apart = nullptr;  // attention backward's per-head dK, dV (GQA)
         double *norm_scratch = nullptr;
         int32_t *uniq = nullptr, *start = nullptr, *order = nullptr;
@@ -311,30 +317,128 @@ struct Model {
     }
 
     int64_t qkv_cols() const { return cfg.d + 2 * cfg.kv(); }
-    const float *embed() const { return w; }
-    const float *block(int64_t l) const { return w + cfg.vocab * cfg.d + l * cfg.block_params(); }
-    const float *attn_norm(int64_t l) const { return block(l); }
-    const float *wo(int64_t l) const {
-        const int64_t d = cfg.d, kv = cfg.kv();
-        return block(l) + d + d * d + 2 * d * kv;
+    // The device layout: embed [V,d]; per block attn_norm [d], Wqkv [d, qc],
+    // Wo [d,d], mlp_norm [d], Wgu [d, 2*ff_pad], Wd [ff,d]; final_norm [d];
+    // lm_head [d,V] when untied.
+    int64_t dev_block() const {
+        const int64_t d = cfg.d;
+        return 2 * d + d * qkv_cols() + d * d + 2 * d * ff_pad + cfg.ff * d;
     }
-    const float *mlp_norm(int64_t l) const { return wo(l) + cfg.d * cfg.d; }
-    const float *wd(int64_t l) const { return mlp_norm(l) + cfg.d + 2 * cfg.d * cfg.ff; }
-    const float *final_norm() const { return block(cfg.layers); }
+    int64_t dev_count() const {
+        return cfg.vocab * cfg.d + cfg.layers * dev_block() + cfg.d +
+               (cfg.tie ? 0 : cfg.d * cfg.vocab);
+    }
+    int64_t off_block(int64_t l) const { return cfg.vocab * cfg.d + l * dev_block(); }
+    int64_t off_wqkv(int64_t l) const { return off_block(l) + cfg.d; }
+    int64_t off_wo(int64_t l) const { return off_wqkv(l) + cfg.d * qkv_cols(); }
+    int64_t off_mlp_norm(int64_t l) const { return off_wo(l) + cfg.d * cfg.d; }
+    int64_t off_wgu(int64_t l) const { return off_mlp_norm(l) + cfg.d; }
+    int64_t off_wd(int64_t l) const { return off_wgu(l) + 2 * cfg.d * ff_pad; }
+    int64_t off_final_norm() const { return off_block(cfg.layers); }
+    const float *embed() const { return w; }
+    const float *attn_norm(int64_t l) const { return w + off_block(l); }
+    const float *wqkv(int64_t l) const { return w + off_wqkv(l); }
+    const float *wo(int64_t l) const { return w + off_wo(l); }
+    const float *mlp_norm(int64_t l) const { return w + off_mlp_norm(l); }
+    const float *wgu(int64_t l) const { return w + off_wgu(l); }
+    const float *wd(int64_t l) const { return w + off_wd(l); }
+    const float *final_norm() const { return w + off_final_norm(); }
     const float *lm_head() const { return final_norm() + cfg.d; }
-    int64_t packed_per_layer() const { return cfg.d * qkv_cols() + cfg.d * 2 * ff_pad; }
-    const float *wqkv(int64_t l) const { return packed + l * packed_per_layer(); }
-    const float *wgu(int64_t l) const { return wqkv(l) + cfg.d * qkv_cols(); }
+
+    // Reference parameter order (docs/midman-model.md:20) <-> the device
+    // layout, device to device (ref and dev are parameter-sized buffers).
+    void ref_to_dev(const float *ref, float *dev) {
+        const int64_t d = cfg.d, kv = cfg.kv(), ff = cfg.ff, V = cfg.vocab, qc = qkv_cols();
+        auto copy = [&](float *dst, const float *src, int64_t n) {
+            check_hip(hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice,
+                                     ctx->stream),
+                      "weights copy");
+        };
+        copy(dev, ref, V * d);
+        for (int64_t l = 0; l < cfg.layers; ++l) {
+            const float *r = ref + V * d + l * cfg.block_params();
+            const float *an = r, *wq = an + d, *wk = wq + d * d, *wv = wk + d * kv;
+            const float *wo_ = wv + d * kv, *mn = wo_ + d * d, *wg = mn + d, *wu = wg + d * ff;
+            const float *wd_ = wu + d * ff;
+            copy(dev + off_block(l), an, d);
+            launch_pack_cols(*ctx, wq, d, d, dev + off_wqkv(l), qc, 0);
+            launch_pack_cols(*ctx, wk, d, kv, dev + off_wqkv(l), qc, d);
+            launch_pack_cols(*ctx, wv, d, kv, dev + off_wqkv(l), qc, d + kv);
+            copy(dev + off_wo(l), wo_, d * d);
+            copy(dev + off_mlp_norm(l), mn, d);
+            launch_pack_gate_up(*ctx, wg, wu, d, ff, ff_pad, dev + off_wgu(l));
+            copy(dev + off_wd(l), wd_, ff * d);
+        }
+        const float *rf = ref + V * d + cfg.layers * cfg.block_params();
+        copy(dev + off_final_norm(), rf, d);
+        if (!cfg.tie) copy(dev + off_final_norm() + d, rf + d, d * V);
+    }
+    void dev_to_ref(const float *dev, float *ref) {
+        const int64_t d = cfg.d, kv = cfg.kv(), ff = cfg.ff, V = cfg.vocab, qc = qkv_cols();
+        auto copy = [&](float *dst, const float *src, int64_t n) {
+            check_hip(hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice,
+                                     ctx->stream),
+                      "weights copy");
+        };
+        copy(ref, dev, V * d);
+        for (int64_t l = 0; l < cfg.layers; ++l) {
+            float *r = ref + V * d + l * cfg.block_params();
+            float *an = r, *wq = an + d, *wk = wq + d * d, *wv = wk + d * kv;
+            float *wo_ = wv + d * kv, *mn = wo_ + d * d, *wg = mn + d, *wu = wg + d * ff;
+            float *wd_ = wu + d * ff;
+            copy(an, dev + off_block(l), d);
+            launch_unpack_cols(*ctx, dev + off_wqkv(l), qc, 0, d, d, wq);
+            launch_unpack_cols(*ctx, dev + off_wqkv(l), qc, d, d, kv, wk);
+            launch_unpack_cols(*ctx, dev + off_wqkv(l), qc, d + kv, d, kv, wv);
+            copy(wo_, dev + off_wo(l), d * d);
+            copy(mn, dev + off_mlp_norm(l), d);
+            launch_unpack_gate_up(*ctx, dev + off_wgu(l), d, ff, ff_pad, wg, wu);
+            copy(wd_, dev + off_wd(l), ff * d);
+        }
+        float *rf = ref + V * d + cfg.layers * cfg.block_params();
+        copy(rf, dev + off_final_norm(), d);
+        if (!cfg.tie) copy(rf + d, dev + off_final_norm() + d, d * V);
+    }
+
+    // A temporary device buffer of n floats, freed when it goes out of scope
+    // (after the stream has drained).
+    struct DevTemp {
+        Context *c;
+        float *p = nullptr;
+        DevTemp(Context *cx, int64_t n) : c(cx) {
+            check_hip(hipMalloc(&p, (size_t)std::max<int64_t>(n, 1) * 4), "staging alloc");
+        }
+        ~DevTemp() {
+            if (p) {
+                (void)hipStreamSynchronize(c->stream);
+                (void)hipFree(p);
+            }
+        }
+    };
+
+    // Weights given in the reference order on the device.
+    void set_weights_from_ref(const float *ref_dev) {
+        ref_to_dev(ref_dev, w);
+        check_hip(hipStreamSynchronize(ctx->stream), "weights conversion sync");
+    }
+    // A device buffer (weights or gradients) to the host in the reference order.
+    void download_ref(const float *dev, float *host) {
+        DevTemp t(ctx, n_params);
+        dev_to_ref(dev, t.p);
+        check_hip(hipMemcpyAsync(host, t.p, (size_t)n_params * 4, hipMemcpyDeviceToHost,
+                                 ctx->stream),
+                  "download");
+        check_hip(hipStreamSynchronize(ctx->stream), "download sync");
+    }
 
     void release() {
         ctx->select();
         (void)hipStreamSynchronize(ctx->stream);
         drop_graph();
-        for (void *p : {(void *)w, (void *)packed, (void *)cos_t, (void *)sin_t, (void *)act,
-                        (void *)tr.mem, (void *)grad, (void *)mom1, (void *)mom2,
-                        (void *)ranges})
+        for (void *p : {(void *)w, (void *)cos_t, (void *)sin_t, (void *)act, (void *)tr.mem,
+                        (void *)grad, (void *)mom1, (void *)mom2, (void *)ranges})
             if (p) (void)hipFree(p);
-        w = packed = cos_t = sin_t = act = nullptr;
+        w = cos_t = sin_t = act = nullptr;
         tr.mem = grad = mom1 = mom2 = nullptr;
         ranges = nullptr;
     }
@@ -364,24 +468,8 @@ struct Model {
         staged_n = 0;
     }
 
-    // Copies Wq|Wk|Wv and the interleaved Wg/Wu from w into the packed buffer.
-    void repack() {
-        const int64_t d = cfg.d, kv = cfg.kv(), ff = cfg.ff;
-        for (int64_t l = 0; l < cfg.layers; ++l) {
-            const float *wq = block(l) + d, *wk = wq + d * d, *wv = wk + d * kv;
-            float *dst = const_cast<float *>(wqkv(l));
-            launch_pack_cols(*ctx, wq, d, d, dst, qkv_cols(), 0);
-            launch_pack_cols(*ctx, wk, d, kv, dst, qkv_cols(), d);
-            launch_pack_cols(*ctx, wv, d, kv, dst, qkv_cols(), d + kv);
-            const float *wg = mlp_norm(l) + d, *wu = wg + d * ff;
-            launch_pack_gate_up(*ctx, wg, wu, d, ff, ff_pad, const_cast<float *>(wgu(l)));
-        }
-    }
-
-    void pack() {
-        ff_pad = (cfg.ff + 31) / 32 * 32;
-        check_hip(hipMalloc(&packed, (size_t)(cfg.layers * packed_per_layer()) * 4), "packed alloc");
-        repack();
+    // The rotary tables (rope.rs:71-79, f64 on the host) into HBM.
+    void init_tables() {
         const size_t tab = (size_t)(cfg.max_seq * (cfg.hd() / 2));
         std::vector<float> c(tab), s(tab);
         rope_tables_host(cfg.hd(), cfg.max_seq, cfg.theta, c.data(), s.data());
@@ -389,7 +477,7 @@ struct Model {
         check_hip(hipMalloc(&sin_t, tab * 4), "rope alloc");
         check_hip(hipMemcpyAsync(cos_t, c.data(), tab * 4, hipMemcpyHostToDevice, ctx->stream), "rope upload");
         check_hip(hipMemcpyAsync(sin_t, s.data(), tab * 4, hipMemcpyHostToDevice, ctx->stream), "rope upload");
-        check_hip(hipStreamSynchronize(ctx->stream), "pack sync");
+        check_hip(hipStreamSynchronize(ctx->stream), "rope tables sync");
     }
 
     // Checks of model.rs:134-148 and the id ranges (ops_shape.rs:250-252,
@@ -574,7 +662,6 @@ struct Model {
         }
         const int64_t d = cfg.d, L = cfg.layers, qc = qkv_cols(), ffp2 = 2 * ff_pad;
         auto al = [](int64_t v) { return (v + 63) / 64 * 64; };
-        const int64_t wcols = std::max(qc, ffp2);
         const int64_t sizes[] = {
             al((L + 1) * n * d),            // xs
             al(L * n * d),                  // xn1
@@ -592,7 +679,6 @@ struct Model {
             al(n * d),                      // dctx
             al(n * qc),                     // dqkv
             al(lse_rows(n)),                // dvec
-            al(d * wcols),                  // wtmp
             al(rms_norm_backward_scratch(n, d)),  // rms
             64,                             // norm
             al(attention_backward_scratch_floats(1, cfg.heads, cfg.kv_heads, n, cfg.hd())),
@@ -600,17 +686,17 @@ struct Model {
             al(n), al(n + 1), al(n),        // uniq, start, order (int32)
         };
         constexpr int nslots = (int)(sizeof(sizes) / sizeof(sizes[0]));
-        static_assert(nslots == 24, "training slots");
+        static_assert(nslots == 23, "training slots");
         float *base[nslots];
         tr.mem = alloc_guarded(*ctx, sizes, nslots, base, tr_bands, "training activation alloc");
         float **slots[] = {&tr.xs,   &tr.xn1, &tr.qkv,  &tr.cb,   &tr.lse,  &tr.hres, &tr.xn2,
                            &tr.gu,   &tr.h,   &tr.xnf,  &tr.dx,   &tr.dy,   &tr.dxn,  &tr.dctx,
-                           &tr.dqkv, &tr.dvec, &tr.wtmp, &tr.rms, &tr.norm, &tr.apart};
-        for (int i = 0; i < 20; ++i) *slots[i] = base[i];
-        tr.norm_scratch = reinterpret_cast<double *>(base[20]);
-        tr.uniq = reinterpret_cast<int32_t *>(base[21]);
-        tr.start = reinterpret_cast<int32_t *>(base[22]);
-        tr.order = reinterpret_cast<int32_t *>(base[23]);
+                           &tr.dqkv, &tr.dvec, &tr.rms, &tr.norm, &tr.apart};
+        for (int i = 0; i < 19; ++i) *slots[i] = base[i];
+        tr.norm_scratch = reinterpret_cast<double *>(base[19]);
+        tr.uniq = reinterpret_cast<int32_t *>(base[20]);
+        tr.start = reinterpret_cast<int32_t *>(base[21]);
+        tr.order = reinterpret_cast<int32_t *>(base[22]);
         tr.cap = n;
         staged_index = false;
     }
@@ -758,8 +844,6 @@ struct Model {
             float *qkvl = tr.qkv + l * cap * qc, *cbl = tr.cb + l * cap * d;
             float *hres = tr.hres + l * cap * d, *xn2 = tr.xn2 + l * cap * d;
             float *gu = tr.gu + l * cap * ffp2, *hl = tr.h + l * cap * ff;
-            const float *wq = block(l) + d, *wk = wq + d * d, *wv = wk + d * kv;
-            const float *wg = mlp_norm(l) + d, *wu = wg + d * ff;
             // MLP: y = hres + h . Wd, h = silu(gate) * up
             GemmDesc dh = desc(tr.dx, false, d, wd(l), true, d, gu, ffp2, n, d, ff);
             dh.epi = EPI_SWIGLU_BWD;
@@ -768,8 +852,9 @@ struct Model {
             gemm(c, dh);  // gu now holds (dgate, dup) pairs
             gemm(c, desc(hl, true, ff, tr.dx, false, d, grad_of(wd(l)), d, ff, n, d));
             gemm(c, desc(gu, false, ffp2, wgu(l), true, ffp2, tr.dxn, d, n, ffp2, d));
-            gemm(c, desc(xn2, true, d, gu, false, ffp2, tr.wtmp, ffp2, d, n, ffp2));
-            launch_unpack_gate_up(c, tr.wtmp, d, ff, ff_pad, grad_of(wg), grad_of(wu));
+            // the packed (gate, up) gradient straight into its place (columns
+            // past ff: zero pre-activations, so zero gradients)
+            gemm(c, desc(xn2, true, d, gu, false, ffp2, grad_of(wgu(l)), ffp2, d, n, ffp2));
             launch_rms_norm_backward(c, hres, mlp_norm(l), tr.dxn, n, d, cfg.eps, tr.dx, true,
                                      grad_of(mlp_norm(l)), tr.rms);
             // attention: hres = x + ctx . Wo
@@ -802,10 +887,7 @@ struct Model {
             ab.scratch = cfg.kv_heads < cfg.heads ? tr.apart : nullptr;
             attention_backward(c, ab);
             gemm(c, desc(tr.dqkv, false, qc, wqkv(l), true, qc, tr.dxn, d, n, qc, d));
-            gemm(c, desc(xn1, true, d, tr.dqkv, false, qc, tr.wtmp, qc, d, n, qc));
-            launch_unpack_cols(c, tr.wtmp, qc, 0, d, d, grad_of(wq));
-            launch_unpack_cols(c, tr.wtmp, qc, d, d, kv, grad_of(wk));
-            launch_unpack_cols(c, tr.wtmp, qc, d + kv, d, kv, grad_of(wv));
+            gemm(c, desc(xn1, true, d, tr.dqkv, false, qc, grad_of(wqkv(l)), qc, d, n, qc));
             launch_rms_norm_backward(c, x, attn_norm(l), tr.dxn, n, d, cfg.eps, tr.dx, true,
                                      grad_of(attn_norm(l)), tr.rms);
         }
@@ -817,7 +899,7 @@ struct Model {
     }
 
     void ensure_grad() {
-        if (!grad) check_hip(hipMalloc(&grad, (size_t)n_params * 4), "gradient alloc");
+        if (!grad) check_hip(hipMalloc(&grad, (size_t)n_dev * 4), "gradient alloc");
     }
 
     // Forward + loss + backward on the staged batch; gradients stay on the device.
@@ -829,17 +911,17 @@ struct Model {
         ensure_grad();
         enqueue_train_forward(batch, seq);
         enqueue_backward(batch, seq);
-        launch_global_norm(*ctx, grad, n_params, tr.norm_scratch, tr.norm);
+        launch_global_norm(*ctx, grad, n_dev, tr.norm_scratch, tr.norm);
         has_grad = true;
     }
 
     void ensure_optimizer_state() {
         if (!has_opt) fail(MMH_ERR_ARGUMENT, "no optimizer set (mmh_model_set_optimizer)");
         if (!mom1) {
-            check_hip(hipMalloc(&mom1, (size_t)n_params * 4), "moment alloc");
-            check_hip(hipMalloc(&mom2, (size_t)n_params * 4), "moment alloc");
-            launch_fill(*ctx, mom1, n_params, 0.0f);
-            launch_fill(*ctx, mom2, n_params, 0.0f);
+            check_hip(hipMalloc(&mom1, (size_t)n_dev * 4), "moment alloc");
+            check_hip(hipMalloc(&mom2, (size_t)n_dev * 4), "moment alloc");
+            launch_fill(*ctx, mom1, n_dev, 0.0f);
+            launch_fill(*ctx, mom2, n_dev, 0.0f);
         }
         if (!ranges) {
             // rank-1 parameters: the two norms of every block and the final norm
@@ -852,7 +934,7 @@ struct Model {
             const int64_t f = final_norm() - w;
             r.insert(r.end(), {f, f + d});
             nranges = (int)(r.size() / 2);
-            ranges_worst = adamw_max_ranges_per_chunk(r.data(), nranges, n_params);
+            ranges_worst = adamw_max_ranges_per_chunk(r.data(), nranges, n_dev);
             check_hip(hipMalloc(&ranges, r.size() * 8), "range alloc");
             check_hip(hipMemcpyAsync(ranges, r.data(), r.size() * 8, hipMemcpyHostToDevice,
                                      ctx->stream), "range upload");
@@ -861,7 +943,8 @@ struct Model {
     }
 
     // clip + AdamW at lr for optimizer step opt_steps + 1 (adamw.rs:180-188),
-    // gated on the device by the loss and norm being finite; then repack.
+    // gated on the device by the loss and norm being finite. The packed
+    // matrices are the weights themselves: nothing is copied afterwards.
     void enqueue_update(float lr) {
         if (!(std::isfinite(lr) && lr >= 0.0f))
             fail(MMH_ERR_ARGUMENT, "adamw: lr must be finite and not negative, got " +
@@ -878,9 +961,8 @@ struct Model {
         const float bias1 = (float)(1.0 - std::pow((double)beta1, t));
         a.bias2_sqrt = (float)std::sqrt(1.0 - std::pow((double)beta2, t));
         a.step_size = lr / bias1;
-        launch_adamw(*ctx, w, grad, mom1, mom2, n_params, ranges, nranges, ranges_worst, a, loss,
+        launch_adamw(*ctx, w, grad, mom1, mom2, n_dev, ranges, nranges, ranges_worst, a, loss,
                      tr.norm);
-        repack();
     }
 
     // Guard words of the activation blocks that no longer hold kGuardBits.
@@ -949,7 +1031,12 @@ std::unique_ptr<Model> new_model(mmh_handle ctx, const double *config) {
     m->ctx = &context(ctx);
     m->cfg = parse_config(config);
     m->n_params = m->cfg.param_count();
-    check_hip(hipMalloc(&m->w, (size_t)m->n_params * 4), "weights alloc");
+    m->ff_pad = (m->cfg.ff + 31) / 32 * 32;
+    m->n_dev = m->dev_count();
+    check_hip(hipMalloc(&m->w, (size_t)m->n_dev * 4), "weights alloc");
+    // zero padding (Wgu's columns past ff) before any conversion fills the rest
+    launch_fill(*m->ctx, m->w, m->n_dev, 0.0f);
+    m->init_tables();
     return m;
 }
 
@@ -964,9 +1051,9 @@ void release_models_of(mmh_handle ctx) {
     }
     for (auto &m : dead) {
         m->drop_graph();
-        for (void *p : {(void *)m->w, (void *)m->packed, (void *)m->cos_t, (void *)m->sin_t,
-                        (void *)m->act, (void *)m->tr.mem, (void *)m->grad, (void *)m->mom1,
-                        (void *)m->mom2, (void *)m->ranges})
+        for (void *p : {(void *)m->w, (void *)m->cos_t, (void *)m->sin_t, (void *)m->act,
+                        (void *)m->tr.mem, (void *)m->grad, (void *)m->mom1, (void *)m->mom2,
+                        (void *)m->ranges})
             if (p) (void)hipFree(p);
     }
 }
@@ -989,10 +1076,13 @@ int32_t mmh_model_create(mmh_handle ctx, const double config[10], const float *w
                                     " parameters but " + std::to_string(n_weights) +
                                     " weights were given");
         }
-        check_hip(hipMemcpyAsync(m->w, weights_host, (size_t)n_weights * 4,
-                                 hipMemcpyHostToDevice, m->ctx->stream),
-                  "weights upload");
-        m->pack();
+        {
+            Model::DevTemp ref(m->ctx, m->n_params);
+            check_hip(hipMemcpyAsync(ref.p, weights_host, (size_t)n_weights * 4,
+                                     hipMemcpyHostToDevice, m->ctx->stream),
+                      "weights upload");
+            m->set_weights_from_ref(ref.p);
+        }
         *out_model = register_model(std::move(m));
         return MMH_OK;
     });
@@ -1035,13 +1125,15 @@ int32_t mmh_model_create_seeded(mmh_handle ctx, const double config[10], uint64_
         ones(d);
         if (!c.tie) draw(d * c.vocab, std_);
         if (p - host.data() != m->n_params) fail(MMH_ERR_OTHER, "init: parameter count mismatch");
-        check_hip(hipMemcpyAsync(m->w, host.data(), host.size() * 4, hipMemcpyHostToDevice,
-                                 m->ctx->stream),
-                  "weights upload");
-        check_hip(hipStreamSynchronize(m->ctx->stream), "weights upload sync");
+        {
+            Model::DevTemp ref(m->ctx, m->n_params);
+            check_hip(hipMemcpyAsync(ref.p, host.data(), host.size() * 4, hipMemcpyHostToDevice,
+                                     m->ctx->stream),
+                      "weights upload");
+            m->set_weights_from_ref(ref.p);
+        }
         m->rng = rng;
         m->has_rng = true;
-        m->pack();
         *out_model = register_model(std::move(m));
         return MMH_OK;
     });
@@ -1077,10 +1169,7 @@ int32_t mmh_model_download_weights(mmh_handle model_h, float *out_host, int64_t 
         Model &m = model(model_h);
         if (!out_host) fail(MMH_ERR_ARGUMENT, "out is a null pointer");
         if (n != m.n_params) fail(MMH_ERR_SHAPE, "weights: wrong count");
-        check_hip(hipMemcpyAsync(out_host, m.w, (size_t)n * 4, hipMemcpyDeviceToHost,
-                                 m.ctx->stream),
-                  "weights download");
-        check_hip(hipStreamSynchronize(m.ctx->stream), "weights download sync");
+        m.download_ref(m.w, out_host);
         return MMH_OK;
     });
 }
@@ -1194,10 +1283,7 @@ int32_t mmh_model_download_grads(mmh_handle model_h, float *out_host, int64_t n)
         if (!out_host) fail(MMH_ERR_ARGUMENT, "out is a null pointer");
         if (!m.has_grad) fail(MMH_ERR_ARGUMENT, "no gradients yet: run mmh_model_backward first");
         if (n != m.n_params) fail(MMH_ERR_SHAPE, "gradients: wrong count");
-        check_hip(hipMemcpyAsync(out_host, m.grad, (size_t)n * 4, hipMemcpyDeviceToHost,
-                                 m.ctx->stream),
-                  "gradient download");
-        check_hip(hipStreamSynchronize(m.ctx->stream), "gradient download sync");
+        m.download_ref(m.grad, out_host);
         return MMH_OK;
     });
 }
@@ -1237,8 +1323,8 @@ int32_t mmh_model_set_optimizer(mmh_handle model_h, float beta1, float beta2, fl
         m.has_opt = true;
         m.opt_steps = 0;
         if (m.mom1) {  // a new optimizer starts with no moments
-            launch_fill(*m.ctx, m.mom1, m.n_params, 0.0f);
-            launch_fill(*m.ctx, m.mom2, m.n_params, 0.0f);
+            launch_fill(*m.ctx, m.mom1, m.n_dev, 0.0f);
+            launch_fill(*m.ctx, m.mom2, m.n_dev, 0.0f);
             check_hip(hipStreamSynchronize(m.ctx->stream), "optimizer reset sync");
         }
         return MMH_OK;
@@ -1391,19 +1477,9 @@ std::vector<ParamSpec> specs_of(const Model &m) {
 // The new weights arrive in a separate buffer and replace the old ones only when
 // the whole file has been read (params.rs:126: nothing changes on failure).
 void load_into(Model &m, const std::string &path) {
-    float *fresh = nullptr;
-    check_hip(hipMalloc(&fresh, (size_t)m.n_params * 4), "checkpoint staging alloc");
-    try {
-        load_checkpoint(*m.ctx, specs_of(m), m.n_params, path, fresh, nullptr);
-    } catch (...) {
-        (void)hipFree(fresh);
-        throw;
-    }
-    check_hip(hipMemcpyAsync(m.w, fresh, (size_t)m.n_params * 4, hipMemcpyDeviceToDevice,
-                             m.ctx->stream),
-              "checkpoint swap");
-    check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint swap sync");
-    (void)hipFree(fresh);
+    Model::DevTemp fresh(m.ctx, m.n_params);  // the file's tensors, reference order
+    load_checkpoint(*m.ctx, specs_of(m), m.n_params, path, fresh.p, nullptr);
+    m.set_weights_from_ref(fresh.p);
 }
 
 }  // namespace
@@ -1422,7 +1498,10 @@ int32_t mmh_model_save_checkpoint(mmh_handle model_h, const char *path, const ch
         }
         m.ctx->select();
         check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint sync");
-        save_checkpoint(*m.ctx, m.w, specs_of(m), meta, path);
+        Model::DevTemp ref(m.ctx, m.n_params);  // the weights in the reference order
+        m.dev_to_ref(m.w, ref.p);
+        check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint conversion sync");
+        save_checkpoint(*m.ctx, ref.p, specs_of(m), meta, path);
         return MMH_OK;
     });
 }
@@ -1434,8 +1513,6 @@ int32_t mmh_model_load_checkpoint(mmh_handle model_h, const char *path) {
         m.ctx->select();
         check_hip(hipStreamSynchronize(m.ctx->stream), "checkpoint sync");
         load_into(m, path);
-        m.repack();
-        check_hip(hipStreamSynchronize(m.ctx->stream), "repack sync");
         return MMH_OK;
     });
 }
@@ -1447,12 +1524,11 @@ int32_t mmh_model_create_from_checkpoint(mmh_handle ctx, const double config[10]
         if (!path) fail(MMH_ERR_ARGUMENT, "path is a null pointer");
         auto m = new_model(ctx, config);
         try {
-            load_checkpoint(*m->ctx, specs_of(*m), m->n_params, path, m->w, nullptr);
+            load_into(*m, path);
         } catch (...) {
             m->release();
             throw;
         }
-        m->pack();
         *out_model = register_model(std::move(m));
         return MMH_OK;
     });

@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__
     if (threadIdx.x == 0) out[0] = (float)(part[0] / (double)n);
 }
 
-// ---- weight packing (model creation, after every optimizer step) -------------
+// ---- weight packing (the reference order <-> the model's device layout) -----
 // A workgroup row of the grid (blockIdx.y, striding by gridDim.y) walks whole
 // rows; its threads walk the row in float4s where the layout allows (vec),
 // else in single floats. Bit-exact copies.
