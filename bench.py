@@ -300,6 +300,22 @@ def gemm_sweep(mh, ctx, reps=10):
     return rows
 
 
+def launch_floor_us(mh, ctx, reps=200):
+    """Microseconds per launch of a one-workgroup kernel (an add over 256
+    floats) issued back to back on the stream, as the sweep's GEMMs are: the
+    fixed cost under every GEMM launch there."""
+    a, b, c = ctx.empty((256,)), ctx.empty((256,)), ctx.empty((256,))
+    fn = lambda: mh.check(mh.lib().mmh_add(ctx.handle, a.ptr, b.ptr, c.ptr, 256))
+    warm_up(ctx, fn)
+    ctx.timer_start()
+    for _ in range(reps):
+        fn()
+    us = ctx.timer_stop() / reps * 1000
+    for x in (a, b, c):
+        x.free()
+    return round(us, 2)
+
+
 def time_bandwidth(mh, ctx, reps=20):
     """The op-level bandwidth kernels at the large preset's shapes, each timed
     as `reps` back-to-back launches between two HIP events: the per-launch
@@ -528,8 +544,11 @@ def main():
             f"{k} {v['gbs']:.0f} GB/s ({v['frac_of_hbm']:.0%})" for k, v in bandwidth.items()))
 
     sweep = None
+    floor_us = None
     if not a.no_sweep:
         sweep = gemm_sweep(mh, ctx)
+        floor_us = launch_floor_us(mh, ctx)
+        log(f"launch floor (back-to-back one-workgroup kernels): {floor_us} us")
         log("sweep: " + ", ".join(f"{r['K']}x{r['N']}:{r['fwd_nn']}/{r['dA_nt']}/{r['dB_tn']}"
                                   for r in sweep))
     ctx.close()
@@ -605,6 +624,7 @@ def main():
                 "pcie_inclusive_tokens_per_s": round(tiny["pcie_inclusive_tokens_per_s"], 1),
                 "cpu_baseline": tiny_cpu},
             "gemm_sweep_tflops": sweep,
+            "gemm_sweep_launch_floor_us": floor_us,
             "device": name,
         },
     }

@@ -115,7 +115,7 @@ int32_t mmh_gemm_tn(mmh_handle ctx, const float *a, const float *b, float *c, in
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). The same kernels and split choices as the
  * three entry points above, so the same bits; the split-K partials live in a
- * fixed 32 MiB device array per GPU instead of the context's workspace. A
+ * fixed 16 MiB device array per GPU instead of the context's workspace. A
  * product whose partials need more (splits x m x n x 4 bytes; split-K is
  * chosen only when the output tiles cannot fill the chip, and every product of
  * the benchmark sweep fits) is refused with MMH_ERR_SHAPE before anything

@@ -1321,8 +1321,11 @@ void gemm(Context &ctx, const GemmDesc &d) {
             while (tiles * splits < cus && splits < 16 && ktiles / (splits * 2) >= 8)
                 splits *= 2;
         } else {
-            // Fill the chip: at least two tiles per CU, at least 8 K-steps per split.
-            const int64_t target = 2 * (int64_t)cus;
+            // Fill the chip: a tile per CU (two, with twice the split partials
+            // written and summed, measured 7-10% slower from 1 GFLOP up: the
+            // sweep's dB forms, the training's 2048 x 2048 weight gradient), at
+            // least 8 K-steps per split.
+            const int64_t target = (int64_t)cus;
             while (tiles * splits < target && splits < 16 && ktiles / (splits * 2) >= 8)
                 splits *= 2;
         }

@@ -47,7 +47,7 @@ def operands(form, m, k, n, seed):
     # the 128x128 kernel split along K (16 tiles), then the K-split kernel
     ("nn", (512, 8192, 512), (300, 2000, 200)),
     ("nt", (256, 4096, 1024), (64, 512, 64)),
-    # the sweep's largest partials (32 MiB: dB 4096 x 256 from 2048 rows, 8
+    # the sweep's largest partials (16 MiB: dB 4096 x 256 from 2048 rows, 4
     # splits), then the smallest sweep dB
     ("tn", (4096, 2048, 256), (256, 2048, 256)),
 ])
@@ -68,8 +68,8 @@ def test_noalloc_unsplit_product_and_errors(ctx):
     want = run(ctx, "alloc", "nn", a, b, c0, 2048, 256, 4096, False)
     got = run(ctx, "noalloc", "nn", a, b, c0, 2048, 256, 4096, False)
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
-    # partials over the 32 MiB array: 1152 x 2048 (144 tiles of 128 x 128)
-    # from a 2048-long reduction splits 4 ways, 37.7 MB of partials; refused,
+    # partials over the 16 MiB array: 1152 x 2048 (144 tiles of 128 x 128)
+    # from a 2048-long reduction splits 2 ways, 18.9 MB of partials; refused,
     # the output untouched
     m, k, n = 1152, 2048, 2048
     A, B = ctx.empty((m, k)), ctx.empty((k, n))
