@@ -40,6 +40,7 @@ namespace mmh {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 struct AttnP {
     const float *q, *k, *v;
@@ -286,6 +287,250 @@ __global__ __launch_bounds__(512) void attn_fwd_kernel(AttnP p) {
     }
 }
 
+// 16-row strips, 16 waves (heads of 64 and 128, grids of at least one
+// 128-row block per CU). The same pairing of a long block (nqb-1-z, waves
+// 0-7) with a short one (z, waves 8-15) and the same 32-key K/V tiles shared
+// through a double-buffered LDS stage, but each wave owns 16 query rows and
+// runs 16x16x4 MFMAs, so a wave needs half the registers (at most 128: four
+// waves per SIMD instead of two). Wave w of a block takes strip w (w < 4) or
+// 11 - w, so the two waves of a block that share a SIMD (w and w + 4) hold
+// strips i and 7 - i: every SIMD carries the same causal work, and the
+// barrier that ends each tile waits for no SIMD with more tiles than another.
+// A wave stores its rows straight from its accumulators as soon as its last
+// tile is done, while the other waves still compute.
+//
+// Layouts (lane l, g = l/16, i = l%16; register r of an accumulator block is
+// row 4g + r of the 16x16 result, column i):
+//   S^T block kb (keys 16kb..16kb+15 of the tile, query q0 + i): k-step s
+//     pairs the head dims 32g + s (A: K[16kb + i][32g + s] from LDS, B: the
+//     lane's own Q[q0 + i][32g + s]); lane l's register r is key 16kb+4g+r.
+//   O^T block 4h+e (dims 64h + 4i' + e, i' = 0..15): k-step (kb, r) pairs the
+//     keys 16kb + 4g + r (A: V[16kb+4g+r][64h + 4i + e], B: the lane's own P
+//     register (kb, r)); lane l's register r' is O[q0 + i][64h + 16g + 4r' + e].
+// Row max and sum of a query meet across its four lanes (i, i+16, i+32, i+48)
+// through two lane swaps.
+template <int HD>
+__global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
+    static_assert(HD == 64 || HD == 128, "16-row strips take heads of 64 or 128");
+    constexpr int NT = 1024;
+    constexpr int QB = 128;
+    constexpr int NS = HD / 4;      // S^T k-steps per key block (dims per lane group)
+    constexpr int NH = HD / 64;     // O^T dim halves: blocks 4h .. 4h+3
+    constexpr int KS = HD + 4;      // K row stride (16-byte rows, lanes 4 banks apart)
+    constexpr int F4 = 32 * HD / 4; // float4s per K or V tile
+    constexpr int PER = F4 / NT;    // 1 (HD 128) or 0.5 (HD 64: half the threads load)
+    constexpr int RA = 3;           // LDS operand reads in flight ahead of their MFMAs
+    // Two stages of 64 keys (two 32-key tiles each): one barrier per 64 keys.
+    // Tile kt lives in stage (kt/2)&1, rows 32*(kt&1) ...
+    __shared__ __attribute__((aligned(16))) float smem[2 * 64 * KS + 2 * 64 * HD];
+    auto Ks = [&](int kt) { return smem + ((kt >> 1) & 1) * 64 * KS + (kt & 1) * 32 * KS; };
+    auto Vs = [&](int kt) { return smem + 128 * KS + ((kt >> 1) & 1) * 64 * HD + (kt & 1) * 32 * HD; };
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, li = lane & 15;
+    const int half = wave >> 3, w8 = wave & 7;
+    const int strip = w8 < 4 ? w8 : 11 - w8;
+    const int head = blockIdx.x, b = blockIdx.y;
+    const int long_blk = p.nqb - 1 - (int)blockIdx.z;
+    const int qblk = half ? (int)blockIdx.z : long_blk;
+    const bool active = half == 0 || qblk < long_blk;  // nqb odd: the middle block once
+    const int kvh = head / (p.h / p.hkv);
+    const int T = p.t;
+    const int ntiles = min(long_blk * QB + QB - 1, T - 1) / 32 + 1;
+    const int q0 = qblk * QB + strip * 16;
+    const int my_tiles = active && q0 < T ? min(q0 + 15, T - 1) / 32 + 1 : 0;
+    const int qi = q0 + li;
+
+    const float *Q = p.q + b * p.sqb + head * p.sqh;
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+
+    const float sc = p.scale * 1.4426950408889634f;  // scores in log2 units
+    float qr[NS];
+    {
+        const float4 *src = reinterpret_cast<const float4 *>(Q + (int64_t)min(qi, T - 1) * p.sqt + g * NS);
+#pragma unroll
+        for (int s = 0; s < NS / 4; ++s) {
+            const float4 v = src[s];
+            qr[4 * s + 0] = v.x * sc;
+            qr[4 * s + 1] = v.y * sc;
+            qr[4 * s + 2] = v.z * sc;
+            qr[4 * s + 3] = v.w * sc;
+        }
+    }
+
+    // thread tid loads float4 tid of the K tile and of the V tile (keys past
+    // T read row T-1: finite values whose scores are masked)
+    // (HD 64: threads past the tile read a copy of another thread's float4
+    // and do not store it, so the loads need no branch and can sit inside
+    // the MFMA stream)
+    const bool loader = PER >= 1 || tid < F4;
+    const int ltid = PER >= 1 ? tid : tid % F4;
+    const int lj = (4 * ltid) / HD, lc = (4 * ltid) % HD;
+    float4 kreg, vreg;
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+        const int key = min(kt * 32 + lj, T - 1);
+        kreg = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + lc);
+        vreg = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + lc);
+    };
+    auto store_tile = [&](int kt) __attribute__((always_inline)) {
+        if (loader) {
+            *reinterpret_cast<float4 *>(Ks(kt) + lj * KS + lc) = kreg;
+            *reinterpret_cast<float4 *>(Vs(kt) + lj * HD + lc) = vreg;
+        }
+    };
+
+    floatx4 o[4 * NH];
+#pragma unroll
+    for (int db = 0; db < 4 * NH; ++db) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+
+    // sum / max over a query's four lanes (i, i+16, i+32, i+48)
+    auto quad_max = [](float v) __attribute__((always_inline)) {
+        auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+        auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+    };
+    auto quad_sum = [](float v) __attribute__((always_inline)) {
+        auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+        auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+    };
+
+    float pv[8];  // P of the current tile
+    // scores and softmax of tile kt; the next tile's global loads (tile nxt)
+    // are issued between its first MFMAs, not all at once after the barrier
+    // V operands: 8 * NH float4 per tile, step i = NH*j + h:
+    // V[16(j/4) + 4g + j%4][64h + 4li ..], each feeding 4 MFMAs, read RA ahead;
+    // the first RA are issued before the softmax, so P.V starts without waiting
+    constexpr int NV = 8 * NH;
+    float4 vring[RA + 1];
+    auto vread = [&](int kt, int i) __attribute__((always_inline)) {
+        const int j = i / NH, h = i % NH;
+        return reinterpret_cast<const float4 *>(Vs(kt) + (16 * (j >> 2) + 4 * g + (j & 3)) * HD + 4 * li)[16 * h];
+    };
+    auto qk_softmax = [&](int kt, int nxt) __attribute__((always_inline)) {
+        const float *Kb = Ks(kt);
+        // 16 float4 K operands per tile, step i = 2t + kb: K[16kb + li][g*NS + 4t ..],
+        // each feeding 4 MFMAs; read RA steps ahead through a ring of RA+1
+        // registers so the LDS latency hides behind the MFMAs of earlier steps.
+        floatx4 sacc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+        float4 ring[RA + 1];
+        auto kread = [&](int i) __attribute__((always_inline)) {
+            return reinterpret_cast<const float4 *>(Kb + (16 * (i & 1) + li) * KS + g * NS)[i >> 1];
+        };
+#pragma unroll
+        for (int i = 0; i < RA; ++i) ring[i] = kread(i);
+        __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+#pragma unroll
+        for (int i = 0; i < 2 * (NS / 4); ++i) {
+            if (i + RA < 2 * (NS / 4)) ring[(i + RA) % (RA + 1)] = kread(i + RA);
+            const float4 kv = ring[i % (RA + 1)];
+            const int kb = i & 1, t = i >> 1;
+            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qr[4 * t + 0], sacc[kb], 0, 0, 0);
+            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qr[4 * t + 1], sacc[kb], 0, 0, 0);
+            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qr[4 * t + 2], sacc[kb], 0, 0, 0);
+            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qr[4 * t + 3], sacc[kb], 0, 0, 0);
+            if (i + RA < 2 * (NS / 4)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+            if (i == 1) {
+                load_tile(nxt);
+                __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RA; ++i) vring[i] = vread(kt, i);
+        __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        const int k0 = kt * 32;
+        float mloc = -INFINITY;
+        if (k0 + 31 <= q0 && k0 + 31 < T) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                pv[j] = sacc[j >> 2][j & 3];
+                mloc = fmaxf(mloc, pv[j]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = k0 + 16 * (j >> 2) + 4 * g + (j & 3);
+                pv[j] = (key <= qi && key < T) ? sacc[j >> 2][j & 3] : -INFINITY;
+                mloc = fmaxf(mloc, pv[j]);
+            }
+        }
+        mloc = quad_max(mloc);
+        const bool need = mloc > m_run + 8.0f;  // lazy rescale, as attn_fwd_kernel
+        if (__any(need)) {
+            const float m_new = need ? mloc : m_run;
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+            l_run *= alpha;
+#pragma unroll
+            for (int db = 0; db < 4 * NH; ++db)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
+            m_run = m_new;
+        }
+        float lsum = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            pv[j] = __builtin_amdgcn_exp2f(pv[j] - m_run);
+            lsum += pv[j];
+        }
+        l_run += quad_sum(lsum);
+    };
+    auto pv_apply = [&](int kt) __attribute__((always_inline)) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if (i + RA < NV) vring[(i + RA) % (RA + 1)] = vread(kt, i + RA);
+            const float4 v4 = vring[i % (RA + 1)];
+            const int j = i / NH, h = i % NH;
+            o[4 * h + 0] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.x, pv[j], o[4 * h + 0], 0, 0, 0);
+            o[4 * h + 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.y, pv[j], o[4 * h + 1], 0, 0, 0);
+            o[4 * h + 2] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.z, pv[j], o[4 * h + 2], 0, 0, 0);
+            o[4 * h + 3] = __builtin_amdgcn_mfma_f32_16x16x4f32(v4.w, pv[j], o[4 * h + 3], 0, 0, 0);
+            if (i + RA < NV) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (kt == my_tiles - 1 && qi < T) {
+            // this strip is done: its rows leave now, straight from the accumulators
+            const float inv = 1.0f / l_run;
+            float *orow = p.out + b * p.sob + head * p.soh + (int64_t)qi * p.sot;
+#pragma unroll
+            for (int h = 0; h < NH; ++h)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    *reinterpret_cast<float4 *>(orow + 64 * h + 16 * g + 4 * r) =
+                        make_float4(o[4 * h + 0][r] * inv, o[4 * h + 1][r] * inv,
+                                    o[4 * h + 2][r] * inv, o[4 * h + 3][r] * inv);
+            if (p.lse && g == 0) p.lse[((int64_t)b * p.h + head) * T + qi] = m_run + log2f(l_run);
+        }
+    };
+
+    load_tile(0);
+    store_tile(0);
+    if (ntiles > 1) {
+        load_tile(1);
+        store_tile(1);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        // during tile kt, the tile two ahead goes to the other stage
+        const int nxt = min(kt + 2, ntiles - 1);  // the last steps reload a tile they never store
+        if (kt < my_tiles) {
+            qk_softmax(kt, nxt);
+            pv_apply(kt);
+        } else {
+            load_tile(nxt);
+        }
+        if (kt + 2 < ntiles) store_tile(kt + 2);
+        if ((kt & 1) && kt + 1 < ntiles) __syncthreads();
+    }
+}
+
 // Key-split variant for grids that would not cover the chip (few batch x head
 // pairs, short T: the tiny preset has 32 pairs of 256 rows). A workgroup owns
 // 32 query rows; its 4 waves take the key tiles up to the diagonal round-robin
@@ -493,7 +738,7 @@ __global__ __launch_bounds__(256) void rope_rows_kernel(float *__restrict__ x, i
 }
 
 template <int HD>
-void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool split) {
+void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool split, bool rows16) {
     if constexpr (HD <= 64) {
         if (split) {
             hipLaunchKernelGGL((attn_fwd_split_kernel<HD>), grid, dim3(256), 0, ctx.stream, p);
@@ -501,6 +746,12 @@ void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool split) {
         }
     }
     grid.z = (grid.z + 1) / 2;  // query blocks in pairs
+    if constexpr (HD == 64 || HD == 128) {
+        if (rows16) {
+            hipLaunchKernelGGL((attn_fwd16_kernel<HD>), grid, dim3(1024), 0, ctx.stream, p);
+            return;
+        }
+    }
     hipLaunchKernelGGL((attn_fwd_kernel<HD>), grid, dim3(512), 0, ctx.stream, p);
 }
 
@@ -583,13 +834,15 @@ void attention(Context &ctx, const AttnDesc &d) {
     p.nqb = (int)(split ? (d.t + 31) / 32 : (d.t + 127) / 128);
     p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
     dim3 grid((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
+    // the 16-row kernel stores rows as float4s
+    const bool rows16 = al16(d.out) && d.sob % 4 == 0 && d.soh % 4 == 0 && d.sot % 4 == 0;
     switch (d.hd) {
-        case 4: launch_hd<4>(ctx, p, grid, split); break;
-        case 8: launch_hd<8>(ctx, p, grid, split); break;
-        case 16: launch_hd<16>(ctx, p, grid, split); break;
-        case 32: launch_hd<32>(ctx, p, grid, split); break;
-        case 64: launch_hd<64>(ctx, p, grid, split); break;
-        default: launch_hd<128>(ctx, p, grid, split); break;
+        case 4: launch_hd<4>(ctx, p, grid, split, false); break;
+        case 8: launch_hd<8>(ctx, p, grid, split, false); break;
+        case 16: launch_hd<16>(ctx, p, grid, split, false); break;
+        case 32: launch_hd<32>(ctx, p, grid, split, false); break;
+        case 64: launch_hd<64>(ctx, p, grid, split, rows16); break;
+        default: launch_hd<128>(ctx, p, grid, split, rows16); break;
     }
     check_hip(hipGetLastError(), "attention launch");
 }

@@ -89,6 +89,8 @@ ATTN_SHAPES = [  # B, H, Hkv, T, hd
     # grids of at least one 128-row block per CU take the block kernels (the
     # shapes above, the strip kernels) also for heads of 64 and 32
     (4, 16, 8, 512, 64), (8, 8, 8, 512, 32),
+    # the large preset's heads at its training shape and at its max_seq_len
+    (4, 16, 8, 1024, 128), (1, 16, 8, 2048, 128),
 ]
 
 
