@@ -12,7 +12,8 @@
 // loads are in flight while the current one is used. A SIMD then runs one wave
 // of each block, nqb+1 blocks' worth of tiles in every workgroup, where
 // unpaired blocks would leave the CUs that drew two long blocks working while
-// the rest idle. (attn_fwd_split_kernel below covers small grids.)
+// the rest idle. (attn_fwd16_kernel below takes heads of 64 and 128 with 16
+// rows per wave; attn_fwd_split_kernel covers small grids.)
 // Each wave keeps an online softmax for its rows, so no [T,T] tensor exists.
 //
 // The products are computed transposed so that every per-query quantity lives

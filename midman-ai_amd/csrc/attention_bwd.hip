@@ -454,6 +454,365 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
     }
 }
 
+// ---- 16-row strips (heads of 64 and 128) ------------------------------------
+// The products above with 16x16x4 MFMAs and 16 rows (dq: queries, dkv: keys)
+// per wave, 8 waves per workgroup (one 128-row block), at most 256 VGPRs: two
+// waves per SIMD where the 32-row kernels ran one. The waves of a SIMD (w and
+// w + 4) hold strips i and 7 - i, whose causal work is equal; tiles come
+// through two LDS stages of 64 rows (one barrier per two 32-row tiles), the
+// next tiles' global loads sit between the first MFMAs, and every operand
+// read from LDS is issued three MFMA groups ahead through a register ring.
+// Layouts (lane l, g = l/16, i = l%16; register r of a 16x16 block is row
+// 4g + r, column i):
+//   dq:  S^T, dP^T blocks kb (keys 16kb..): k-step s pairs the dims 32g + s
+//        (A: K or V rows from LDS, B: the lane's own Q (scaled) or dO);
+//        dQ^T block 4h+e (dims 64h + 4i' + e) += K^T . dS^T over the keys
+//        16kb + 4g + r (A: K[16kb+4g+r][64h+4i+e], B: the lane's dS register).
+//   dkv: S, dP blocks qb (queries 16qb..): A: Q or dO rows from LDS, B: the
+//        lane's own K (scaled) or V; dV^T and dK^T blocks += dO^T . P and
+//        Q^T . dS over the queries 16qb + 4g + r.
+// A lane's register r' of block 4h+e is then dim 64h + 16g + 4r' + e of its
+// row, so results leave as float4 rows straight from the accumulators.
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float quad_sum(float v) {
+    auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
+
+// acc[blk] += X[16 blk + i][32g + s] . y[s] over s: the 2 x NS/4 float4
+// operands of an LDS tile (row stride RS) read RA groups ahead. The tile's
+// next global loads (a lambda) are issued after the second group.
+template <int NS, int RS, int RA, int NLOAD, class Load>
+__device__ __forceinline__ void rows_dot(const float *X, int i, int g, const float (&y)[NS],
+                                         floatx4 (&acc)[2], Load &&load) {
+    constexpr int N = 2 * (NS / 4);
+    float4 ring[RA + 1];
+    auto rd = [&](int e) __attribute__((always_inline)) {
+        return reinterpret_cast<const float4 *>(X + (16 * (e & 1) + i) * RS + g * NS)[e >> 1];
+    };
+#pragma unroll
+    for (int e = 0; e < RA; ++e) ring[e] = rd(e);
+    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+        if (e + RA < N) ring[(e + RA) % (RA + 1)] = rd(e + RA);
+        const float4 x = ring[e % (RA + 1)];
+        const int blk = e & 1, t = e >> 1;
+        acc[blk] = mfma16(x.x, y[4 * t + 0], acc[blk]);
+        acc[blk] = mfma16(x.y, y[4 * t + 1], acc[blk]);
+        acc[blk] = mfma16(x.z, y[4 * t + 2], acc[blk]);
+        acc[blk] = mfma16(x.w, y[4 * t + 3], acc[blk]);
+        if (e + RA < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        if (NLOAD > 0 && e == 1) {
+            load();
+            __builtin_amdgcn_sched_group_barrier(0x020, NLOAD, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// acc[4h+e] += Y[16(j/4) + 4g + j%4][64h + 4i + e] . b[j] over the 8 rows j of
+// each lane group: 8 * NH float4 operands read RA ahead.
+template <int NH, int RS, int RA>
+__device__ __forceinline__ void cols_acc(const float *Y, int i, int g, const float (&bv)[8],
+                                         floatx4 (&acc)[4 * NH]) {
+    constexpr int N = 8 * NH;
+    float4 ring[RA + 1];
+    auto rd = [&](int e) __attribute__((always_inline)) {
+        const int j = e / NH, h = e % NH;
+        return reinterpret_cast<const float4 *>(Y + (16 * (j >> 2) + 4 * g + (j & 3)) * RS + 4 * i)[16 * h];
+    };
+#pragma unroll
+    for (int e = 0; e < RA; ++e) ring[e] = rd(e);
+    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+#pragma unroll
+    for (int e = 0; e < N; ++e) {
+        if (e + RA < N) ring[(e + RA) % (RA + 1)] = rd(e + RA);
+        const float4 y = ring[e % (RA + 1)];
+        const int j = e / NH, h = e % NH;
+        acc[4 * h + 0] = mfma16(y.x, bv[j], acc[4 * h + 0]);
+        acc[4 * h + 1] = mfma16(y.y, bv[j], acc[4 * h + 1]);
+        acc[4 * h + 2] = mfma16(y.z, bv[j], acc[4 * h + 2]);
+        acc[4 * h + 3] = mfma16(y.w, bv[j], acc[4 * h + 3]);
+        if (e + RA < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+template <int HD>
+__global__ __launch_bounds__(512, 1) void attn_bwd_dq16_kernel(BwdP p) {
+    static_assert(HD == 64 || HD == 128, "16-row strips take heads of 64 and 128");
+    constexpr int NT = 512, NS = HD / 4, NH = HD / 64, KS = HD + 4, RA = 3;
+    constexpr int F4 = 32 * HD / 4, PER = F4 / NT;  // float4s of K (and of V) per thread per tile
+    // two stages of 64 keys: K rows then V rows; tile kt in stage (kt/2)&1, rows 32*(kt&1)..
+    __shared__ __attribute__((aligned(16))) float smem[2 * 2 * 64 * KS];
+    auto Ks = [&](int kt) { return smem + ((kt >> 1) & 1) * 128 * KS + (kt & 1) * 32 * KS; };
+    auto Vs = [&](int kt) { return Ks(kt) + 64 * KS; };
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, li = lane & 15;
+    const int strip = wave < 4 ? wave : 11 - wave;
+    const int head = blockIdx.x, b = blockIdx.y;
+    const int qblk = p.nqb - 1 - (int)blockIdx.z;  // longest rows first
+    const int kvh = head / (p.h / p.hkv);
+    const int T = p.t;
+    const int ntiles = min(qblk * 128 + 127, T - 1) / 32 + 1;
+    const int q0 = qblk * 128 + strip * 16;
+    const int my_tiles = q0 < T ? min(q0 + 15, T - 1) / 32 + 1 : 0;
+    const int qi = q0 + li, qc = min(qi, T - 1);
+
+    const float *Q = p.q + b * p.sqb + head * p.sqh;
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+    const float *O = p.o + b * p.sob + head * p.soh;
+    const float *dO = p.dout + b * p.sob + head * p.soh;
+    const int64_t rows = ((int64_t)b * p.h + head) * T;
+
+    const float sc = p.scale * 1.4426950408889634f;  // S in log2 units
+    float qr[NS], gr[NS];
+    load_run<NS>(qr, Q + (int64_t)qc * p.sqt + g * NS);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qr[s] *= sc;
+    load_run<NS>(gr, dO + (int64_t)qc * p.sot + g * NS);
+    float dsum = 0.0f;
+    {
+        const float *orow = O + (int64_t)qc * p.sot + g * NS;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) dsum += gr[s] * orow[s];
+    }
+    const float Dq = quad_sum(dsum);
+    const float L2 = p.lse[rows + qc];
+    if (g == 0 && qi < T) p.dvec[rows + qi] = Dq;
+
+    // thread tid loads float4s tid (and tid + 512 at HD 128) of the K and V
+    // tiles (keys past T read row T-1: finite values whose P is 0); named
+    // registers, not an array, so they stay out of scratch memory
+    float4 kreg0, vreg0, kreg1, vreg1;
+    const int j0 = (4 * tid) / HD, c0 = (4 * tid) % HD;
+    const int j1 = (4 * (tid + NT)) / HD, c1 = (4 * (tid + NT)) % HD;
+    auto load_tile = [&](int kt) __attribute__((always_inline)) {
+        const int key0 = min(kt * 32 + j0, T - 1);
+        kreg0 = *reinterpret_cast<const float4 *>(K + (int64_t)key0 * p.skt + c0);
+        vreg0 = *reinterpret_cast<const float4 *>(V + (int64_t)key0 * p.svt + c0);
+        if constexpr (PER > 1) {
+            const int key1 = min(kt * 32 + j1, T - 1);
+            kreg1 = *reinterpret_cast<const float4 *>(K + (int64_t)key1 * p.skt + c1);
+            vreg1 = *reinterpret_cast<const float4 *>(V + (int64_t)key1 * p.svt + c1);
+        }
+    };
+    auto store_tile = [&](int kt) __attribute__((always_inline)) {
+        *reinterpret_cast<float4 *>(Ks(kt) + j0 * KS + c0) = kreg0;
+        *reinterpret_cast<float4 *>(Vs(kt) + j0 * KS + c0) = vreg0;
+        if constexpr (PER > 1) {
+            *reinterpret_cast<float4 *>(Ks(kt) + j1 * KS + c1) = kreg1;
+            *reinterpret_cast<float4 *>(Vs(kt) + j1 * KS + c1) = vreg1;
+        }
+    };
+
+    floatx4 dqa[4 * NH];
+#pragma unroll
+    for (int db = 0; db < 4 * NH; ++db) dqa[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    load_tile(0);
+    store_tile(0);
+    if (ntiles > 1) {
+        load_tile(1);
+        store_tile(1);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < ntiles; ++kt) {
+        const int nxt = min(kt + 2, ntiles - 1);  // the last steps reload a tile they never store
+        if (kt < my_tiles) {
+            floatx4 s[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+            floatx4 dp[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+            rows_dot<NS, KS, RA, 2 * PER>(Ks(kt), li, g, qr, s, [&] { load_tile(nxt); });
+            rows_dot<NS, KS, RA, 0>(Vs(kt), li, g, gr, dp, [] {});
+            const int k0 = kt * 32;
+            const bool full = k0 + 31 <= q0 && k0 + 31 < T;
+            float ds[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int key = k0 + 16 * (j >> 2) + 4 * g + (j & 3);
+                const float e = __builtin_amdgcn_exp2f(s[j >> 2][j & 3] - L2);
+                const float pr = (full || (key <= qi && key < T)) ? e : 0.0f;
+                ds[j] = pr * (dp[j >> 2][j & 3] - Dq);
+            }
+            cols_acc<NH, KS, RA>(Ks(kt), li, g, ds, dqa);
+            if (kt == my_tiles - 1 && qi < T) {
+                float *drow = p.dq + b * p.sqb + head * p.sqh + (int64_t)qi * p.sqt;
+#pragma unroll
+                for (int h = 0; h < NH; ++h)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        *reinterpret_cast<float4 *>(drow + 64 * h + 16 * g + 4 * r) =
+                            make_float4(dqa[4 * h + 0][r] * p.scale, dqa[4 * h + 1][r] * p.scale,
+                                        dqa[4 * h + 2][r] * p.scale, dqa[4 * h + 3][r] * p.scale);
+            }
+        } else {
+            load_tile(nxt);
+        }
+        if (kt + 2 < ntiles) store_tile(kt + 2);
+        if ((kt & 1) && kt + 1 < ntiles) __syncthreads();
+    }
+}
+
+template <int HD>
+__global__ __launch_bounds__(512, 1) void attn_bwd_dkv16_kernel(BwdP p) {
+    static_assert(HD == 64 || HD == 128, "16-row strips take heads of 64 and 128");
+    constexpr int NT = 512, NS = HD / 4, NH = HD / 64, KS = HD + 4, RA = 3;
+    constexpr int F4 = 32 * HD / 4, PER = F4 / NT;
+    // two stages of 64 queries: Q rows, dO rows, then lse2[64] and D[64];
+    // query tile it in stage (it/2)&1, rows 32*(it&1)..
+    constexpr int STAGE = 2 * 64 * KS + 128;
+    __shared__ __attribute__((aligned(16))) float smem[2 * STAGE];
+    auto Qs = [&](int it) { return smem + ((it >> 1) & 1) * STAGE + (it & 1) * 32 * KS; };
+    auto Gs = [&](int it) { return Qs(it) + 64 * KS; };
+    auto Ls = [&](int it) { return smem + ((it >> 1) & 1) * STAGE + 128 * KS + (it & 1) * 32; };
+    auto Ds = [&](int it) { return Ls(it) + 64; };
+
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int g = lane >> 4, li = lane & 15;
+    const int strip = wave < 4 ? wave : 11 - wave;
+    const int groups = p.h / p.hkv;
+    const int kvh = p.part ? (int)blockIdx.x / groups : (int)blockIdx.x;
+    const int g0 = p.part ? (int)blockIdx.x - kvh * groups : 0;
+    const int ng = p.part ? 1 : groups;
+    const int b = blockIdx.y;
+    const int kblk = blockIdx.z;  // block 0 sees the most queries and starts first
+    const int T = p.t;
+    const int k_first = kblk * 128;
+    const int k0 = k_first + strip * 16;
+    const int kj = k0 + li, kc = min(kj, T - 1);
+    const int qt_first = k_first / 32;
+    const int per_head = (T + 31) / 32 - qt_first;
+    const int total = ng * per_head;
+    const int my_first = k0 / 32;  // earlier query tiles lie wholly above these keys
+
+    const float *K = p.k + b * p.skb + kvh * p.skh;
+    const float *V = p.v + b * p.svb + kvh * p.svh;
+    const float sc = p.scale * 1.4426950408889634f;
+    float kr[NS], vr[NS];
+    load_run<NS>(kr, K + (int64_t)kc * p.skt + g * NS);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) kr[s] *= sc;
+    load_run<NS>(vr, V + (int64_t)kc * p.svt + g * NS);
+
+    float4 qreg0, greg0, qreg1, greg1;  // named registers: no scratch array
+    const int j0 = (4 * tid) / HD, c0 = (4 * tid) % HD;
+    const int j1 = (4 * (tid + NT)) / HD, c1 = (4 * (tid + NT)) % HD;
+    float lreg = 0.0f;
+    auto load_tile = [&](int it) __attribute__((always_inline)) {
+        const int hh = it / per_head;
+        const int qt = qt_first + (it - hh * per_head);
+        const int head = kvh * groups + g0 + hh;
+        const float *Qh = p.q + b * p.sqb + head * p.sqh;
+        const float *Gh = p.dout + b * p.sob + head * p.soh;
+        const int q0r = min(qt * 32 + j0, T - 1);  // rows past T: finite, P = 0
+        qreg0 = *reinterpret_cast<const float4 *>(Qh + (int64_t)q0r * p.sqt + c0);
+        greg0 = *reinterpret_cast<const float4 *>(Gh + (int64_t)q0r * p.sot + c0);
+        if constexpr (PER > 1) {
+            const int q1r = min(qt * 32 + j1, T - 1);
+            qreg1 = *reinterpret_cast<const float4 *>(Qh + (int64_t)q1r * p.sqt + c1);
+            greg1 = *reinterpret_cast<const float4 *>(Gh + (int64_t)q1r * p.sot + c1);
+        }
+        // lanes 0-31 of each wave fetch the tile's log-sum-exps, 32-63 its D
+        const int q = min(qt * 32 + (tid & 31), T - 1);
+        lreg = ((tid & 32) ? p.dvec : p.lse)[((int64_t)b * p.h + head) * T + q];
+    };
+    auto store_tile = [&](int it) __attribute__((always_inline)) {
+        *reinterpret_cast<float4 *>(Qs(it) + j0 * KS + c0) = qreg0;
+        *reinterpret_cast<float4 *>(Gs(it) + j0 * KS + c0) = greg0;
+        if constexpr (PER > 1) {
+            *reinterpret_cast<float4 *>(Qs(it) + j1 * KS + c1) = qreg1;
+            *reinterpret_cast<float4 *>(Gs(it) + j1 * KS + c1) = greg1;
+        }
+        if (tid < 32)
+            Ls(it)[tid] = lreg;
+        else if (tid < 64)
+            Ds(it)[tid - 32] = lreg;
+    };
+
+    floatx4 dka[4 * NH], dva[4 * NH];
+#pragma unroll
+    for (int db = 0; db < 4 * NH; ++db) {
+        dka[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+        dva[db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    load_tile(0);
+    store_tile(0);
+    if (total > 1) {
+        load_tile(1);
+        store_tile(1);
+    }
+    __syncthreads();
+    for (int it = 0; it < total; ++it) {
+        const int nxt = min(it + 2, total - 1);
+        const int hh = it / per_head;
+        const int qt = qt_first + (it - hh * per_head);
+        if (qt >= my_first && k0 < T) {
+            floatx4 s[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+            floatx4 dp[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+            rows_dot<NS, KS, RA, 2 * PER>(Qs(it), li, g, kr, s, [&] { load_tile(nxt); });
+            rows_dot<NS, KS, RA, 0>(Gs(it), li, g, vr, dp, [] {});
+            // the tile's lse2 and D for the queries 16qb + 4g + r of this lane
+            const float4 l0 = *reinterpret_cast<const float4 *>(Ls(it) + 4 * g);
+            const float4 l1 = *reinterpret_cast<const float4 *>(Ls(it) + 16 + 4 * g);
+            const float4 d0 = *reinterpret_cast<const float4 *>(Ds(it) + 4 * g);
+            const float4 d1 = *reinterpret_cast<const float4 *>(Ds(it) + 16 + 4 * g);
+            const float lv[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+            const float dv8[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+            const bool full = qt * 32 >= k0 + 15 && qt * 32 + 31 < T && k0 + 15 < T;
+            float pv[8], ds[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int q = qt * 32 + 16 * (j >> 2) + 4 * g + (j & 3);
+                const float e = __builtin_amdgcn_exp2f(s[j >> 2][j & 3] - lv[j]);
+                const float pr = (full || (kj <= q && q < T && kj < T)) ? e : 0.0f;
+                pv[j] = pr;
+                ds[j] = pr * (dp[j >> 2][j & 3] - dv8[j]);
+            }
+            cols_acc<NH, KS, RA>(Gs(it), li, g, pv, dva);
+            cols_acc<NH, KS, RA>(Qs(it), li, g, ds, dka);
+        } else {
+            load_tile(nxt);
+        }
+        if (it + 2 < total) store_tile(it + 2);
+        if ((it & 1) && it + 1 < total) __syncthreads();
+    }
+
+    if (k0 < T && kj < T) {
+        float *dkrow, *dvrow;
+        if (p.part) {
+            const int64_t plane = (int64_t)gridDim.y * p.h * T * HD;
+            dkrow = p.part + ((int64_t)b * p.h + blockIdx.x) * T * HD + (int64_t)kj * HD;
+            dvrow = dkrow + plane;
+        } else {
+            dkrow = p.dk + b * p.skb + kvh * p.skh + (int64_t)kj * p.skt;
+            dvrow = p.dv + b * p.svb + kvh * p.svh + (int64_t)kj * p.svt;
+        }
+#pragma unroll
+        for (int h = 0; h < NH; ++h)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                *reinterpret_cast<float4 *>(dkrow + 64 * h + 16 * g + 4 * r) =
+                    make_float4(dka[4 * h + 0][r] * p.scale, dka[4 * h + 1][r] * p.scale,
+                                dka[4 * h + 2][r] * p.scale, dka[4 * h + 3][r] * p.scale);
+                *reinterpret_cast<float4 *>(dvrow + 64 * h + 16 * g + 4 * r) =
+                    make_float4(dva[4 * h + 0][r], dva[4 * h + 1][r], dva[4 * h + 2][r],
+                                dva[4 * h + 3][r]);
+            }
+    }
+}
+
 // ---- small grids ----------------------------------------------------------
 // When the 128-row blocks leave CUs idle and the head is at most 64 wide (the
 // tiny preset: 4 heads x 8 sequences of 256 rows give 64 workgroups), each
@@ -784,6 +1143,11 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
                 hipLaunchKernelGGL((attn_bwd_dkv_split_kernel<HD>), sk, blk, 0, ctx.stream, p); \
                 break;                                                                     \
             }                                                                              \
+        }                                                                                  \
+        if constexpr (HD == 64 || HD == 128) {                                             \
+            hipLaunchKernelGGL((attn_bwd_dq16_kernel<HD>), gq, dim3(512), 0, ctx.stream, p);  \
+            hipLaunchKernelGGL((attn_bwd_dkv16_kernel<HD>), gk, dim3(512), 0, ctx.stream, p); \
+            break;                                                                         \
         }                                                                                  \
         hipLaunchKernelGGL((attn_bwd_dq_kernel<HD>), gq, blk, 0, ctx.stream, p);           \
         hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD>), gk, blk, 0, ctx.stream, p);          \
