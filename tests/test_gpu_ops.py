@@ -96,6 +96,7 @@ ATTN_CASES = [
     (1, 16, 8, 2048, 128),  # the large preset's max_seq_len
     (2, 16, 8, 77, 128),
     (3, 6, 3, 1, 64),
+    (2, 4, 2, 1, 128),  # a lone position in the 16-row kernel
     # odd counts of 128-row query blocks (the middle one has no partner)
     (1, 4, 2, 300, 128),
     (8, 16, 8, 300, 64),

@@ -91,6 +91,8 @@ ATTN_SHAPES = [  # B, H, Hkv, T, hd
     (4, 16, 8, 512, 64), (8, 8, 8, 512, 32),
     # the large preset's heads at its training shape and at its max_seq_len
     (4, 16, 8, 1024, 128), (1, 16, 8, 2048, 128),
+    # a lone position and a single partial tile at hd 128 (the 16-row kernels)
+    (1, 2, 1, 1, 128), (2, 4, 2, 17, 128),
 ]
 
 
