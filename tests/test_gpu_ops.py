@@ -318,10 +318,11 @@ def test_op_outputs_stay_inside_their_buffers(ctx, off):
         out = Fenced(ctx, n * d, off)
         mh.check(L.mmh_embedding(ctx.handle, T.ptr, V, d, mh._ip(ids), n, out.ptr))
         assert np.array_equal(out.check(f"embedding {V}x{d}").reshape(n, d), table[ids])
-    # attention output: each kernel (paired 128-row blocks at hd 128 and 64,
-    # the key-split kernel at hd 32), ragged T
-    for B, H, Hkv, T, hd in ((1, 4, 2, 300, 128), (2, 4, 4, 77, 64), (4, 4, 4, 130, 32),
-                             (2, 2, 1, 12, 8)):
+    # attention output: each kernel (16-row strips at hd 128 and 64 when the
+    # output is 16-byte aligned, the 32-row paired blocks when it is not, the
+    # key-split kernel for small grids), ragged T
+    for B, H, Hkv, T, hd in ((1, 4, 2, 300, 128), (8, 8, 4, 520, 64), (2, 4, 4, 77, 64),
+                             (4, 4, 4, 130, 32), (2, 2, 1, 12, 8)):
         r = O.rng(B * 100 + T)
         q = O.randn((B, H, T, hd), 1.0, r)
         k = O.randn((B, Hkv, T, hd), 1.0, r)
