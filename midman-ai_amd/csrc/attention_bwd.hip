@@ -30,6 +30,9 @@
 // second kernel sums a group's partials in head order. The gradient of
 // the scaled scores is dS*scale (attention.rs:83), applied to dQ and dK at
 // the end. Entries above the diagonal have P = 0 and contribute nothing.
+// Heads of 64 and 128 take the same products with 16 rows per wave
+// (attn_bwd_dq16_kernel, attn_bwd_dkv16_kernel below); small grids take the
+// strip kernels at the end of the file.
 #include <algorithm>
 
 #include "mmh_internal.h"
