@@ -1104,6 +1104,8 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
     const void *ptrs[] = {d.q, d.k, d.v, d.o, d.dout, d.dq, d.dk, d.dv};
     for (const void *ptr : ptrs)
         if (!al16(ptr)) fail(MMH_ERR_ARGUMENT, "attention backward: buffers must be 16-byte aligned");
+    if (d.scratch && !al16(d.scratch))
+        fail(MMH_ERR_ARGUMENT, "attention backward: the partials scratch must be 16-byte aligned");
     BwdP p{};
     p.q = d.q;
     p.k = d.k;
