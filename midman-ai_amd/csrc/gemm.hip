@@ -110,8 +110,8 @@ __device__ __forceinline__ void unroll_seq(F &&f, std::integer_sequence<int, Is.
 }
 
 // Reductions over each 32-lane half of a wave with DPP moves (quad permutes,
-// then rotations within a 16-lane row) and one swizzle across the two rows of
-// the half. For the max every lane ends with the result; for the sum the
+// then rotations within a 16-lane row) and one v_permlane16_swap across the
+// two rows of the half (a VALU exchange: no trip through the LDS unit). For the max every lane ends with the result; for the sum the
 // lanes associate the terms differently, and lane 0 of the half (the one read)
 // always the same way.
 __device__ __forceinline__ float dpp_f(float v, int ctrl) {
@@ -122,23 +122,25 @@ __device__ __forceinline__ float dpp_f(float v, int ctrl) {
         default: return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
     }
 }
-__device__ __forceinline__ float swap16_f(float v) {
-    // ds_swizzle bit mode: and 0x1f, or 0, xor 0x10 (lane ^ 16 within 32)
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+// The pair {v[l], v[l ^ 16]} in each lane l (in some order).
+__device__ __forceinline__ auto pair16_f(float v) {
+    return __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
 }
 __device__ __forceinline__ float half_max32(float v) {
     v = fmaxf(v, dpp_f(v, 0xB1));   // quad_perm [1,0,3,2]
     v = fmaxf(v, dpp_f(v, 0x4E));   // quad_perm [2,3,0,1]
     v = fmaxf(v, dpp_f(v, 0x124));  // row_ror:4
     v = fmaxf(v, dpp_f(v, 0x128));  // row_ror:8
-    return fmaxf(v, swap16_f(v));
+    const auto q = pair16_f(v);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 __device__ __forceinline__ float half_sum32(float v) {
     v += dpp_f(v, 0xB1);
     v += dpp_f(v, 0x4E);
     v += dpp_f(v, 0x124);
     v += dpp_f(v, 0x128);
-    return v + swap16_f(v);
+    const auto q = pair16_f(v);
+    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
 // The K loop of one 128x128 tile; see the file comment.
@@ -395,6 +397,10 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[j][r] = p.acc_init;
+    // EPI_CE: the tile's target ids go to LDS before the K loop (whose
+    // barriers order them before the epilogue reads them)
+    __shared__ int ce_t[EPI == EPI_CE ? BM : 1];
+    if (EPI == EPI_CE && tid < BM) ce_t[tid] = m0 + tid < M ? p.ce_targets[m0 + tid] : -1;
     const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
                       (kend - kbeg) % BK == 0;
     if (fast)
@@ -460,9 +466,6 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
         // half by DPP moves, then over the two waves sharing the rows through
         // LDS. The lane holding a row's target column keeps its logit.
         __shared__ float ce_m[2][BM], ce_s[2][BM];
-        __shared__ int ce_t[BM];
-        if (tid < BM) ce_t[tid] = m0 + tid < M ? p.ce_targets[m0 + tid] : -1;
-        __syncthreads();
         constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -910,6 +913,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
 // x * w feeds the MFMAs, the sums of squares of x are gathered per lane and
 // combined over the lane halves and then the waves, and each row's 1/rms
 // scales the summed results.
+// The epilogue's own reads (the residual of EPI_ACCUM, the cos/sin of the
+// rotation) are issued before the operand loads, so their latency hides
+// behind the main loop instead of following it.
 // MODE: 2 when the K range of every split is a multiple of 32 and the
 // k-contiguous operands (A rows when !TA, B rows when TB, the norm weights)
 // are 16-byte aligned: float4 reads, no predicates; 1 when only the rows are
@@ -940,6 +946,32 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     const int64_t am = min(m0 + lr, M - 1), bn = min(n0 + lr, N - 1);
     const float *arow = TA ? p.a + am : p.a + am * p.lda;    // then + k * (TA ? lda : 1)
     const float *bcol = TB ? p.b + bn * p.ldb : p.b + bn;    // then + k * (TB ? 1 : ldb)
+
+    // Register r of lane l is C[m0 + 8*(r/4) + 4*(l/32) + r%4][n0 + l%32]; wave
+    // w applies the epilogue to registers w + i*NW, i < NR.
+    constexpr int NR = (16 + NW - 1) / NW;
+    const int64_t col = n0 + lr;
+    float *C = p.c;
+    const float *R = p.resid ? p.resid : C;
+    const bool fin = p.splits == 1;
+    float pre_r[NR], pre_c[NR], pre_s[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        pre_r[i] = 0.0f;
+        pre_c[i] = 1.0f;
+        pre_s[i] = 0.0f;
+        const int r = wave + i * NW;
+        const int64_t row = m0 + 8 * (r >> 2) + 4 * lk + (r & 3);
+        if (r >= 16 || !fin || row >= M || col >= N) continue;
+        if (EPI == EPI_ACCUM) pre_r[i] = R[row * p.ldc + col];
+        if (EPI == EPI_STORE && p.rope_cos && col < p.rope_cols) {
+            const int hd = p.rope_hd, half = hd >> 1;
+            const int pc = (int)col % hd;  // rows and columns below 2^31 (checked at launch)
+            const int64_t t = (int64_t)((int)row % p.rope_seq) * half + (pc < half ? pc : pc - half);
+            pre_c[i] = p.rope_cos[t];
+            pre_s[i] = p.rope_sin[t];
+        }
+    }
 
     floatx16 acc;
 #pragma unroll
@@ -1020,20 +1052,32 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
         }
         __syncthreads();
     }
-    // Register r of lane l is C[m0 + 8*(r/4) + 4*(l/32) + r%4][n0 + l%32].
-    float *C = p.c;
-    const float *R = p.resid ? p.resid : C;
-    const int64_t col = n0 + lr;
-    for (int r = wave; r < 16; r += NW) {
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+        const int r = wave + i * NW;
+        if (r >= 16) break;
         float v = part[0][r][lane];
 #pragma unroll
         for (int w = 1; w < NW; ++w) v = __fadd_rn(v, part[w][r][lane]);
         const int rl = 8 * (r >> 2) + 4 * lk + (r & 3);
+        const int64_t row = m0 + rl;
         if (NORM) v = __fmul_rn(v, sm_inv[rl]);
-        if (p.splits > 1) {
-            if (m0 + rl < M && col < N) p.partial[((int64_t)split * M + m0 + rl) * N + col] = v;
+        if (!fin) {
+            if (row < M && col < N) p.partial[((int64_t)split * M + row) * N + col] = v;
+        } else if (EPI == EPI_ACCUM) {
+            if (row < M && col < N) C[row * p.ldc + col] = __fadd_rn(pre_r[i], v);
+        } else if (EPI == EPI_STORE && p.rope_cos) {
+            // RoPE as in block32_epilogue, with the cos/sin read up front
+            const int hd = p.rope_hd, half = hd >> 1;
+            const float other = __shfl_xor(v, half, 64);
+            if (row >= M || col >= N) continue;
+            if (col < p.rope_cols) {
+                const int pc = (int)col % hd;
+                v = pc < half ? v * pre_c[i] - other * pre_s[i] : v * pre_c[i] + other * pre_s[i];
+            }
+            C[row * p.ldc + col] = v;
         } else {
-            block32_epilogue<EPI>(p, C, R, m0 + rl, col, lr, v);
+            block32_epilogue<EPI>(p, C, R, row, col, lr, v);
         }
     }
 }
@@ -1043,9 +1087,15 @@ void launch_ksplit_mode(Context &ctx, const KParams &p, dim3 grid, int nw) {
     if (nw == 4)
         hipLaunchKernelGGL((gemm_f32_mfma_ksplit<TA, TB, EPI, NORM, 4, MODE>), grid, dim3(256), 0,
                            ctx.stream, p);
-    else
+    else if (nw == 8)
         hipLaunchKernelGGL((gemm_f32_mfma_ksplit<TA, TB, EPI, NORM, 8, MODE>), grid, dim3(512), 0,
                            ctx.stream, p);
+    else if (nw == 12)
+        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<TA, TB, EPI, NORM, 12, MODE>), grid, dim3(768),
+                           0, ctx.stream, p);
+    else
+        hipLaunchKernelGGL((gemm_f32_mfma_ksplit<TA, TB, EPI, NORM, 16, MODE>), grid, dim3(1024),
+                           0, ctx.stream, p);
 }
 
 template <bool TA, bool TB, int EPI, bool NORM>
@@ -1058,10 +1108,13 @@ void launch_ksplit_nw(Context &ctx, const KParams &p, dim3 grid, int mode, int n
         launch_ksplit_mode<TA, TB, EPI, NORM, 0>(ctx, p, grid, nw);
 }
 
-// Four waves up to four K steps of a split (one step each), eight beyond.
+// One wave per K step of a split, in multiples of four waves (one per SIMD)
+// up to sixteen: a wave that walked two steps would wait on its second
+// step's loads after its first step's MFMAs, and the others on it.
 template <bool TA, bool TB, int EPI>
 void launch_ksplit(Context &ctx, const KParams &p, dim3 grid, int mode) {
-    const int nw = (p.k_per_split + 31) / 32 <= 4 ? 4 : 8;
+    const int64_t steps = (p.k_per_split + 31) / 32;
+    const int nw = steps <= 4 ? 4 : steps <= 8 ? 8 : steps <= 12 ? 12 : 16;
     if constexpr (!TA && !TB && (EPI == EPI_STORE || EPI == EPI_SWIGLU)) {
         if (p.norm_w) {
             launch_ksplit_nw<false, false, EPI, true>(ctx, p, grid, mode, nw);
@@ -1356,7 +1409,8 @@ void gemm(Context &ctx, const GemmDesc &d) {
     const bool rope = d.rope_cos != nullptr;
     if (rope) {
         if (d.batch != 1 || d.rope_hd <= 0 || d.rope_hd % 2 || d.rope_seq <= 0 ||
-            d.m % d.rope_seq || d.rope_cols % d.rope_hd || d.rope_cols > d.n || !d.rope_sin)
+            d.m % d.rope_seq || d.rope_cols % d.rope_hd || d.rope_cols > d.n || !d.rope_sin ||
+            d.m > INT32_MAX || d.n > INT32_MAX)
             fail(MMH_ERR_ARGUMENT, "gemm: bad rope arguments");
         if (fuse.rope && splits == 1) {
             p.rope_cos = d.rope_cos;
