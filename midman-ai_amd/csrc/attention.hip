@@ -534,19 +534,21 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
 
 // Key-split variant for grids that would not cover the chip (few batch x head
 // pairs, short T: the tiny preset has 32 pairs of 256 rows). A workgroup owns
-// 32 query rows; its 4 waves take the key tiles up to the diagonal round-robin
-// (wave w: tiles w, w+4, ...), each keeping the online softmax of its share,
+// 32 query rows; its NWV waves (4, or 8 when a block reaches more than 4 key
+// tiles, so no wave walks two tiles while others idle) take the key tiles up
+// to the diagonal round-robin (wave w: tiles w, w+NWV, ...), each keeping the
+// online softmax of its share,
 // with K and V read straight from memory into the MFMA operand layouts (no
 // LDS staging; the next tile's loads are in flight during the current one).
-// The 4 partial states then merge through LDS in wave order: m = max m_w,
+// The NWV partial states then merge through LDS in wave order: m = max m_w,
 // l = sum l_w 2^(m_w - m), O = sum O_w 2^(m_w - m) / l. Heads up to 64 wide.
-template <int HD>
-__global__ __launch_bounds__(256) void attn_fwd_split_kernel(AttnP p) {
+template <int HD, int NWV>
+__global__ __launch_bounds__(64 * NWV) void attn_fwd_split_kernel(AttnP p) {
     constexpr int NS = HD / 2;
     constexpr int NDB = (HD + 31) / 32;
     constexpr int OS = HD + 1;
-    __shared__ float sm_m[4][32], sm_l[4][32];
-    __shared__ float sm_o[4][32 * OS];
+    __shared__ float sm_m[NWV][32], sm_l[NWV][32];
+    __shared__ float sm_o[NWV][32 * OS];
 
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int lq = lane & 31, lh = lane >> 5;
@@ -616,8 +618,8 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(AttnP p) {
     float m_run = -INFINITY, l_run = 0.0f;
 
     if (wave < ntiles) load_tile(wave, kr, vr);
-    for (int kt = wave; kt < ntiles; kt += 4) {
-        if (kt + 4 < ntiles) load_tile(kt + 4, kn, vn);
+    for (int kt = wave; kt < ntiles; kt += NWV) {
+        if (kt + NWV < ntiles) load_tile(kt + NWV, kn, vn);
         floatx16 sacc, sacc1;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -680,10 +682,10 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(AttnP p) {
     __syncthreads();
     float mx = sm_m[0][lq];
 #pragma unroll
-    for (int w = 1; w < 4; ++w) mx = fmaxf(mx, sm_m[w][lq]);
+    for (int w = 1; w < NWV; ++w) mx = fmaxf(mx, sm_m[w][lq]);
     float L = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) L += sm_l[w][lq] * exp2f(sm_m[w][lq] - mx);
+    for (int w = 0; w < NWV; ++w) L += sm_l[w][lq] * exp2f(sm_m[w][lq] - mx);
     const float f = exp2f(m_run - mx) / L;  // 0 for a wave that saw no key
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
@@ -696,12 +698,13 @@ __global__ __launch_bounds__(256) void attn_fwd_split_kernel(AttnP p) {
     if (p.lse && wave == 0 && lh == 0 && qi < T)
         p.lse[((int64_t)b * p.h + head) * T + qi] = mx + log2f(L);
     __syncthreads();
-    for (int idx = tid; idx < 32 * HD; idx += 256) {
+    for (int idx = tid; idx < 32 * HD; idx += 64 * NWV) {
         const int j = idx / HD, c = idx - j * HD;
         const int q = q0 + j;
         if (q < T) {
-            const float v = ((sm_o[0][j * OS + c] + sm_o[1][j * OS + c]) + sm_o[2][j * OS + c]) +
-                            sm_o[3][j * OS + c];
+            float v = sm_o[0][j * OS + c];
+#pragma unroll
+            for (int w = 1; w < NWV; ++w) v += sm_o[w][j * OS + c];
             p.out[b * p.sob + head * p.soh + (int64_t)q * p.sot + c] = v;
         }
     }
@@ -742,7 +745,10 @@ template <int HD>
 void launch_hd(Context &ctx, const AttnP &p, dim3 grid, bool split, bool rows16) {
     if constexpr (HD <= 64) {
         if (split) {
-            hipLaunchKernelGGL((attn_fwd_split_kernel<HD>), grid, dim3(256), 0, ctx.stream, p);
+            if (p.t > 4 * 32)
+                hipLaunchKernelGGL((attn_fwd_split_kernel<HD, 8>), grid, dim3(512), 0, ctx.stream, p);
+            else
+                hipLaunchKernelGGL((attn_fwd_split_kernel<HD, 4>), grid, dim3(256), 0, ctx.stream, p);
             return;
         }
     }

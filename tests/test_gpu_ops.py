@@ -101,6 +101,9 @@ ATTN_CASES = [
     (1, 4, 2, 300, 128),
     (8, 16, 8, 300, 64),
     (16, 8, 8, 260, 32),
+    # the key-split kernel's 8-wave form (blocks of more than 4 key tiles)
+    (2, 4, 2, 200, 64),
+    (1, 2, 1, 150, 16),
 ]
 
 
