@@ -278,11 +278,12 @@ struct Model {
     bool staged_targets = false;
     // The staged forward + loss of one (batch, seq) as a HIP graph: launch-bound
     // small presets replay ~30 kernels with one call. Valid while the
-    // activation buffer it was captured on is the current one.
+    // activation buffer and the context's split-K scratch it was captured on
+    // are the current ones (other calls on the context may grow the scratch).
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     int64_t graph_b = 0, graph_t = 0, warm_b = 0, warm_t = 0;
-    const void *graph_act = nullptr, *warm_act = nullptr;
+    const void *graph_act = nullptr, *warm_act = nullptr, *graph_ws = nullptr;
 
     // ---- training state, allocated on the first training call ----
     struct TrainBuf {
@@ -313,7 +314,7 @@ struct Model {
         graph_exec = nullptr;
         graph = nullptr;
         graph_b = graph_t = 0;
-        graph_act = nullptr;
+        graph_act = graph_ws = nullptr;
     }
 
     int64_t qkv_cols() const { return cfg.d + 2 * cfg.kv(); }
@@ -448,7 +449,11 @@ struct Model {
         if (act) {
             check_hip(hipStreamSynchronize(ctx->stream), "sync");
             check_hip(hipFree(act), "free activations");
+            // nothing points into the old buffer any more, also when the
+            // allocation below fails
             act = nullptr;
+            cap = 0;
+            staged_n = 0;
         }
         const int64_t d = cfg.d;
         auto al = [](int64_t v) { return (v + 63) / 64 * 64; };
@@ -485,6 +490,8 @@ struct Model {
     void stage(const int32_t *inputs, const int32_t *targets, int64_t batch, int64_t seq) {
         if (batch <= 0 || seq <= 0)
             fail(MMH_ERR_ARGUMENT, "forward: batch and seq must be at least 1");
+        if (batch > (int64_t(1) << 40) / seq)
+            fail(MMH_ERR_ARGUMENT, "forward: batch x seq is too large");
         if (seq > cfg.max_seq)
             fail(MMH_ERR_ARGUMENT, "forward: sequence length " + std::to_string(seq) +
                                        " exceeds max_seq_len " + std::to_string(cfg.max_seq));
@@ -603,7 +610,7 @@ struct Model {
     // The graph holds no memset or allocation: only kernel launches.
     void run_staged(int64_t batch, int64_t seq) {
         if (graph_exec && graph_b == batch && graph_t == seq && graph_act == act &&
-            staged_n == batch * seq && staged_targets) {
+            graph_ws == ctx->ws[0] && staged_n == batch * seq && staged_targets) {
             check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
             return;
         }
@@ -629,6 +636,7 @@ struct Model {
         graph_b = batch;
         graph_t = seq;
         graph_act = act;
+        graph_ws = ctx->ws[0];
         check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
     }
 
@@ -917,11 +925,10 @@ struct Model {
 
     void ensure_optimizer_state() {
         if (!has_opt) fail(MMH_ERR_ARGUMENT, "no optimizer set (mmh_model_set_optimizer)");
-        if (!mom1) {
-            check_hip(hipMalloc(&mom1, (size_t)n_dev * 4), "moment alloc");
-            check_hip(hipMalloc(&mom2, (size_t)n_dev * 4), "moment alloc");
-            launch_fill(*ctx, mom1, n_dev, 0.0f);
-            launch_fill(*ctx, mom2, n_dev, 0.0f);
+        for (float **mom : {&mom1, &mom2}) {  // each on its own: a failed second alloc
+            if (*mom) continue;                // leaves the first, which stays valid
+            check_hip(hipMalloc(mom, (size_t)n_dev * 4), "moment alloc");
+            launch_fill(*ctx, *mom, n_dev, 0.0f);
         }
         if (!ranges) {
             // rank-1 parameters: the two norms of every block and the final norm
@@ -933,12 +940,18 @@ struct Model {
             }
             const int64_t f = final_norm() - w;
             r.insert(r.end(), {f, f + d});
+            int64_t *dev = nullptr;
+            check_hip(hipMalloc(&dev, r.size() * 8), "range alloc");
+            const hipError_t e1 = hipMemcpyAsync(dev, r.data(), r.size() * 8,
+                                                 hipMemcpyHostToDevice, ctx->stream);
+            const hipError_t e2 = e1 == hipSuccess ? hipStreamSynchronize(ctx->stream) : e1;
+            if (e2 != hipSuccess) {
+                (void)hipFree(dev);
+                check_hip(e2, "range upload");
+            }
+            ranges = dev;  // set only once the ranges are on the device
             nranges = (int)(r.size() / 2);
             ranges_worst = adamw_max_ranges_per_chunk(r.data(), nranges, n_dev);
-            check_hip(hipMalloc(&ranges, r.size() * 8), "range alloc");
-            check_hip(hipMemcpyAsync(ranges, r.data(), r.size() * 8, hipMemcpyHostToDevice,
-                                     ctx->stream), "range upload");
-            check_hip(hipStreamSynchronize(ctx->stream), "range upload sync");
         }
     }
 
@@ -1034,10 +1047,28 @@ std::unique_ptr<Model> new_model(mmh_handle ctx, const double *config) {
     m->ff_pad = (m->cfg.ff + 31) / 32 * 32;
     m->n_dev = m->dev_count();
     check_hip(hipMalloc(&m->w, (size_t)m->n_dev * 4), "weights alloc");
-    // zero padding (Wgu's columns past ff) before any conversion fills the rest
-    launch_fill(*m->ctx, m->w, m->n_dev, 0.0f);
-    m->init_tables();
+    try {
+        // zero padding (Wgu's columns past ff) before any conversion fills the rest
+        launch_fill(*m->ctx, m->w, m->n_dev, 0.0f);
+        m->init_tables();
+    } catch (...) {
+        m->release();
+        throw;
+    }
     return m;
+}
+
+// Runs fill(m) on a model not yet registered; on any failure the model's
+// device memory is released before the error propagates (a Model frees
+// nothing by itself: its memory goes back through release()).
+template <class F>
+void fill_or_release(Model &m, F &&fill) {
+    try {
+        fill(m);
+    } catch (...) {
+        m.release();
+        throw;
+    }
 }
 
 }  // namespace
@@ -1070,19 +1101,17 @@ int32_t mmh_model_create(mmh_handle ctx, const double config[10], const float *w
         if (!out_model) fail(MMH_ERR_ARGUMENT, "out_model is a null pointer");
         if (!weights_host) fail(MMH_ERR_ARGUMENT, "weights is a null pointer");
         auto m = new_model(ctx, config);
-        if (n_weights != m->n_params) {
-            m->release();
-            fail(MMH_ERR_SHAPE, "the config has " + std::to_string(m->n_params) +
-                                    " parameters but " + std::to_string(n_weights) +
-                                    " weights were given");
-        }
-        {
-            Model::DevTemp ref(m->ctx, m->n_params);
+        fill_or_release(*m, [&](Model &mm) {
+            if (n_weights != mm.n_params)
+                fail(MMH_ERR_SHAPE, "the config has " + std::to_string(mm.n_params) +
+                                        " parameters but " + std::to_string(n_weights) +
+                                        " weights were given");
+            Model::DevTemp ref(mm.ctx, mm.n_params);
             check_hip(hipMemcpyAsync(ref.p, weights_host, (size_t)n_weights * 4,
-                                     hipMemcpyHostToDevice, m->ctx->stream),
+                                     hipMemcpyHostToDevice, mm.ctx->stream),
                       "weights upload");
-            m->set_weights_from_ref(ref.p);
-        }
+            mm.set_weights_from_ref(ref.p);
+        });
         *out_model = register_model(std::move(m));
         return MMH_OK;
     });
@@ -1095,45 +1124,47 @@ int32_t mmh_model_create_seeded(mmh_handle ctx, const double config[10], uint64_
         if (!(std::isfinite(std_) && std_ > 0.f))
             fail(MMH_ERR_ARGUMENT, "init std must be positive and finite");
         auto m = new_model(ctx, config);
-        const Config &c = m->cfg;
-        // model.rs:51-83 draw order; norms are ones (norm.rs:60).
-        std::vector<float> host((size_t)m->n_params);
-        HostRng rng = HostRng::seed(seed);
-        const float out_std = std_ / std::sqrt(2.0f * (float)c.layers);  // init.rs:38
-        const int64_t d = c.d, kv = c.kv(), ff = c.ff;
-        float *p = host.data();
-        auto ones = [&](int64_t n) {
-            std::fill(p, p + n, 1.0f);
-            p += n;
-        };
-        auto draw = [&](int64_t n, float s) {
-            randn_parallel(rng, p, n, s);
-            p += n;
-        };
-        draw(c.vocab * d, std_);
-        for (int64_t l = 0; l < c.layers; ++l) {
+        fill_or_release(*m, [&](Model &mm) {
+            const Config &c = mm.cfg;
+            // model.rs:51-83 draw order; norms are ones (norm.rs:60).
+            std::vector<float> host((size_t)mm.n_params);
+            HostRng rng = HostRng::seed(seed);
+            const float out_std = std_ / std::sqrt(2.0f * (float)c.layers);  // init.rs:38
+            const int64_t d = c.d, kv = c.kv(), ff = c.ff;
+            float *p = host.data();
+            auto ones = [&](int64_t n) {
+                std::fill(p, p + n, 1.0f);
+                p += n;
+            };
+            auto draw = [&](int64_t n, float s) {
+                randn_parallel(rng, p, n, s);
+                p += n;
+            };
+            draw(c.vocab * d, std_);
+            for (int64_t l = 0; l < c.layers; ++l) {
+                ones(d);
+                draw(d * d, std_);
+                draw(d * kv, std_);
+                draw(d * kv, std_);
+                draw(d * d, out_std);
+                ones(d);
+                draw(d * ff, std_);
+                draw(d * ff, std_);
+                draw(ff * d, out_std);
+            }
             ones(d);
-            draw(d * d, std_);
-            draw(d * kv, std_);
-            draw(d * kv, std_);
-            draw(d * d, out_std);
-            ones(d);
-            draw(d * ff, std_);
-            draw(d * ff, std_);
-            draw(ff * d, out_std);
-        }
-        ones(d);
-        if (!c.tie) draw(d * c.vocab, std_);
-        if (p - host.data() != m->n_params) fail(MMH_ERR_OTHER, "init: parameter count mismatch");
-        {
-            Model::DevTemp ref(m->ctx, m->n_params);
-            check_hip(hipMemcpyAsync(ref.p, host.data(), host.size() * 4, hipMemcpyHostToDevice,
-                                     m->ctx->stream),
-                      "weights upload");
-            m->set_weights_from_ref(ref.p);
-        }
-        m->rng = rng;
-        m->has_rng = true;
+            if (!c.tie) draw(d * c.vocab, std_);
+            if (p - host.data() != mm.n_params) fail(MMH_ERR_OTHER, "init: parameter count mismatch");
+            {
+                Model::DevTemp ref(mm.ctx, mm.n_params);
+                check_hip(hipMemcpyAsync(ref.p, host.data(), host.size() * 4, hipMemcpyHostToDevice,
+                                         mm.ctx->stream),
+                          "weights upload");
+                mm.set_weights_from_ref(ref.p);
+            }
+            mm.rng = rng;
+            mm.has_rng = true;
+        });
         *out_model = register_model(std::move(m));
         return MMH_OK;
     });
@@ -1523,12 +1554,7 @@ int32_t mmh_model_create_from_checkpoint(mmh_handle ctx, const double config[10]
         if (!out_model) fail(MMH_ERR_ARGUMENT, "out_model is a null pointer");
         if (!path) fail(MMH_ERR_ARGUMENT, "path is a null pointer");
         auto m = new_model(ctx, config);
-        try {
-            load_into(*m, path);
-        } catch (...) {
-            m->release();
-            throw;
-        }
+        fill_or_release(*m, [&](Model &mm) { load_into(mm, path); });
         *out_model = register_model(std::move(m));
         return MMH_OK;
     });

@@ -305,6 +305,38 @@ def test_staged_graph_replays_match_eager(ctx, preset, batch, seq):
     m.close()
 
 
+def test_staged_graph_follows_the_split_scratch():
+    # A forward whose down projection splits K (d 128, ff 2048, 256 rows: the
+    # split partials live in the context's scratch) is captured; then an
+    # op-level product with larger partials makes the context replace that
+    # scratch. The next run_staged must capture again on the new scratch:
+    # same loss, and a buffer that may now sit at the old scratch's address
+    # (filled with a sentinel) is left alone. A fresh context, so the scratch
+    # starts at the forward's size.
+    print("\n[graph scratch] d128 ff2048 B1 T256", flush=True)
+    cfg = [64, 128, 1, 4, 4, 2048, 256, 10000.0, 1e-5, 1]
+    with mh.Context(0) as ctx:
+        m = mh.Model.new(ctx, cfg, 5)
+        x, y = m.lab_tokens(1, 256)
+        eager = m.loss(x, y, 1, 256)
+        m.stage(x, y, 1, 256)
+        for _ in range(3):  # eager, capture, replay
+            m.run_staged(1, 256)
+            assert m.read_loss() == eager
+        a = ctx.empty((65536, 1024))
+        b = ctx.empty((65536, 1024))
+        c = ctx.empty((1024, 1024))
+        mh.gemm(ctx, "tn", a, b, c, 1024, 65536, 1024)  # 4 splits: 16 MiB of partials
+        ctx.synchronize()
+        sentinel = np.full(1 << 18, 3.25, np.float32)
+        victim = ctx.to_device(sentinel)
+        for _ in range(3):
+            m.run_staged(1, 256)
+            assert m.read_loss() == eager
+        assert np.array_equal(victim.numpy(), sentinel)
+        m.close()
+
+
 def test_model_errors(ctx):
     cfg = mh.PRESETS["smoke"]
     m = mh.Model.new(ctx, cfg, 1)
