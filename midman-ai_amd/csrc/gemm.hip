@@ -512,30 +512,64 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
         }
         return;
     }
+    // The epilogues that read memory (the saved gate/up pairs, the residual)
+    // issue their reads ahead of their stores, 8 or 16 rows at a time: the
+    // destination may be the buffer read (in-place gradients, C += ...), so
+    // the compiler may not move a read past a store and would otherwise wait
+    // out one memory latency per row. Each lane reads only the elements it
+    // writes, so the early reads see the same values.
     if (EPI == EPI_SWIGLU_BWD) {
         // acc is dh[row][col, col+1]; their (g, u) pairs sit at aux columns
         // 2*col .. 2*col+3 and the (dg, du) pairs go to the same columns of C.
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + row_local(r);
-            if (row >= M) continue;
-            const float *gu = p.aux + row * p.ldaux + 2 * col;
-            float *dst = C + row * p.ldc + 2 * col;
-            if (col + 1 < N) {
-                const float4 v = *reinterpret_cast<const float4 *>(gu);
-                const float2 a = swiglu_bwd_f(acc[0][r], v.x, v.y);
-                const float2 b2 = swiglu_bwd_f(acc[1][r], v.z, v.w);
-                *reinterpret_cast<float4 *>(dst) = make_float4(a.x, a.y, b2.x, b2.y);
-            } else if (col < N) {
-                const float2 a = swiglu_bwd_f(acc[0][r], gu[0], gu[1]);
-                dst[0] = a.x;
-                dst[1] = a.y;
+        for (int r0 = 0; r0 < 16; r0 += 8) {
+            float4 g[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t row = m0 + row_local(r0 + j);
+                g[j] = row < M && col + 1 < N
+                           ? *reinterpret_cast<const float4 *>(p.aux + row * p.ldaux + 2 * col)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int r = r0 + j;
+                const int64_t row = m0 + row_local(r);
+                if (row >= M) continue;
+                float *dst = C + row * p.ldc + 2 * col;
+                if (col + 1 < N) {
+                    const float2 a = swiglu_bwd_f(acc[0][r], g[j].x, g[j].y);
+                    const float2 b2 = swiglu_bwd_f(acc[1][r], g[j].z, g[j].w);
+                    *reinterpret_cast<float4 *>(dst) = make_float4(a.x, a.y, b2.x, b2.y);
+                } else if (col < N) {
+                    const float *gu = p.aux + row * p.ldaux + 2 * col;
+                    const float2 a = swiglu_bwd_f(acc[0][r], gu[0], gu[1]);
+                    dst[0] = a.x;
+                    dst[1] = a.y;
+                }
             }
         }
         return;
     }
     const float *R = p.resid ? p.resid + batch * p.stride_c : C;
     const bool pair = p.vec_c && col + 1 < N;
+    if (EPI == EPI_ACCUM && pair) {
+        float2 o[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + row_local(r);
+            o[r] = row < M ? *reinterpret_cast<const float2 *>(R + row * p.ldc + col)
+                           : make_float2(0.f, 0.f);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t row = m0 + row_local(r);
+            if (row >= M) continue;
+            *reinterpret_cast<float2 *>(C + row * p.ldc + col) =
+                make_float2(__fadd_rn(o[r].x, acc[0][r]), __fadd_rn(o[r].y, acc[1][r]));
+        }
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int64_t row = m0 + row_local(r);
