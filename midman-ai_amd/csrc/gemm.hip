@@ -83,6 +83,12 @@ struct KParams {
     // EPI_CE (128x128 kernel): targets in, per-tile (max, sum) pairs and target logits out
     const int32_t *ce_targets;
     float *ce_part, *ce_zt;
+    // Tail balance (128x128 kernel, one matrix): workgroups from tail_first on
+    // each take one of tail_s K-pieces (tail_k long) of tiles tail_first.. in
+    // the grouped order, and write their partial tile to partial (tile-local
+    // [BM][BN] blocks, piece-major); tail_reduce sums them in piece order.
+    int tail_first, tail_s;
+    int64_t tail_k;
     // The value the sums of products start from: +0 (a product, as the
     // reference's fresh zeroed C), or -0 when the sum is added into C (the
     // seam's accumulate: C's own value starts the reference's sum, so a -0 in
@@ -360,6 +366,17 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
     }, std::make_integer_sequence<int, U>{});
 }
 
+// Tile t of the grouped order: GROUP_M tile rows at a time, column by column.
+__device__ __forceinline__ void grouped_tile(const KParams &p, int t, int &tm, int &tn) {
+    const int per_group = GROUP_M * p.tiles_n;
+    const int group = t / per_group;
+    const int first_m = group * GROUP_M;
+    const int gsize = min(p.tiles_m - first_m, GROUP_M);
+    const int in_group = t - group * per_group;
+    tm = first_m + in_group % gsize;
+    tn = in_group / gsize;
+}
+
 template <bool TA, bool TB, int EPI, int CL = 0>
 __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     static_assert(CL == 0 || EPI == EPI_STORE, "the RoPE column layouts store plain values");
@@ -368,28 +385,30 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
 
     const int tid = threadIdx.x;
 
-    // XCD-aware renumbering, then grouped tile order.
+    // XCD-aware renumbering of the whole tiles, then grouped tile order; the
+    // tail pieces (if any) follow the whole tiles.
     int bid = blockIdx.x;
-    {
-        const int nb = gridDim.x, q = nb >> 3, r = nb & 7;
+    int piece = -1;
+    int64_t kbeg = (int64_t)blockIdx.z * p.k_per_split;
+    int64_t kend = min(p.k, kbeg + p.k_per_split);
+    if (p.tail_s > 1 && bid >= p.tail_first) {
+        piece = bid - p.tail_first;
+        bid = p.tail_first + piece / p.tail_s;
+        kbeg = (int64_t)(piece % p.tail_s) * p.tail_k;
+        kend = min(p.k, kbeg + p.tail_k);
+    } else {
+        const int nb = p.tail_s > 1 ? p.tail_first : (int)gridDim.x, q = nb >> 3, r = nb & 7;
         const int xcd = bid & 7, local = bid >> 3;
         bid = xcd * q + (xcd < r ? xcd : r) + local;
     }
-    const int per_group = GROUP_M * p.tiles_n;
-    const int group = bid / per_group;
-    const int first_m = group * GROUP_M;
-    const int gsize = min(p.tiles_m - first_m, GROUP_M);
-    const int in_group = bid - group * per_group;
-    const int tm = first_m + in_group % gsize;
-    const int tn = in_group / gsize;
+    int tm, tn;
+    grouped_tile(p, bid, tm, tn);
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
 
     const int64_t batch = blockIdx.y;
     const int split = blockIdx.z;
     const float *__restrict__ A = p.a + batch * p.stride_a;
     const float *__restrict__ B = p.b + batch * p.stride_b;
-    const int64_t kbeg = (int64_t)split * p.k_per_split;
-    const int64_t kend = min(p.k, kbeg + p.k_per_split);
     const int64_t M = p.m, N = p.n;
 
     floatx16 acc[2];
@@ -418,6 +437,13 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     auto row_local = [&](int r) __attribute__((always_inline)) {
         return wm * 32 + 8 * (r >> 2) + 4 * lk + (r & 3);
     };
+    if (piece >= 0) {  // a tail piece: its partial tile, whole (edges included)
+        float *P = p.partial + (int64_t)piece * (BM * BN) + wn * 64 + 2 * lr;
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            *reinterpret_cast<float2 *>(P + row_local(r) * BN) = make_float2(acc[0][r], acc[1][r]);
+        return;
+    }
     if constexpr (CL != 0) {
         // Column block j of lane lr is column c0 + j*half of C (half = 32 for
         // CL 1, 64 for CL 2), c0 the lane's column in the first half of its
@@ -1214,6 +1240,36 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ p
     }
 }
 
+// The tail tiles of a balanced 128x128 launch: each element sums its tile's
+// tail_s pieces in piece order, then takes the epilogue (store, accumulate, or
+// the SwiGLU backward into the (dg, du) pairs). One workgroup per tile.
+template <int EPI>
+__global__ __launch_bounds__(256) void tail_reduce(KParams p) {
+    const int t = p.tail_first + (int)blockIdx.x;
+    int tm, tn;
+    grouped_tile(p, t, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const float *part = p.partial + (int64_t)blockIdx.x * p.tail_s * (BM * BN);
+    const float *R = p.resid ? p.resid : p.c;
+    for (int e = threadIdx.x; e < BM * BN; e += 256) {
+        const int64_t row = m0 + e / BN, col = n0 + e % BN;
+        if (row >= p.m || col >= p.n) continue;
+        float v = part[e];
+        for (int i = 1; i < p.tail_s; ++i) v = __fadd_rn(v, part[(int64_t)i * (BM * BN) + e]);
+        if (EPI == EPI_SWIGLU_BWD) {
+            const float *gu = p.aux + row * p.ldaux + 2 * col;
+            const float2 o = swiglu_bwd_f(v, gu[0], gu[1]);
+            float *dst = p.c + row * p.ldc + 2 * col;
+            dst[0] = o.x;
+            dst[1] = o.y;
+        } else if (EPI == EPI_ACCUM) {
+            p.c[row * p.ldc + col] = __fadd_rn(R[row * p.ldc + col], v);
+        } else {
+            p.c[row * p.ldc + col] = v;
+        }
+    }
+}
+
 template <bool TA, bool TB, int EPI>
 void launch(Context &ctx, const KParams &p, dim3 grid, bool small) {
     if constexpr (!TA && !TB && (EPI == EPI_STORE || EPI == EPI_SWIGLU)) {
@@ -1455,9 +1511,39 @@ void gemm(Context &ctx, const GemmDesc &d) {
         }
     }
 
-    if (tiles > 0x7fffffff || d.batch > 65535) fail(MMH_ERR_SHAPE, "gemm: grid too large");
-    dim3 grid((unsigned)tiles, (unsigned)d.batch, (unsigned)splits);
+    // Tail balance for the 128x128 kernel: with tiles = q * CUs + R (q >= 1,
+    // R > 0) the CUs that draw q + 1 tiles set the launch's length. The last R
+    // tiles instead split K into s pieces (each a workgroup of its own, at
+    // least 16 K-steps long), so every CU takes about q + R/CUs tiles' work;
+    // tail_reduce sums each tile's pieces in order. Chosen when it shortens
+    // the longest CU's share by at least 5%.
     const int epi = splits > 1 ? EPI_STORE : d.epi;
+    if (!ksplit && !small && splits == 1 && d.batch == 1 && !p.rope_cos && d.force_splits == 0 &&
+        (epi == EPI_STORE || epi == EPI_ACCUM || epi == EPI_SWIGLU_BWD)) {
+        const int64_t cus = cus_of(ctx), q = tiles / cus, R = tiles % cus;
+        int best_s = 1;
+        double best = (double)(q + (R > 0));
+        for (int s : {2, 3, 4, 6, 8}) {
+            if (q < 1 || R == 0 || ktiles / s < 16) break;
+            const double span = (double)q + (double)((R * s + cus - 1) / cus) / s;
+            if (span < best - 1e-9) {
+                best = span;
+                best_s = s;
+            }
+        }
+        const size_t need = (size_t)R * best_s * BM * BN * 4;
+        if (best_s > 1 && best <= 0.95 * (double)(q + 1) &&
+            (!d.scratch || need <= d.scratch_bytes)) {
+            p.tail_first = (int)(tiles - R);
+            p.tail_s = best_s;
+            p.tail_k = (ktiles + best_s - 1) / best_s * BK;
+            p.partial = d.scratch ? d.scratch : static_cast<float *>(ctx.get_scratch(need));
+        }
+    }
+    const int64_t tail_pieces = p.tail_s > 1 ? (tiles - p.tail_first) * p.tail_s : 0;
+    const int64_t grid_x = p.tail_s > 1 ? p.tail_first + tail_pieces : tiles;
+    if (grid_x > 0x7fffffff || d.batch > 65535) fail(MMH_ERR_SHAPE, "gemm: grid too large");
+    dim3 grid((unsigned)grid_x, (unsigned)d.batch, (unsigned)splits);
     if (ksplit) {
         // The k-contiguous operands (A when !ta, B when tb, the norm weights)
         // decide between vector and predicated reads (vec_a / vec_b hold
@@ -1505,6 +1591,16 @@ void gemm(Context &ctx, const GemmDesc &d) {
             hipLaunchKernelGGL(splitk_reduce<EPI_STORE>, dim3(blocks), dim3(256), 0, ctx.stream,
                                p.partial, d.c, nullptr, d.m, d.n, d.ldc, splits);
         check_hip(hipGetLastError(), "split-k reduce launch");
+    }
+    if (p.tail_s > 1) {
+        const dim3 rg((unsigned)(tiles - p.tail_first));
+        if (epi == EPI_SWIGLU_BWD)
+            hipLaunchKernelGGL(tail_reduce<EPI_SWIGLU_BWD>, rg, dim3(256), 0, ctx.stream, p);
+        else if (epi == EPI_ACCUM)
+            hipLaunchKernelGGL(tail_reduce<EPI_ACCUM>, rg, dim3(256), 0, ctx.stream, p);
+        else
+            hipLaunchKernelGGL(tail_reduce<EPI_STORE>, rg, dim3(256), 0, ctx.stream, p);
+        check_hip(hipGetLastError(), "tail reduce launch");
     }
     if (rope && !p.rope_cos)
         launch_rope_strided(ctx, d.c, d.rope_seq * d.ldc, d.rope_hd, d.ldc, d.m / d.rope_seq,

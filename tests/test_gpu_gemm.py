@@ -83,7 +83,11 @@ def test_sweep_forward_and_backward(ctx, k, n):
                                    (2050, 112, 4100),
                                    # short-K shapes of the tiny preset and its edges
                                    (2048, 128, 384), (2048, 352, 128), (2047, 480, 97),
-                                   (2000, 481, 50), (65, 33, 700)])
+                                   (2000, 481, 50), (65, 33, 700),
+                                   # 384 and 448 tiles of 128x128 on 256 CUs: the last
+                                   # 128 / 192 run as 2 / 4 K-pieces + tail_reduce
+                                   # (ragged edges and a short last piece in the first)
+                                   (3000, 1000, 2000), (3584, 1024, 2048)])
 @pytest.mark.parametrize("form", ["nn", "nt", "tn"])
 def test_ragged_shapes_and_accumulate(ctx, m, k, n, form):
     print(f"\n[gemm ragged] {form} m={m} k={k} n={n}", flush=True)
@@ -119,6 +123,7 @@ SPECIAL_PATHS = [
     ("32x32 K-split tiles", 2048, 344, 128),
     ("32x32 K-split over 8 workgroups + reduce", 256, 2048, 256),
     ("128x128 split 8 ways along K + reduce", 1024, 8192, 1024),
+    ("128x128 whole tiles + K-pieces of the last tiles + tail_reduce", 3000, 1000, 2000),
 ]
 
 

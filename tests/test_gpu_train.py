@@ -29,6 +29,9 @@ CASES = {
     "hd32_gqa_t70": ([97, 128, 2, 4, 2, 96, 96, 10000.0, 1e-5, 1], 2, 70, 0.1),
     "hd64_untied_t130": ([301, 256, 2, 4, 2, 200, 160, 10000.0, 1e-5, 0], 1, 130, 0.08),
     "hd128_gqa_t100": ([301, 256, 1, 2, 1, 136, 160, 10000.0, 1e-5, 1], 2, 100, 0.08),
+    # the down projection's backward (SwiGLU-backward epilogue) at 352 tiles of
+    # 128x128 on 256 CUs: its last 96 tiles run as K-pieces plus tail_reduce
+    "tail_pieces_d512_t2048": ([64, 512, 1, 4, 4, 2816, 2048, 10000.0, 1e-5, 1], 1, 2048, 0.05),
 }
 
 
