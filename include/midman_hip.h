@@ -252,6 +252,21 @@ int32_t mmh_model_stage(mmh_handle model, const int32_t *inputs_host,
 int32_t mmh_model_run_staged(mmh_handle model, int64_t batch, int64_t seq);
 int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
 
+/* Which kernels a loss-only forward (mmh_model_loss, run_staged, evaluation)
+ * runs on (no reference counterpart: the reference has one CPU path).
+ * MMH_PATH_AUTO (the default): one persistent launch for the whole forward +
+ * loss where the model fits it (heads of 16 or 32, d_model a multiple of 32
+ * up to 256, d_ff a multiple of 4, at most 16384 tokens: the smoke and tiny
+ * presets), the per-operation kernels otherwise. MMH_PATH_PER_OP: always the
+ * per-operation kernels. The two agree within the forward's tolerance. A
+ * fused launch that fails (a dependency wait past its bound) makes the next
+ * loss read or mmh_model_loss return MMH_ERR_DEVICE. Logits-producing
+ * forwards, mmh_model_profile and training always use the per-operation
+ * kernels. */
+#define MMH_PATH_AUTO 0
+#define MMH_PATH_PER_OP 1
+int32_t mmh_model_set_forward_path(mmh_handle model, int32_t path);
+
 /* Kernel classes timed by mmh_model_profile. */
 #define MMH_PROF_EMBEDDING 0
 #define MMH_PROF_RMS_NORM 1

@@ -22,7 +22,7 @@ LIB = os.path.join(HERE, "libmidman_hip.so")
 ARCH = "gfx950"
 
 HIP_SOURCES = ["runtime.hip", "gemm.hip", "rowops.hip", "attention.hip", "attention_bwd.hip",
-               "train.hip", "checkpoint.hip", "model.hip", "noalloc.hip"]
+               "train.hip", "checkpoint.hip", "model.hip", "noalloc.hip", "fused_forward.hip"]
 # Host code with no HIP in it (also built with the sanitizers: build_sanitized.py)
 HOST_SOURCES = ["host_errors.cpp", "host_math.cpp", "host_sha256.cpp", "host_safetensors.cpp",
                 "host_data.cpp"]

@@ -209,6 +209,43 @@ void launch_adamw(Context &ctx, float *w, const float *g, float *m, float *v, in
                   const int64_t *ranges_dev, int nranges, int64_t max_per_chunk,
                   const AdamArgs &a, const float *loss_dev, const float *norm_dev);
 
+// ---- fused forward (fused_forward.hip) --------------------------------------
+// The loss-only forward of a small model as one persistent launch: per-XCD
+// teams of workgroups, each owning the sequences s with s % 8 == its XCD.
+struct FusedShape {
+    int64_t batch = 0, seq = 0, d = 0, heads = 0, kv_heads = 0, ff = 0, ff_pad = 0, vocab = 0,
+            layers = 0, max_seq = 0;
+    bool tie = true;
+    float eps = 0.0f;
+    int64_t weight_floats = 0;  // the device weight layout's size
+};
+// The fused kernel's arena: every buffer it writes plus a copy of the rotary
+// tables, as float offsets of one allocation.
+struct FusedLayout {
+    int64_t qc = 0, nrb = 0, smax = 0, nsi = 0, ctl_ints = 0, tab_floats = 0;
+    int64_t o_x = 0, o_cb = 0, o_h = 0, o_qkv = 0, o_part = 0, o_zt = 0, o_rl = 0, o_p64 = 0,
+            o_ctl = 0, o_err = 0, o_cos = 0, o_sin = 0;
+    int64_t floats = 0;
+};
+struct FusedArgs {
+    FusedShape shape;
+    const float *w = nullptr;
+    int64_t off_block0 = 0, block_floats = 0, off_final_norm = 0;
+    const int32_t *ids = nullptr, *tgt = nullptr;  // tgt after ids in one allocation
+    float *loss = nullptr;
+    // fused_layout(shape).floats floats: counters (the exit ticket, the team
+    // slots of the 8 XCDs, the task counters) and error word zero before
+    // the first launch, the rotary tables at o_cos / o_sin
+    float *arena = nullptr;
+};
+// Whether the fused kernel takes this shape (heads of 16 or 32, d a multiple
+// of 32 up to 256, ff a multiple of 4, at most 16384 rows, 32-bit offsets).
+bool fused_forward_fits(const Context &ctx, const FusedShape &s);
+FusedLayout fused_layout(const FusedShape &s);
+// Queues the forward + loss; the loss lands in a.loss, the row losses in
+// a.row_loss. The counters are back at zero when the launch ends.
+void launch_fused_forward(Context &ctx, const FusedArgs &a);
+
 // ---- attention --------------------------------------------------------------
 // Element (b,h,t,p) of q is q[b*sqb + h*sqh + t*sqt + p] (likewise k, v with
 // the kv head, and out with the query head).

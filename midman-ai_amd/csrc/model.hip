@@ -283,7 +283,16 @@ struct Model {
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     int64_t graph_b = 0, graph_t = 0, warm_b = 0, warm_t = 0;
-    const void *graph_act = nullptr, *warm_act = nullptr, *graph_ws = nullptr;
+    const void *graph_act = nullptr, *warm_act = nullptr, *graph_ws = nullptr,
+               *graph_arena = nullptr;
+    // The fused loss-only forward (fused_forward.hip): its arena, laid out for
+    // (fused_b, fused_t); forward_path 1 keeps every forward on the
+    // per-operation kernels. fused_check: a fused launch ran since the error
+    // word was last read.
+    float *fused_arena = nullptr;
+    int64_t fused_floats = 0, fused_b = 0, fused_t = 0;
+    int forward_path = 0;
+    bool fused_check = false;
 
     // ---- training state, allocated on the first training call ----
     struct TrainBuf {
@@ -314,7 +323,7 @@ struct Model {
         graph_exec = nullptr;
         graph = nullptr;
         graph_b = graph_t = 0;
-        graph_act = graph_ws = nullptr;
+        graph_act = graph_ws = graph_arena = nullptr;
     }
 
     int64_t qkv_cols() const { return cfg.d + 2 * cfg.kv(); }
@@ -437,9 +446,10 @@ struct Model {
         (void)hipStreamSynchronize(ctx->stream);
         drop_graph();
         for (void *p : {(void *)w, (void *)cos_t, (void *)sin_t, (void *)act, (void *)tr.mem,
-                        (void *)grad, (void *)mom1, (void *)mom2, (void *)ranges})
+                        (void *)grad, (void *)mom1, (void *)mom2, (void *)ranges,
+                        (void *)fused_arena})
             if (p) (void)hipFree(p);
-        w = cos_t = sin_t = act = nullptr;
+        w = cos_t = sin_t = act = fused_arena = nullptr;
         tr.mem = grad = mom1 = mom2 = nullptr;
         ranges = nullptr;
     }
@@ -483,6 +493,80 @@ struct Model {
         check_hip(hipMemcpyAsync(cos_t, c.data(), tab * 4, hipMemcpyHostToDevice, ctx->stream), "rope upload");
         check_hip(hipMemcpyAsync(sin_t, s.data(), tab * 4, hipMemcpyHostToDevice, ctx->stream), "rope upload");
         check_hip(hipStreamSynchronize(ctx->stream), "rope tables sync");
+    }
+
+    FusedShape fused_shape(int64_t batch, int64_t seq) const {
+        FusedShape f;
+        f.batch = batch;
+        f.seq = seq;
+        f.d = cfg.d;
+        f.heads = cfg.heads;
+        f.kv_heads = cfg.kv_heads;
+        f.ff = cfg.ff;
+        f.ff_pad = ff_pad;
+        f.vocab = cfg.vocab;
+        f.layers = cfg.layers;
+        f.max_seq = cfg.max_seq;
+        f.tie = cfg.tie;
+        f.eps = cfg.eps;
+        f.weight_floats = n_dev;
+        return f;
+    }
+    bool use_fused(int64_t batch, int64_t seq, bool with_loss, bool want_logits) const {
+        return forward_path == 0 && with_loss && !want_logits &&
+               fused_forward_fits(*ctx, fused_shape(batch, seq));
+    }
+    // The arena laid out for (batch, seq): zeroed (counters, error word) with
+    // the rotary tables copied in. Never inside a graph capture: the first
+    // run of a shape is eager and prepares it.
+    void ensure_fused(int64_t batch, int64_t seq) {
+        if (fused_arena && fused_b == batch && fused_t == seq) return;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        check_hip(hipStreamIsCapturing(ctx->stream, &cs), "capture status");
+        if (cs != hipStreamCaptureStatusNone)
+            fail(MMH_ERR_OTHER, "fused forward: arena not prepared before capture");
+        const FusedLayout f = fused_layout(fused_shape(batch, seq));
+        check_hip(hipStreamSynchronize(ctx->stream), "sync");
+        if (f.floats > fused_floats) {
+            if (fused_arena) (void)hipFree(fused_arena);
+            fused_arena = nullptr;
+            fused_floats = 0;
+            fused_b = fused_t = 0;
+            check_hip(hipMalloc(&fused_arena, (size_t)f.floats * 4), "fused arena alloc");
+            fused_floats = f.floats;
+        }
+        check_hip(hipMemsetAsync(fused_arena, 0, (size_t)f.floats * 4, ctx->stream), "arena clear");
+        const size_t tab = (size_t)f.tab_floats * 4;
+        check_hip(hipMemcpyAsync(fused_arena + f.o_cos, cos_t, tab, hipMemcpyDeviceToDevice,
+                                 ctx->stream),
+                  "arena tables");
+        check_hip(hipMemcpyAsync(fused_arena + f.o_sin, sin_t, tab, hipMemcpyDeviceToDevice,
+                                 ctx->stream),
+                  "arena tables");
+        check_hip(hipStreamSynchronize(ctx->stream), "arena sync");
+        fused_b = batch;
+        fused_t = seq;
+        fused_check = false;
+    }
+    // Raises (and clears the word and the counters) when a fused launch since
+    // the last check reported an error; waits for queued work.
+    void check_fused() {
+        if (!fused_check || !fused_arena) return;
+        const FusedLayout f = fused_layout(fused_shape(fused_b, fused_t));
+        int32_t e = 0;
+        check_hip(hipMemcpyAsync(&e, fused_arena + f.o_err, 4, hipMemcpyDeviceToHost, ctx->stream),
+                  "fused error word");
+        check_hip(hipStreamSynchronize(ctx->stream), "fused error sync");
+        fused_check = false;
+        if (e == 0) return;
+        check_hip(hipMemsetAsync(fused_arena + f.o_ctl, 0, (size_t)(f.o_cos - f.o_ctl) * 4,
+                                 ctx->stream),
+                  "fused reset");
+        check_hip(hipStreamSynchronize(ctx->stream), "fused reset sync");
+        fail(MMH_ERR_DEVICE, std::string("fused forward failed:") +
+                                 ((e & 1) ? " a dependency wait timed out;" : "") +
+                                 ((e & 2) ? " more workgroups landed on one XCD than its team holds;" : "") +
+                                 ((e & 4) ? " row blocks were left uncombined;" : ""));
     }
 
     // Checks of model.rs:134-148 and the id ranges (ops_shape.rs:250-252,
@@ -544,6 +628,22 @@ struct Model {
         if (with_loss && !staged_targets) fail(MMH_ERR_ARGUMENT, "no targets staged");
         Context &c = *ctx;
         const int64_t d = cfg.d, V = cfg.vocab;
+        if (!prof && use_fused(batch, seq, with_loss, want_logits)) {
+            ensure_fused(batch, seq);
+            FusedArgs fa;
+            fa.shape = fused_shape(batch, seq);
+            fa.w = w;
+            fa.off_block0 = off_block(0);
+            fa.block_floats = dev_block();
+            fa.off_final_norm = off_final_norm();
+            fa.ids = ids;
+            fa.tgt = tgt;
+            fa.loss = loss;
+            fa.arena = fused_arena;
+            launch_fused_forward(c, fa);
+            fused_check = true;
+            return;
+        }
         timed(prof, MMH_PROF_EMBEDDING, [&] { launch_embedding(c, embed(), d, ids, n, x); });
         BlockRun r;
         r.cos_t = cos_t;
@@ -610,11 +710,16 @@ struct Model {
     // The graph holds no memset or allocation: only kernel launches.
     void run_staged(int64_t batch, int64_t seq) {
         if (graph_exec && graph_b == batch && graph_t == seq && graph_act == act &&
-            graph_ws == ctx->ws[0] && staged_n == batch * seq && staged_targets) {
+            graph_ws == ctx->ws[0] && graph_arena == fused_arena && fused_b == batch &&
+            fused_t == seq && staged_n == batch * seq && staged_targets) {
             check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
             return;
         }
-        if (!(warm_b == batch && warm_t == seq && warm_act == act)) {
+        // eager first for a new shape, new activations, or a fused arena laid
+        // out for another shape (it is prepared outside any capture)
+        const bool arena_ready = !use_fused(batch, seq, true, false) ||
+                                 (fused_arena && fused_b == batch && fused_t == seq);
+        if (!(warm_b == batch && warm_t == seq && warm_act == act) || !arena_ready) {
             enqueue(batch, seq, true, false);
             warm_b = batch;
             warm_t = seq;
@@ -637,6 +742,7 @@ struct Model {
         graph_t = seq;
         graph_act = act;
         graph_ws = ctx->ws[0];
+        graph_arena = fused_arena;
         check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
     }
 
@@ -653,6 +759,7 @@ struct Model {
                                      hipMemcpyDeviceToHost, c.stream),
                       "logits download");
         check_hip(hipStreamSynchronize(c.stream), "forward sync");
+        check_fused();
     }
 
     // ---------------------------------------------------------------- training
@@ -1260,6 +1367,24 @@ int32_t mmh_model_read_loss(mmh_handle model_h, float *loss_host) {
         check_hip(hipMemcpyAsync(loss_host, m.loss, 4, hipMemcpyDeviceToHost, m.ctx->stream),
                   "loss download");
         check_hip(hipStreamSynchronize(m.ctx->stream), "loss sync");
+        m.check_fused();
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_set_forward_path(mmh_handle model_h, int32_t path) {
+    return guard([&] {
+        if (path != MMH_PATH_AUTO && path != MMH_PATH_PER_OP)
+            fail(MMH_ERR_ARGUMENT, "forward path must be MMH_PATH_AUTO or MMH_PATH_PER_OP");
+        Model &m = model(model_h);
+        if (m.forward_path != path) {
+            m.ctx->select();
+            (void)hipStreamSynchronize(m.ctx->stream);
+            m.drop_graph();
+            m.warm_b = m.warm_t = 0;
+            m.warm_act = nullptr;
+            m.forward_path = path;
+        }
         return MMH_OK;
     });
 }

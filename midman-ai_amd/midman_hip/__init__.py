@@ -122,6 +122,7 @@ _SIGNATURES = {
     "mmh_model_stage": [_h, _i32p, _i32p, _i64, _i64],
     "mmh_model_run_staged": [_h, _i64, _i64],
     "mmh_model_read_loss": [_h, _f32p],
+    "mmh_model_set_forward_path": [_h, _i32],
     "mmh_model_profile": [_h, _i64, _i64, _f32p, _i32p],
     "mmh_rms_norm_backward": [_h, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp],
     "mmh_apply_rope_backward": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
@@ -922,6 +923,10 @@ class Batcher(_Handle):
 
 # ---- the model: midman-model/src/model.rs ------------------------------------------
 
+# mmh_model_set_forward_path
+PATH_AUTO = 0
+PATH_PER_OP = 1
+
 CONFIG_FIELDS = ("vocab_size", "d_model", "n_layers", "n_heads", "n_kv_heads", "d_ff",
                  "max_seq_len", "rope_theta", "norm_eps", "tie_embeddings")
 
@@ -1027,6 +1032,11 @@ class Model:
         loss = ctypes.c_float()
         check(lib().mmh_model_read_loss(self.handle, ctypes.byref(loss)))
         return loss.value
+
+    def set_forward_path(self, path: int):
+        """PATH_AUTO: loss-only forwards of models that fit run as one fused
+        launch; PATH_PER_OP: always the per-operation kernels."""
+        check(lib().mmh_model_set_forward_path(self.handle, path))
 
     def profile(self, batch: int, seq: int) -> dict:
         """One staged run with per-launch HIP events: {class: (ms, launches)}."""

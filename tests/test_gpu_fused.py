@@ -1,0 +1,118 @@
+"""GPU parity of the fused loss-only forward (fused_forward.hip: the whole of
+model.rs:127-183 as one persistent launch, per-XCD teams of workgroups).
+
+Every case runs the same model and tokens through the fused launch
+(MMH_PATH_AUTO) and through the per-operation kernels (MMH_PATH_PER_OP) and
+compares both with the oracle. Tolerances: fused vs oracle <= 1e-4 relative
+(the stated loss target); fused vs per-operation <= 2e-6 relative (two f32
+paths of the same arithmetic in different orders); repeated fused runs and
+graph replays bit-identical (fixed reduction orders, no atomics on data).
+"""
+import numpy as np
+import pytest
+
+import midman_hip as mh
+import mm_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def oracle_config(cfg):
+    return O.config(*[int(v) for v in cfg[:7]], float(cfg[7]), float(cfg[8]), bool(cfg[9]))
+
+
+def both_paths(m, x, y, batch, seq):
+    m.set_forward_path(mh.PATH_AUTO)
+    fused = float(m.loss(x, y, batch, seq))
+    again = float(m.loss(x, y, batch, seq))
+    m.set_forward_path(mh.PATH_PER_OP)
+    per_op = float(m.loss(x, y, batch, seq))
+    m.set_forward_path(mh.PATH_AUTO)
+    return fused, again, per_op
+
+
+@pytest.mark.parametrize("preset,batch,seq", [("tiny", 8, 256), ("smoke", 2, 32), ("smoke", 4, 128)])
+def test_fused_presets(ctx, preset, batch, seq):
+    print(f"\n[fused] {preset} B{batch} T{seq} seed 0", flush=True)
+    cfg = mh.PRESETS[preset]
+    m = mh.Model.new(ctx, cfg, 0)
+    try:
+        x, y = m.lab_tokens(batch, seq)
+        fused, again, per_op = both_paths(m, x, y, batch, seq)
+        c = oracle_config(cfg)
+        w_ref, _, _ = O.lab_setup(c, 0, batch, seq)
+        ref = float(O.forward_loss(c, w_ref, x, y, batch, seq, want_logits=False)[0])
+        print(f"  fused {fused:.7f} per-op {per_op:.7f} oracle {ref:.7f}", flush=True)
+        assert fused == again
+        assert abs(fused - per_op) <= 2e-6 * per_op
+        assert abs(fused - ref) <= 1e-4 * ref
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("cfg,batch,seq", [
+    # hd 32, GQA, untied head, V ending inside a 256-row block, ragged T:
+    # XCD 0 owns sequences 0 and 8, the others one each
+    ([1000, 128, 2, 4, 2, 96, 64, 10000.0, 1e-5, 0], 9, 45),
+    # hd 16, one token: a single row in the whole launch
+    ([50, 64, 2, 4, 4, 40, 16, 10000.0, 1e-5, 1], 1, 1),
+    # d 256 (K = 256 steps over both K-groups), 8 heads of 32, 2 kv heads,
+    # ff 100 (gate/up padded to 128 pairs), 16 sequences: two per XCD
+    ([300, 256, 1, 8, 2, 100, 64, 500.0, 1e-6, 1], 16, 64),
+    # T = 257: nine key tiles, so a wave walks two; a one-row last block
+    ([257, 64, 1, 4, 2, 64, 300, 10000.0, 1e-5, 1], 2, 257),
+    # 20 sequences of 33 rows: XCDs 0-3 own three, 4-7 two; partial blocks
+    ([77, 96, 2, 3, 1, 36, 40, 10000.0, 1e-5, 0], 20, 33),
+])
+def test_fused_shapes_against_oracle(ctx, cfg, batch, seq):
+    print(f"\n[fused] {cfg[:7]} tie={cfg[9]} B{batch} T{seq}", flush=True)
+    c = oracle_config(cfg)
+    w = O.init_weights(c, O.rng(41), std=0.1)
+    r = np.random.default_rng(batch * 1000 + seq)
+    x = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    y = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    m = mh.Model.from_weights(ctx, cfg, w)
+    try:
+        fused, again, per_op = both_paths(m, x, y, batch, seq)
+        ref = float(O.forward_loss(c, w, x, y, batch, seq, want_logits=False)[0])
+        print(f"  fused {fused:.7f} per-op {per_op:.7f} oracle {ref:.7f}", flush=True)
+        assert fused == again
+        assert abs(fused - per_op) <= 2e-6 * per_op
+        assert abs(fused - ref) <= 1e-4 * ref
+    finally:
+        m.close()
+
+
+def test_fused_graph_replays_and_reshapes(ctx):
+    # run_staged captures the fused launch into a graph; replays interleaved
+    # with eager fused runs, per-operation runs and a run at another shape
+    # (the arena is laid out again) must keep returning the eager loss.
+    cfg = mh.PRESETS["tiny"]
+    print("\n[fused graph] tiny B8 T256 / B3 T100", flush=True)
+    m = mh.Model.new(ctx, cfg, 7)
+    try:
+        x, y = m.lab_tokens(8, 256)
+        x2, y2 = m.lab_tokens(3, 100)
+        eager = float(m.loss(x, y, 8, 256))
+        eager2 = float(m.loss(x2, y2, 3, 100))
+        for i in range(8):
+            m.stage(x, y, 8, 256)
+            m.run_staged(8, 256)
+            assert m.read_loss() == eager, i
+            if i % 3 == 1:
+                assert float(m.loss(x2, y2, 3, 100)) == eager2
+            if i % 3 == 2:
+                m.set_forward_path(mh.PATH_PER_OP)
+                assert abs(float(m.loss(x, y, 8, 256)) - eager) <= 2e-6 * eager
+                m.set_forward_path(mh.PATH_AUTO)
+    finally:
+        m.close()
+
+
+def test_forward_path_argument(ctx):
+    m = mh.Model.new(ctx, mh.PRESETS["smoke"], 1)
+    try:
+        with pytest.raises(mh.MidmanError):
+            m.set_forward_path(2)
+    finally:
+        m.close()
