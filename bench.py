@@ -197,7 +197,7 @@ def time_data(mh, m, B, T, steps, shards=4, shard_tokens=1 << 22, eval_batches=8
 
 
 def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=False,
-               shards=False):
+               shards=False, per_op=False):
     cfg = mh.PRESETS[preset]
     t0 = time.time()
     m = mh.Model.new(ctx, cfg, 0)
@@ -214,6 +214,21 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
     ctx.synchronize()
     loss = m.read_loss()
     ms_step = ms / steps
+    # the same staged step on the per-operation kernels (the default path of a
+    # model the fused launch takes is that launch)
+    per_op_ms = None
+    if per_op:
+        m.set_forward_path(mh.PATH_PER_OP)
+        for _ in range(warmup):
+            m.run_staged(B, T)
+        ctx.synchronize()
+        ctx.timer_start()
+        for _ in range(steps):
+            m.run_staged(B, T)
+        per_op_ms = ctx.timer_stop() / steps
+        ctx.synchronize()
+        m.read_loss()
+        m.set_forward_path(mh.PATH_AUTO)
     # the same step through the host-buffer boundary (ids upload + loss download)
     t1 = time.perf_counter()
     for _ in range(max(1, steps // 2)):
@@ -235,6 +250,7 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
             log(f"shard-fed timing skipped: {e}")
     m.close()
     return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
+            "per_op_ms_per_step": per_op_ms,
             "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg,
             "train": train, "checkpoint": ckpt, "data": data}
 
@@ -480,9 +496,10 @@ def main():
         log("copy probe: add over 2^26 floats done")
 
     if a.tiny_only:
-        tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup)
+        tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup, per_op=True)
         log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
-            f"loss {tiny['loss']:.5f}")
+            f"loss {tiny['loss']:.5f} (one fused launch; per-operation kernels "
+            f"{tiny['per_op_ms_per_step']:.4f} ms/step, kernel classes below)")
         for k, (ms, nl) in tiny["profile"].items():
             log(f"  {k}: {ms:.4f} ms over {nl} launches (HIP events per launch)")
         ctx.close()
@@ -510,8 +527,9 @@ def main():
         log(f"{b['workload']}: {b['ms']} ms, {b['tflops']} TFLOP/s")
     tiny = None
     if not a.no_tiny:
-        tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5))
-        log(f"tiny: {tiny['ms_per_step']:.3f} ms/step, {tiny['tokens_per_s']:.0f} tok/s")
+        tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5), per_op=True)
+        log(f"tiny: {tiny['ms_per_step']:.3f} ms/step, {tiny['tokens_per_s']:.0f} tok/s "
+            f"(per-operation kernels {tiny['per_op_ms_per_step']:.3f} ms/step)")
 
     flops = model_flops(large["cfg"], 4, 1024)
     nbytes = model_bytes(large["cfg"], 4, 1024)
@@ -621,6 +639,8 @@ def main():
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),
+                "path": "one fused persistent launch (fused_forward.hip)",
+                "per_op_ms_per_step": round(tiny["per_op_ms_per_step"], 4),
                 "pcie_inclusive_tokens_per_s": round(tiny["pcie_inclusive_tokens_per_s"], 1),
                 "cpu_baseline": tiny_cpu},
             "gemm_sweep_tflops": sweep,
