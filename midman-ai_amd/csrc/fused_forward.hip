@@ -58,8 +58,10 @@ constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor: read
 constexpr int kSpinLimit = 1 << 18;
 constexpr int kLdsFloats = 8 * 32 * 33 + 2 * 8 * 32;
 
-// task stages within a layer, then the head and the combine
-enum : int { ST_Q = 0, ST_A = 1, ST_O = 2, ST_G = 3, ST_D = 4 };
+// task stages within a layer (stage 2, the O projection, rides on the
+// attention tasks and the gate/up tasks' loads; its counter slot is unused),
+// then the head (5)
+enum : int { ST_Q = 0, ST_A = 1, ST_G = 3, ST_D = 4 };
 
 __device__ __forceinline__ Rsrc rsrc(const void *p, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), 0, (int)bytes, 0x00020000);
@@ -115,13 +117,13 @@ struct FusedP {
     int32_t *err;         // error bits (a word of the arena, also addressed here)
     uint32_t w_bytes, f_bytes, i_bytes, tgt_off;
     // arena regions (float offsets)
-    uint32_t o_x, o_cb, o_h, o_qkv, o_part, o_zt, o_rl, o_p64, o_ctl, o_err, o_cos, o_sin;
+    uint32_t o_x, o_h, o_qkv, o_part, o_zt, o_rl, o_p64, o_ctl, o_err, o_cos, o_sin, o_op, o_x2;
     uint32_t ctl_ints;
     int B, T, d, H, Hkv, ff, ff_pad, V, L, tie, qc, kvw, n;
     float eps, scale;
     // weights (floats): layer l's block at blk0 + l * blk, then its parts
     int blk0, blk, o_wqkv, o_wo, o_mn, o_wgu, o_wd, o_fn, o_head;
-    int nrb, smax, nsi, nq_c, no_c, ng_c, nd_c, nh_c;
+    int nrb, smax, nsi, nq_c, ng_c, nd_c, nh_c;
     int hb, nh_t;  // head: 256-row vocabulary blocks per task, tasks per row block
 };
 
@@ -312,8 +314,11 @@ __device__ __forceinline__ void gemm_run(int tid, const FusedP &p, const Res &R,
 // 512 threads cover the 32 rows), each with d / 64 float4s; the row's sum of
 // squares meets over the 16 lanes by XOR exchanges, so every lane holds the
 // same sum. AS 0: rows of x (sc1 loads); AS 1: the embedding rows of the ids
-// (weights), also stored as the rows of x when xcopy. Rows past `rows`
-// repeat the last one.
+// (weights), also stored as the rows of x when xcopy; AS 2: the rows of x
+// plus the heads' O-projection partials (x + ((p_0 + p_1) + ...), block.rs:79),
+// stored as the rows of x2 when xcopy (the down projection's residual; x
+// itself stays as it is while the row block's other gate/up tasks read it).
+// Rows past `rows` repeat the last one.
 template <int AS>
 __device__ __forceinline__ void stage_norm_rows(int tid, const FusedP &p, const Res &R, int row0,
                                                 int rows, const float *nw, float *xs, bool xcopy) {
@@ -329,11 +334,29 @@ __device__ __forceinline__ void stage_norm_rows(int tid, const FusedP &p, const 
     }
     float4 v[4];
     float ss = 0.0f;
+    if (AS == 2) {
+        const uint32_t pb = 4u * (p.o_op + (uint32_t)row * (uint32_t)p.H * (uint32_t)d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int k = 4 * (tl + 16 * i);
+            if (k < d) {
+                float4 sm = ld4<kDev>(R.f, pb + 4u * k);
+                for (int h2 = 1; h2 < p.H; ++h2) {
+                    const float4 pv = ld4<kDev>(R.f, pb + 4u * (h2 * d + k));
+                    sm = make_float4(__fadd_rn(sm.x, pv.x), __fadd_rn(sm.y, pv.y), __fadd_rn(sm.z, pv.z),
+                                     __fadd_rn(sm.w, pv.w));
+                }
+                const float4 xv = ld4<kDev>(R.f, base + 4u * k);
+                v[i] = make_float4(__fadd_rn(xv.x, sm.x), __fadd_rn(xv.y, sm.y), __fadd_rn(xv.z, sm.z),
+                                   __fadd_rn(xv.w, sm.w));
+            }
+        }
+    }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int k = 4 * (tl + 16 * i);
         if (k < d) {
-            v[i] = AS == 1 ? ld4<0>(R.w, base + 4u * k) : ld4<kDev>(R.f, base + 4u * k);
+            if (AS != 2) v[i] = AS == 1 ? ld4<0>(R.w, base + 4u * k) : ld4<kDev>(R.f, base + 4u * k);
             ss = __fadd_rn(ss, __fmul_rn(v[i].x, v[i].x));
             ss = __fadd_rn(ss, __fmul_rn(v[i].y, v[i].y));
             ss = __fadd_rn(ss, __fmul_rn(v[i].z, v[i].z));
@@ -350,10 +373,10 @@ __device__ __forceinline__ void stage_norm_rows(int tid, const FusedP &p, const 
     for (int i = 0; i < 4; ++i) {
         const int k = 4 * (tl + 16 * i);
         if (k < d) {
-            if (AS == 1 && xcopy && r < rows)
+            if (AS != 0 && xcopy && r < rows)
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(u32x4, v[i]), R.f,
-                    4u * (p.o_x + (uint32_t)row * (uint32_t)d + k), 0, 0);
+                    4u * ((AS == 2 ? p.o_x2 : p.o_x) + (uint32_t)row * (uint32_t)d + k), 0, 0);
             const float4 w = *reinterpret_cast<const float4 *>(nw + k);
             *reinterpret_cast<float4 *>(xs + r * xst + k) =
                 make_float4(__fmul_rn(__fmul_rn(v[i].x, inv), w.x), __fmul_rn(__fmul_rn(v[i].y, inv), w.y),
@@ -429,7 +452,8 @@ __device__ __forceinline__ void share_block(int tid, float *lds, floatx16 &acc) 
 // with 8 waves taking the key tiles round-robin.
 template <int HD>
 __device__ __forceinline__ void attention_task(int tid, const FusedP &p, const Res &R, float *lds,
-                                               uint32_t qkv_off, int s, int hh, int qb) {
+                                               uint32_t qkv_off, int s, int hh, int qb,
+                                               float *ctx) {
     constexpr int NS = HD / 2;
     constexpr int OS = HD + 1;
     float *sm_o = lds;                   // [8][32 * OS]
@@ -558,13 +582,10 @@ __device__ __forceinline__ void attention_task(int tid, const FusedP &p, const R
     __syncthreads();
     for (int idx = tid; idx < 32 * HD; idx += kNT) {
         const int jr = idx / HD, c = idx - jr * HD;
-        const int q = q0 + jr;
-        if (q < T) {
-            float v = sm_o[jr * OS + c];
+        float v = sm_o[jr * OS + c];
 #pragma unroll
-            for (int w = 1; w < 8; ++w) v += sm_o[w * 32 * OS + jr * OS + c];
-            st1(R.f, 4u * (p.o_cb + (rbase + (uint32_t)q) * (uint32_t)p.d + hh * HD + c), v);
-        }
+        for (int w = 1; w < 8; ++w) v += sm_o[w * 32 * OS + jr * OS + c];
+        ctx[jr * (HD + 4) + c] = v;
     }
 }
 
@@ -627,9 +648,9 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     // this XCD's sequences: s = x + 8 j
     const int S = x < p.B ? (p.B - x + 7) >> 3 : 0;
     const int nrb = p.nrb;
-    const int nQ = S * nrb * p.nq_c, nA = S * p.H * nrb, nO = S * nrb * p.no_c,
-              nG = S * nrb * p.ng_c, nD = S * nrb * p.nd_c;
-    const int LT = nQ + nA + nO + nG + nD;
+    const int nQ = S * nrb * p.nq_c, nA = S * p.H * nrb, nG = S * nrb * p.ng_c,
+              nD = S * nrb * p.nd_c;
+    const int LT = nQ + nA + nG + nD;
     const int nH = S * nrb * p.nh_t;
     const int total = on_xcd ? p.L * LT + nH : 0;
     const int d = p.d, T = p.T;
@@ -661,13 +682,7 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                 r /= p.H;
                 j = r % S;
                 q = nrb - 1 - r / S;
-            } else if ((r -= nA) < nO) {
-                st = ST_O;
-                c = r % p.no_c;
-                r /= p.no_c;
-                j = r % S;
-                q = r / S;
-            } else if ((r -= nO) < nG) {
+            } else if ((r -= nA) < nG) {
                 st = ST_G;
                 c = r % p.ng_c;
                 r /= p.ng_c;
@@ -700,8 +715,7 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
         const bool isq = st == ST_Q;
         const int ncol = isq ? p.qc : 2 * p.ff_pad;    // Q / G output columns
         const int qg_wo = isq ? wb + p.o_wqkv : wb + p.o_wgu;
-        const int od_wo = st == ST_O ? wb + p.o_wo : wb + p.o_wd;
-        const int od_k = st == ST_O ? d : p.ff;
+        const int od_wo = wb + p.o_wd, od_k = p.ff;  // down
         const int hns = (d + 31) >> 5;                 // head: K steps per vocabulary block
         const int hb0 = c * p.hb, hb1 = min(p.nh_c, hb0 + p.hb);  // its 256-row blocks
         int tg = 0;                                    // head: the lane's row's target
@@ -724,7 +738,16 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                     s_sn[i] = ld1<0>(R.f, 4u * p.o_sin + ti);
                 }
             }
-        } else if (st == ST_O || st == ST_D) {
+        } else if (st == ST_A) {
+            // the head's HD rows of Wo for this wave's 32 output columns (waves
+            // below d / 32): gp.v[j] = Wo[HD hh + 16 (l/32) + j][32 w + l%32]
+            if (32 * wave < d) {
+                const uint32_t vb = 4u * ((uint32_t)(wb + p.o_wo) + (uint32_t)(hh * HD + 16 * lk) * (uint32_t)d +
+                                          32u * wave + lr);
+#pragma unroll
+                for (int jj = 0; jj < 16; ++jj) gp.v[jj] = ld1s<0>(R.w, vb, 4 * jj * d);
+            }
+        } else if (st == ST_D) {
             gemm_fetch_b<1>(tid, R, od_wo, d, 32 * c, d, od_k, gp);
         } else if (st == 5) {
             for (int i = tid; i < d; i += kNT) s_nw[i] = ld1<0>(R.w, 4u * (uint32_t)(p.o_fn + i));
@@ -744,8 +767,7 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
             };
             if (st == ST_Q && l > 0) wait((l - 1) * 5 + ST_D, q, 1, p.nd_c);
             if (st == ST_A) wait(l * 5 + ST_Q, 0, q + 1, p.nq_c);
-            if (st == ST_O) wait(l * 5 + ST_A, q, 1, p.H);
-            if (st == ST_G) wait(l * 5 + ST_O, q, 1, p.no_c);
+            if (st == ST_G) wait(l * 5 + ST_A, q, 1, p.H);  // every head's O partial
             if (st == ST_D) wait(l * 5 + ST_G, q, 1, p.ng_c);
             if (st == 5) wait((p.L - 1) * 5 + ST_D, q, 1, p.nd_c);
             if (lane == 0) s_ok = ok;
@@ -758,8 +780,10 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
             // (128-column blocks, two K groups); G: SwiGLU into h (256 columns)
             if (isq && l == 0)  // the embedding rows; column block 0 also stores them as x
                 stage_norm_rows<1>(tid, p, R, row0, rows, s_nw, s_xs, c == 0);
-            else
+            else if (isq)
                 stage_norm_rows<0>(tid, p, R, row0, rows, s_nw, s_xs, false);
+            else  // x after the O projection; column block 0 stores it as x2
+                stage_norm_rows<2>(tid, p, R, row0, rows, s_nw, s_xs, c == 0);
             __syncthreads();
             floatx16 acc;
 #pragma unroll
@@ -805,28 +829,24 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                             __fmul_rn(silu_f(g), u));
                 }
             }
-        } else if (st == ST_O || st == ST_D) {
-            // x += A . W over one 32-column block, K split over the 8 waves; wave
-            // w adds the residual to registers w and w + 8
+        } else if (st == ST_D) {
+            // x = x2 + h . Wd over one 32-column block, K split over the 8 waves;
+            // wave w adds the residual to registers w and w + 8
             const int col = 32 * c + lr;
             float res[2];
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const int rl = row_local(wave + 8 * i, lk);
                 res[i] = ld1<kDev>(R.f, rl < rows && col < d
-                                            ? 4u * (p.o_x + (uint32_t)(row0 + rl) * (uint32_t)d + col)
+                                            ? 4u * (p.o_x2 + (uint32_t)(row0 + rl) * (uint32_t)d + col)
                                             : kOOB);
             }
             floatx16 acc;
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
             float ss = 0.0f;
-            if (st == ST_O)
-                gemm_run<1, 0, false>(tid, p, R, p.o_cb, d, ra, false, gp, od_wo, d, 32 * c, d, d,
-                                      nullptr, acc, ss);
-            else
-                gemm_run<1, 0, false>(tid, p, R, p.o_h, p.ff, ra, false, gp, od_wo, d, 32 * c, d,
-                                      p.ff, nullptr, acc, ss);
+            gemm_run<1, 0, false>(tid, p, R, p.o_h, p.ff, ra, false, gp, od_wo, d, 32 * c, d, p.ff,
+                                  nullptr, acc, ss);
             share_block<1>(tid, lds, acc);
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
@@ -836,7 +856,31 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                         __fadd_rn(res[i], acc[i]));
             }
         } else if (st == ST_A) {
-            attention_task<HD>(tid, p, R, lds, qkv_off, s, hh, q);
+            // attention, then this head's share of the O projection, ctx_h .
+            // Wo[head rows] (32 x d, K = HD), as a partial; the gate/up tasks of
+            // the row block add the partials in head order to the residual
+            float *ctx = s_xs;  // [32][HD + 4]
+            attention_task<HD>(tid, p, R, lds, qkv_off, s, hh, q, ctx);
+            __syncthreads();
+            if (32 * wave < d) {
+                floatx16 acc;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
+#pragma unroll
+                for (int jj = 0; jj < 16; ++jj) {
+                    const int k = 16 * lk + jj;
+                    const float a = k < HD ? ctx[lr * (HD + 4) + k] : 0.0f;
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a, k < HD ? gp.v[jj] : 0.0f, acc, 0, 0, 0);
+                }
+                const int col = 32 * wave + lr;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int rl = row_local(e, lk);
+                    if (rl < rows)
+                        st1(R.f, 4u * (p.o_op + ((uint32_t)(row0 + rl) * (uint32_t)p.H + hh) * (uint32_t)d + col),
+                            acc[e]);
+                }
+            }
         } else {
             // logits^T of 32 vocabulary rows per wave and 256-row block against the
             // block's normalised rows (staged in LDS): lane l holds row l % 32,
@@ -1052,7 +1096,8 @@ FusedLayout fused_layout(const FusedShape &s) {
         return at;
     };
     f.o_x = take(n * s.d);
-    f.o_cb = take(n * s.d);
+    f.o_op = take(n * s.heads * s.d);
+    f.o_x2 = take(n * s.d);
     f.o_h = take(n * s.ff);
     f.o_qkv = take(s.layers * n * f.qc);
     f.o_part = take(n * ((s.vocab + 255) / 256) * 2);
@@ -1084,7 +1129,8 @@ void launch_fused_forward(Context &ctx, const FusedArgs &a) {
     p.tgt_off = (uint32_t)(a.tgt - a.ids);
     p.i_bytes = (uint32_t)((p.tgt_off + n) * 4);
     p.o_x = (uint32_t)f.o_x;
-    p.o_cb = (uint32_t)f.o_cb;
+    p.o_op = (uint32_t)f.o_op;
+    p.o_x2 = (uint32_t)f.o_x2;
     p.o_h = (uint32_t)f.o_h;
     p.o_qkv = (uint32_t)f.o_qkv;
     p.o_part = (uint32_t)f.o_part;
@@ -1124,9 +1170,9 @@ void launch_fused_forward(Context &ctx, const FusedArgs &a) {
     p.smax = (int)f.smax;
     p.nsi = (int)f.nsi;
     p.nq_c = (int)((f.qc + 127) / 128);
-    p.no_c = (int)((s.d + 31) / 32);
+
     p.ng_c = (int)((2 * s.ff_pad + 255) / 256);
-    p.nd_c = p.no_c;
+    p.nd_c = (int)((s.d + 31) / 32);
     p.nh_c = (int)((s.vocab + 255) / 256);
     // head tasks: about one per team workgroup over the row blocks of an XCD
     const int team = ctx.cu_count / 8;

@@ -223,8 +223,8 @@ struct FusedShape {
 // tables, as float offsets of one allocation.
 struct FusedLayout {
     int64_t qc = 0, nrb = 0, smax = 0, nsi = 0, ctl_ints = 0, tab_floats = 0;
-    int64_t o_x = 0, o_cb = 0, o_h = 0, o_qkv = 0, o_part = 0, o_zt = 0, o_rl = 0, o_p64 = 0,
-            o_ctl = 0, o_err = 0, o_cos = 0, o_sin = 0;
+    int64_t o_x = 0, o_h = 0, o_qkv = 0, o_part = 0, o_zt = 0, o_rl = 0, o_p64 = 0,
+            o_ctl = 0, o_err = 0, o_cos = 0, o_sin = 0, o_op = 0, o_x2 = 0;
     int64_t floats = 0;
 };
 struct FusedArgs {
