@@ -1089,10 +1089,14 @@ FusedLayout fused_layout(const FusedShape &s) {
     f.nsi = 5 * s.layers + 2;
     f.ctl_ints = 64 + 8 * f.nsi * f.smax * f.nrb;
     f.tab_floats = s.max_seq * (hd / 2);
-    int64_t o = 0;
+    // every region is fenced by a guard band of kBand floats on each side
+    int64_t o = FusedLayout::kBand;
+    f.bands[f.nbands++] = 0;
     auto take = [&](int64_t floats) {
         const int64_t at = o;
         o += al(floats);
+        f.bands[f.nbands++] = o;
+        o += FusedLayout::kBand;
         return at;
     };
     f.o_x = take(n * s.d);

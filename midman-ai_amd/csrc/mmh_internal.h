@@ -220,9 +220,13 @@ struct FusedShape {
     int64_t weight_floats = 0;  // the device weight layout's size
 };
 // The fused kernel's arena: every buffer it writes plus a copy of the rotary
-// tables, as float offsets of one allocation.
+// tables, as float offsets of one allocation, each region between guard
+// bands (filled with the model's guard word at allocation).
 struct FusedLayout {
+    static constexpr int64_t kBand = 64;  // guard band floats around each region
     int64_t qc = 0, nrb = 0, smax = 0, nsi = 0, ctl_ints = 0, tab_floats = 0;
+    int64_t bands[24] = {};  // float offsets of the guard bands
+    int nbands = 0;
     int64_t o_x = 0, o_h = 0, o_qkv = 0, o_part = 0, o_zt = 0, o_rl = 0, o_p64 = 0,
             o_ctl = 0, o_err = 0, o_cos = 0, o_sin = 0, o_op = 0, o_x2 = 0;
     int64_t floats = 0;

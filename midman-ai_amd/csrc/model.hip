@@ -536,6 +536,10 @@ struct Model {
             fused_floats = f.floats;
         }
         check_hip(hipMemsetAsync(fused_arena, 0, (size_t)f.floats * 4, ctx->stream), "arena clear");
+        for (int i = 0; i < f.nbands; ++i)
+            check_hip(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(fused_arena + f.bands[i]),
+                                        (int)kGuardBits, (size_t)FusedLayout::kBand, ctx->stream),
+                      "arena guard fill");
         const size_t tab = (size_t)f.tab_floats * 4;
         check_hip(hipMemcpyAsync(fused_arena + f.o_cos, cos_t, tab, hipMemcpyDeviceToDevice,
                                  ctx->stream),
@@ -559,9 +563,9 @@ struct Model {
         check_hip(hipStreamSynchronize(ctx->stream), "fused error sync");
         fused_check = false;
         if (e == 0) return;
-        check_hip(hipMemsetAsync(fused_arena + f.o_ctl, 0, (size_t)(f.o_cos - f.o_ctl) * 4,
-                                 ctx->stream),
+        check_hip(hipMemsetAsync(fused_arena + f.o_ctl, 0, (size_t)f.ctl_ints * 4, ctx->stream),
                   "fused reset");
+        check_hip(hipMemsetAsync(fused_arena + f.o_err, 0, 4, ctx->stream), "fused reset");
         check_hip(hipStreamSynchronize(ctx->stream), "fused reset sync");
         fail(MMH_ERR_DEVICE, std::string("fused forward failed:") +
                                  ((e & 1) ? " a dependency wait timed out;" : "") +
@@ -1090,7 +1094,13 @@ struct Model {
         check_hip(hipStreamSynchronize(ctx->stream), "guard check sync");
         uint64_t broken = 0;
         std::vector<uint32_t> host((size_t)kGuardFloats);
-        for (const auto *bands : {&act_bands, &tr_bands})
+        std::vector<float *> arena_bands;
+        if (fused_arena) {
+            const FusedLayout f = fused_layout(fused_shape(fused_b, fused_t));
+            for (int i = 0; i < f.nbands; ++i) arena_bands.push_back(fused_arena + f.bands[i]);
+        }
+        static_assert(FusedLayout::kBand == kGuardFloats, "one guard band size");
+        for (const auto *bands : {&act_bands, &tr_bands, &arena_bands})
             for (float *b : *bands) {
                 check_hip(hipMemcpy(host.data(), b, (size_t)kGuardFloats * 4,
                                     hipMemcpyDeviceToHost),

@@ -1,5 +1,6 @@
 """GPU parity of the fused loss-only forward (fused_forward.hip: the whole of
-model.rs:127-183 as one persistent launch, per-XCD teams of workgroups).
+model.rs:127-183 as one persistent launch, per-XCD teams of workgroups),
+and the guard bands around every region of its arena.
 
 Every case runs the same model and tokens through the fused launch
 (MMH_PATH_AUTO) and through the per-operation kernels (MMH_PATH_PER_OP) and
@@ -79,6 +80,9 @@ def test_fused_shapes_against_oracle(ctx, cfg, batch, seq):
         assert fused == again
         assert abs(fused - per_op) <= 2e-6 * per_op
         assert abs(fused - ref) <= 1e-4 * ref
+        # every region of the fused arena (and of the activations) kept its
+        # guard bands (kernels_avx.rs:368-390)
+        assert m.broken_guards() == 0
     finally:
         m.close()
 
