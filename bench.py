@@ -197,10 +197,12 @@ def time_data(mh, m, B, T, steps, shards=4, shard_tokens=1 << 22, eval_batches=8
 
 
 def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=False,
-               shards=False, per_op=False):
+               shards=False, per_op=False, only_per_op=False):
     cfg = mh.PRESETS[preset]
     t0 = time.time()
     m = mh.Model.new(ctx, cfg, 0)
+    if only_per_op:
+        m.set_forward_path(mh.PATH_PER_OP)
     log(f"{preset}: seeded init + upload {time.time() - t0:.1f}s, {m.num_parameters():,} params")
     x, y = m.lab_tokens(B, T)
     m.stage(x, y, B, T)
@@ -469,6 +471,9 @@ def main():
                     help="skip the back-to-back timing of the op-level bandwidth kernels")
     ap.add_argument("--no-mfma-probe", action="store_true",
                     help="skip the fp32 MFMA issue-rate probe (the measured ceiling)")
+    ap.add_argument("--tiny-per-op", action="store_true",
+                    help="with --tiny-only: time the per-operation kernels only (the path the "
+                         "tiny kernel trace in profiles/ covers)")
     ap.add_argument("--tiny-only", action="store_true",
                     help="time only the tiny preset's forward+loss and log it (no JSON line): "
                          "the command its kernel-trace profile is taken on")
@@ -496,10 +501,15 @@ def main():
         log("copy probe: add over 2^26 floats done")
 
     if a.tiny_only:
-        tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup, per_op=True)
-        log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
-            f"loss {tiny['loss']:.5f} (one fused launch; per-operation kernels "
-            f"{tiny['per_op_ms_per_step']:.4f} ms/step, kernel classes below)")
+        if a.tiny_per_op:
+            tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup, only_per_op=True)
+            log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
+                f"loss {tiny['loss']:.5f} (per-operation kernels, kernel classes below)")
+        else:
+            tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup, per_op=True)
+            log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
+                f"loss {tiny['loss']:.5f} (one fused launch; per-operation kernels "
+                f"{tiny['per_op_ms_per_step']:.4f} ms/step, kernel classes below)")
         for k, (ms, nl) in tiny["profile"].items():
             log(f"  {k}: {ms:.4f} ms over {nl} launches (HIP events per launch)")
         ctx.close()
@@ -527,7 +537,8 @@ def main():
         log(f"{b['workload']}: {b['ms']} ms, {b['tflops']} TFLOP/s")
     tiny = None
     if not a.no_tiny:
-        tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 50), max(a.warmup, 5), per_op=True)
+        tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 1000), max(a.warmup, 100),
+                          per_op=True)
         log(f"tiny: {tiny['ms_per_step']:.3f} ms/step, {tiny['tokens_per_s']:.0f} tok/s "
             f"(per-operation kernels {tiny['per_op_ms_per_step']:.3f} ms/step)")
 
