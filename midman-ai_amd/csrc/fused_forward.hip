@@ -44,6 +44,8 @@
 // so an index outside it reads zero / writes nothing instead of faulting.
 #include "mmh_internal.h"
 
+#include <type_traits>
+
 namespace mmh {
 namespace {
 
@@ -591,12 +593,13 @@ __device__ __forceinline__ void attention_task(int tid, const FusedP &p, const R
 
 // The head's A operand for vocabulary block b (256 rows), K step stp: the
 // wave's 32 vocabulary rows 256 b + 32 w + l % 32 (clamped to V - 1), k =
-// 32 stp + 16 (l / 32) + j, from the tied embedding [V, d] or lm_head [d, V].
+// 32 stp + 16 (l / 32) + j, from the tied embedding [V, d] (TIE) or lm_head [d, V].
+template <bool TIE>
 __device__ __forceinline__ void head_load_a(int tid, const FusedP &p, const Res &R, int b, int stp,
                                             int wave, float *a) {
     const int lane = tid & 63, lr = lane & 31, lk = lane >> 5;
     const int v = min(256 * b + 32 * wave + lr, p.V - 1);
-    if (p.tie) {
+    if constexpr (TIE) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const float4 ev = ld4s<0>(R.w, 4u * (uint32_t)v * (uint32_t)p.d + 64u * lk + 16u * i, 128 * stp);
@@ -755,7 +758,12 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
             // the first two K steps of the first block
 #pragma unroll
             for (int f = 0; f < 2; ++f)
-                if (f < hns) head_load_a(tid, p, R, hb0, f, wave, gp.v + 16 * f);
+                if (f < hns) {
+                    if (p.tie)
+                        head_load_a<true>(tid, p, R, hb0, f, wave, gp.v + 16 * f);
+                    else
+                        head_load_a<false>(tid, p, R, hb0, f, wave, gp.v + 16 * f);
+                }
         }
 
         // ---- dependencies
@@ -894,35 +902,52 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
             float m_run = -INFINITY, s_run = 0.0f;
-            auto head_step = [&](int stp, const float *a) __attribute__((always_inline)) {
-                float xb[16];
+            // K step stp: 16 MFMAs in four groups of 4, each group's four x
+            // values one LDS read, issued a group ahead (x0 holds the step's
+            // first group on entry and step nstp's first group on return), so
+            // no group waits for its read
+            auto head_step = [&](int stp, int nstp, const float *a, float4 &x0) __attribute__((always_inline)) {
+                float4 cur = x0;
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float4 v = *reinterpret_cast<const float4 *>(xr + 32 * stp + 4 * i);
-                    xb[4 * i + 0] = v.x;
-                    xb[4 * i + 1] = v.y;
-                    xb[4 * i + 2] = v.z;
-                    xb[4 * i + 3] = v.w;
+                for (int q = 0; q < 4; ++q) {
+                    const float4 nxt = *reinterpret_cast<const float4 *>(xr + (q < 3 ? 32 * stp + 4 * (q + 1) : 32 * nstp));
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * q + 0], cur.x, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * q + 1], cur.y, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * q + 2], cur.z, acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[4 * q + 3], cur.w, acc, 0, 0, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+                    cur = nxt;
                 }
-#pragma unroll
-                for (int jj = 0; jj < 16; ++jj)
-                    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[jj], xb[jj], acc, 0, 0, 0);
+                x0 = cur;
             };
+            float4 x0 = *reinterpret_cast<const float4 *>(xr);
             // block b's logits complete: the target logit out, the block's (max,
             // sum of exp) over the wave's 32 rows into the running pair
             auto head_block = [&](int b) __attribute__((always_inline)) {
                 const int v0 = 256 * b + 32 * wave;
-                float mx = -INFINITY, zt = 0.0f;
-                bool hit = false;
+                // (both tests below are wave-uniform: most blocks skip them)
+                // the target logit, where some lane's target is in these 32 rows
+                if (__any((unsigned)(tg - v0) < 32u)) {
+                    float zt = 0.0f;
+                    bool hit = false;
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int v = v0 + row_local(e, lk);
-                    zt = v == tg ? acc[e] : zt;
-                    hit = hit || v == tg;
-                    if (v >= p.V) acc[e] = -INFINITY;
-                    mx = fmaxf(mx, acc[e]);
+                    for (int e = 0; e < 16; ++e) {
+                        const int v = v0 + row_local(e, lk);
+                        zt = v == tg ? acc[e] : zt;
+                        hit = hit || v == tg;
+                    }
+                    if (hit && row_ok) st1(R.f, 4u * (p.o_zt + (uint32_t)ra), zt);
                 }
-                if (hit && row_ok) st1(R.f, 4u * (p.o_zt + (uint32_t)ra), zt);
+                // rows past the vocabulary, where it ends inside these 32
+                if (v0 + 32 > p.V) {
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        if (v0 + row_local(e, lk) >= p.V) acc[e] = -INFINITY;
+                }
+                float mx = -INFINITY;
+#pragma unroll
+                for (int e = 0; e < 16; ++e) mx = fmaxf(mx, acc[e]);
                 mx = pair32_max(mx);
                 float sum = 0.0f;
                 if (mx != -INFINITY) {
@@ -933,6 +958,11 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[e] = 0.0f;
             };
+            // one loop per head layout: with the layout chosen inside the
+            // loop, the compiler's wait for a register set covered the other
+            // set's newer loads as well (each set then waited out its loads)
+            auto head_loop = [&](auto tie_c) __attribute__((always_inline)) {
+            constexpr bool TIE = decltype(tie_c)::value;
             if ((hns & 1) == 0) {
                 // steps in pairs: register set 0 holds the even step, set 1 the odd
                 // one; each set is refilled two steps ahead (across blocks)
@@ -940,13 +970,24 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                 for (int b = hb0; b < hb1; ++b) {
 #pragma unroll 1
                     for (int stp = 0; stp < hns; stp += 2) {
-                        head_step(stp, gp.v);
-                        const bool wrap = stp + 2 >= hns;
-                        if (!wrap || b + 1 < hb1)
-                            head_load_a(tid, p, R, wrap ? b + 1 : b, wrap ? 0 : stp + 2, wave, gp.v);
-                        head_step(stp + 1, gp.v + 16);
-                        if (!wrap || b + 1 < hb1)
-                            head_load_a(tid, p, R, wrap ? b + 1 : b, wrap ? 1 : stp + 3, wave, gp.v + 16);
+                        head_step(stp, stp + 1, gp.v, x0);
+                        // every pair issues both sets' loads: the task's last
+                        // pair reloads its own rows (in range, never used), so
+                        // each path through the loop has the same loads in
+                        // flight and the compiler waits for a set only where
+                        // that set is used, two steps after its loads
+                        const bool wrap = stp + 2 >= hns, last = wrap && b + 1 >= hb1;
+                        const int nb = wrap && !last ? b + 1 : b;
+                        const int ns = wrap ? (last ? stp : 0) : stp + 2;
+                        // (scheduling barriers keep the loads where they are
+                        // written: the scheduler would sink them to the end)
+                        __builtin_amdgcn_sched_barrier(0);
+                        head_load_a<TIE>(tid, p, R, nb, ns, wave, gp.v);
+                        __builtin_amdgcn_sched_barrier(0);
+                        head_step(stp + 1, stp + 2 < hns ? stp + 2 : 0, gp.v + 16, x0);
+                        __builtin_amdgcn_sched_barrier(0);
+                        head_load_a<TIE>(tid, p, R, nb, ns + 1, wave, gp.v + 16);
+                        __builtin_amdgcn_sched_barrier(0);
                     }
                     head_block(b);
                 }
@@ -955,12 +996,17 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                 for (int b = hb0; b < hb1; ++b) {
 #pragma unroll 1
                     for (int stp = 0; stp < hns; ++stp) {
-                        if (b != hb0 || stp >= 2) head_load_a(tid, p, R, b, stp, wave, gp.v);
-                        head_step(stp, gp.v + (b == hb0 && stp == 1 ? 16 : 0));
+                        if (b != hb0 || stp >= 2) head_load_a<TIE>(tid, p, R, b, stp, wave, gp.v);
+                        head_step(stp, stp + 1 < hns ? stp + 1 : 0, gp.v + (b == hb0 && stp == 1 ? 16 : 0), x0);
                     }
                     head_block(b);
                 }
             }
+            };
+            if (p.tie)
+                head_loop(std::true_type{});
+            else
+                head_loop(std::false_type{});
             float *sm_m = lds, *sm_s = lds + 8 * 32;
             if (lk == 0) {
                 sm_m[wave * 32 + lr] = m_run;
