@@ -40,6 +40,28 @@ __global__ __launch_bounds__(256) void embedding_kernel(const float *__restrict_
     }
 }
 
+// Row-major form for float4 rows of d4 = RPW-dividing or 256-multiple
+// lengths: a workgroup owns RPW rows (256 / RPW threads each) and a thread
+// copies U float4s of its row, all U loads issued before the stores. The
+// row's id is read once (per thread group), not once per float4, and there
+// is no per-element index division.
+template <int RPW, int U>
+__global__ __launch_bounds__(256) void embedding_rows_kernel(const float *__restrict__ table,
+                                                             int64_t d, const int32_t *__restrict__ ids,
+                                                             int64_t n, float *__restrict__ out) {
+    constexpr int TPR = 256 / RPW;  // threads per row
+    const int64_t row = (int64_t)blockIdx.x * RPW + threadIdx.x / TPR;
+    if (row >= n) return;
+    const int t = threadIdx.x % TPR;
+    const float4 *__restrict__ src = reinterpret_cast<const float4 *>(table + (int64_t)ids[row] * d);
+    float4 *__restrict__ dst = reinterpret_cast<float4 *>(out + row * d);
+    float4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = src[t + u * TPR];
+#pragma unroll
+    for (int u = 0; u < U; ++u) dst[t + u * TPR] = v[u];
+}
+
 // ---- RMSNorm: norm.rs:36-38 -------------------------------------------------
 // One wave per row: sum of squares (wave reduction), mean = sum * (1/d),
 // inv = (mean + eps)^(-1/2), out = (x * inv) * w.
@@ -357,8 +379,26 @@ bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 void launch_embedding(Context &ctx, const float *table, int64_t d, const int32_t *ids_dev,
                       int64_t n, float *out) {
     const int vec = (d % 4 == 0) && al16(table) && al16(out);
-    hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(vec ? n * d / 4 : n * d)), dim3(256), 0,
-                       ctx.stream, table, d, ids_dev, n, out, vec);
+    const int64_t d4 = d / 4;
+    auto rows = [&](auto kernel, int rpw) {
+        hipLaunchKernelGGL(kernel, dim3((unsigned)((n + rpw - 1) / rpw)), dim3(256), 0, ctx.stream,
+                           table, d, ids_dev, n, out);
+    };
+    if (vec && d4 == 512)  // the large preset's rows
+        rows(embedding_rows_kernel<1, 2>, 1);
+    else if (vec && d4 == 256)
+        rows(embedding_rows_kernel<1, 1>, 1);
+    else if (vec && d4 == 1024)
+        rows(embedding_rows_kernel<1, 4>, 1);
+    else if (vec && d4 == 128)
+        rows(embedding_rows_kernel<2, 1>, 2);
+    else if (vec && d4 == 64)
+        rows(embedding_rows_kernel<4, 1>, 4);
+    else if (vec && d4 == 32)
+        rows(embedding_rows_kernel<8, 1>, 8);
+    else
+        hipLaunchKernelGGL(embedding_kernel, dim3(grid_for(vec ? n * d / 4 : n * d)), dim3(256), 0,
+                           ctx.stream, table, d, ids_dev, n, out, vec);
     check_hip(hipGetLastError(), "embedding launch");
 }
 

@@ -32,6 +32,17 @@ def rel_max(got, want):
     return float(np.max(np.abs(got.astype(np.float64) - want)) / max(np.max(np.abs(want)), 1e-30))
 
 
+@pytest.mark.parametrize("d", [128, 256, 512, 1024, 2048, 4096])
+def test_embedding_row_kernels_bit_exact(ctx, d):
+    # the row-per-workgroup gathers (1, 2, 4 or 8 rows per workgroup), with a
+    # row count that leaves the last workgroup partly empty
+    print(f"\n[embedding] d={d}", flush=True)
+    table = O.randn((300, d), 1.0, O.rng(d))
+    ids = np.random.default_rng(d).integers(0, 300, size=257).astype(np.int32)
+    out = mh.embedding(ctx, ctx.to_device(table), ids)
+    assert np.array_equal(out.numpy(), O.embedding(table, ids))
+
+
 def test_embedding_bit_exact_and_index_error(ctx):
     print("\n[embedding]", flush=True)
     table = O.randn((300, 48), 0.02, O.rng(5))
