@@ -266,6 +266,10 @@ int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
 #define MMH_PATH_AUTO 0
 #define MMH_PATH_PER_OP 1
 int32_t mmh_model_set_forward_path(mmh_handle model, int32_t path);
+/* 1 in *fused when the model's last queued forward (or the graph that
+ * mmh_model_run_staged replays) is the fused launch, else 0 (no reference
+ * counterpart; lets a caller or a test see which path MMH_PATH_AUTO took). */
+int32_t mmh_model_last_forward_fused(mmh_handle model, int32_t *fused);
 
 /* Kernel classes timed by mmh_model_profile. */
 #define MMH_PROF_EMBEDDING 0

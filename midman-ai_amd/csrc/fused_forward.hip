@@ -1103,12 +1103,34 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     for (int i = tid0; i < (int)p.ctl_ints; i += kNT) st1<kDev>(R.f, 4u * (p.o_ctl + i), 0.0f);
 }
 
+// One single-wave workgroup per CU, counted per XCD.
+__global__ __launch_bounds__(64) void xcd_probe_kernel(int *counts) {
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(counts + (xcc_id() & 15), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace
 
 // ---- host side -------------------------------------------------------------
 
-bool fused_forward_fits(const Context &ctx, const FusedShape &s) {
+bool probe_xcd_teams(Context &ctx) {
     if (ctx.cu_count < 8 || ctx.cu_count % 8 != 0) return false;
+    int *counts = nullptr;
+    int h[16] = {};
+    bool ok = hipMalloc(&counts, sizeof(h)) == hipSuccess;
+    ok = ok && hipMemset(counts, 0, sizeof(h)) == hipSuccess;
+    if (ok) {
+        hipLaunchKernelGGL(xcd_probe_kernel, dim3((unsigned)ctx.cu_count), dim3(64), 0, nullptr, counts);
+        ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
+             hipMemcpy(h, counts, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
+    }
+    if (counts) (void)hipFree(counts);
+    for (int x = 0; x < 16 && ok; ++x) ok = h[x] == (x < 8 ? ctx.cu_count / 8 : 0);
+    return ok;
+}
+
+bool fused_forward_fits(const Context &ctx, const FusedShape &s) {
+    if (!ctx.xcd_teams || ctx.cu_count < 8 || ctx.cu_count % 8 != 0) return false;
     if (s.heads <= 0 || s.kv_heads <= 0 || s.heads % s.kv_heads != 0) return false;
     const int64_t hd = s.d / s.heads;
     if (hd * s.heads != s.d || (hd != 16 && hd != 32)) return false;

@@ -58,6 +58,9 @@ struct Context {
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
     int cu_count = 0;
+    // 8 XCDs, each dealt cu_count / 8 of a cu_count-workgroup grid (probed at
+    // creation): what the fused forward's per-XCD teams need
+    bool xcd_teams = false;
     std::string name;
     void *ws[kSlots] = {nullptr, nullptr, nullptr, nullptr};
     size_t ws_bytes[kSlots] = {0, 0, 0, 0};
@@ -243,8 +246,12 @@ struct FusedArgs {
     float *arena = nullptr;
 };
 // Whether the fused kernel takes this shape (heads of 16 or 32, d a multiple
-// of 32 up to 256, ff a multiple of 4, at most 16384 rows, 32-bit offsets).
+// of 32 up to 256, ff a multiple of 4, at most 16384 rows, 32-bit offsets)
+// on this device (ctx.xcd_teams).
 bool fused_forward_fits(const Context &ctx, const FusedShape &s);
+// Launches one workgroup per CU and checks that 8 XCDs take cu_count / 8 each
+// (false on a device partitioned otherwise, or on any error).
+bool probe_xcd_teams(Context &ctx);
 FusedLayout fused_layout(const FusedShape &s);
 // Queues the forward + loss; the loss lands in a.loss, the row losses in
 // a.row_loss. The counters are back at zero when the launch ends.

@@ -288,11 +288,13 @@ struct Model {
     // The fused loss-only forward (fused_forward.hip): its arena, laid out for
     // (fused_b, fused_t); forward_path 1 keeps every forward on the
     // per-operation kernels. fused_check: a fused launch ran since the error
-    // word was last read.
+    // word was last read. last_fused: the last queued forward (or the graph
+    // the staged runs replay) was the fused launch.
     float *fused_arena = nullptr;
     int64_t fused_floats = 0, fused_b = 0, fused_t = 0;
     int forward_path = 0;
     bool fused_check = false;
+    bool last_fused = false;
 
     // ---- training state, allocated on the first training call ----
     struct TrainBuf {
@@ -632,7 +634,8 @@ struct Model {
         if (with_loss && !staged_targets) fail(MMH_ERR_ARGUMENT, "no targets staged");
         Context &c = *ctx;
         const int64_t d = cfg.d, V = cfg.vocab;
-        if (!prof && use_fused(batch, seq, with_loss, want_logits)) {
+        last_fused = !prof && use_fused(batch, seq, with_loss, want_logits);
+        if (last_fused) {
             ensure_fused(batch, seq);
             FusedArgs fa;
             fa.shape = fused_shape(batch, seq);
@@ -1395,6 +1398,14 @@ int32_t mmh_model_set_forward_path(mmh_handle model_h, int32_t path) {
             m.warm_act = nullptr;
             m.forward_path = path;
         }
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_last_forward_fused(mmh_handle model_h, int32_t *fused) {
+    return guard([&] {
+        if (!fused) fail(MMH_ERR_ARGUMENT, "fused is null");
+        *fused = model(model_h).last_fused ? 1 : 0;
         return MMH_OK;
     });
 }

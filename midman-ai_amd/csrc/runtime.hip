@@ -107,6 +107,7 @@ int32_t mmh_context_create(int32_t device, mmh_handle *out_ctx) {
         check_hip(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "stream create");
         check_hip(hipEventCreate(&c->t0), "event create");
         check_hip(hipEventCreate(&c->t1), "event create");
+        c->xcd_teams = probe_xcd_teams(*c);
         std::lock_guard<std::mutex> lock(g_mutex);
         g_contexts.push_back(std::move(c));
         *out_ctx = (mmh_handle)g_contexts.size();

@@ -123,6 +123,7 @@ _SIGNATURES = {
     "mmh_model_run_staged": [_h, _i64, _i64],
     "mmh_model_read_loss": [_h, _f32p],
     "mmh_model_set_forward_path": [_h, _i32],
+    "mmh_model_last_forward_fused": [_h, _i32p],
     "mmh_model_profile": [_h, _i64, _i64, _f32p, _i32p],
     "mmh_rms_norm_backward": [_h, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp],
     "mmh_apply_rope_backward": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
@@ -1037,6 +1038,13 @@ class Model:
         """PATH_AUTO: loss-only forwards of models that fit run as one fused
         launch; PATH_PER_OP: always the per-operation kernels."""
         check(lib().mmh_model_set_forward_path(self.handle, path))
+
+    def last_forward_fused(self) -> bool:
+        """Whether the last queued forward (or the graph run_staged replays)
+        was the fused launch."""
+        v = ctypes.c_int32()
+        check(lib().mmh_model_last_forward_fused(self.handle, ctypes.byref(v)))
+        return bool(v.value)
 
     def profile(self, batch: int, seq: int) -> dict:
         """One staged run with per-launch HIP events: {class: (ms, launches)}."""

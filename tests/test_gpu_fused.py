@@ -23,11 +23,15 @@ def oracle_config(cfg):
 
 
 def both_paths(m, x, y, batch, seq):
+    # every shape here fits the fused kernel: PATH_AUTO must take it (on an
+    # MI355X the context's XCD probe passes), PATH_PER_OP must not
     m.set_forward_path(mh.PATH_AUTO)
     fused = float(m.loss(x, y, batch, seq))
+    assert m.last_forward_fused()
     again = float(m.loss(x, y, batch, seq))
     m.set_forward_path(mh.PATH_PER_OP)
     per_op = float(m.loss(x, y, batch, seq))
+    assert not m.last_forward_fused()
     m.set_forward_path(mh.PATH_AUTO)
     return fused, again, per_op
 
@@ -103,6 +107,7 @@ def test_fused_graph_replays_and_reshapes(ctx):
             m.stage(x, y, 8, 256)
             m.run_staged(8, 256)
             assert m.read_loss() == eager, i
+            assert m.last_forward_fused()
             if i % 3 == 1:
                 assert float(m.loss(x2, y2, 3, 100)) == eager2
             if i % 3 == 2:
@@ -118,5 +123,27 @@ def test_forward_path_argument(ctx):
     try:
         with pytest.raises(mh.MidmanError):
             m.set_forward_path(2)
+    finally:
+        m.close()
+
+
+def test_unfit_model_and_logits_stay_per_op(ctx):
+    # heads of 64 (outside the fused kernel) and a logits-producing forward
+    # run on the per-operation kernels even under PATH_AUTO
+    cfg = [64, 128, 1, 2, 2, 64, 32, 10000.0, 1e-5, 1]
+    m = mh.Model.new(ctx, cfg, 3)
+    try:
+        x, y = m.lab_tokens(2, 16)
+        m.loss(x, y, 2, 16)
+        assert not m.last_forward_fused()
+    finally:
+        m.close()
+    m = mh.Model.new(ctx, mh.PRESETS["smoke"], 3)
+    try:
+        x, y = m.lab_tokens(2, 16)
+        m.loss(x, y, 2, 16)
+        assert m.last_forward_fused()
+        m.forward(x, 2, 16)
+        assert not m.last_forward_fused()
     finally:
         m.close()
