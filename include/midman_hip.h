@@ -258,9 +258,14 @@ int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
  * loss where the model fits it (heads of 16 or 32, d_model a multiple of 32
  * up to 256, d_ff a multiple of 4, at most 16384 tokens: the smoke and tiny
  * presets), the per-operation kernels otherwise. MMH_PATH_PER_OP: always the
- * per-operation kernels. The two agree within the forward's tolerance. A
- * fused launch that fails (a dependency wait past its bound) makes the next
- * loss read or mmh_model_loss return MMH_ERR_DEVICE. Logits-producing
+ * per-operation kernels. The two agree within the forward's tolerance. The
+ * fused launch needs every CU of the GPU at once (one workgroup per CU, 8
+ * XCDs dealt equal shares: checked when the context is created, else AUTO
+ * means PER_OP); kernels of other streams or processes that hold CUs delay
+ * it, and two fused launches on different streams of one GPU can hold each
+ * other's CUs until a wait gives up. A fused launch that fails (a dependency
+ * wait past its bound of 2^18 polls) makes the next loss read or mmh_model_loss
+ * return MMH_ERR_DEVICE. Logits-producing
  * forwards, mmh_model_profile and training always use the per-operation
  * kernels. */
 #define MMH_PATH_AUTO 0

@@ -13,7 +13,8 @@
 //     the XCD's L2, where device-scope (sc1) loads of other CUs of the same
 //     XCD find them (sc1 loads miss the per-CU L1 and take dirty L2 lines);
 //   * a finished task bumps a device-scope atomic counter; a waiting task
-//     polls it with sc1 loads;
+//     polls it with device-scope atomic loads and then reads the data with
+//     sc1 loads;
 //   * no cross-XCD fence is needed (agent-scope release/acquire fences write
 //     back and invalidate the whole L2: ~18 us per round measured on the box,
 //     against ~1.3 us for a 32-workgroup round of the scheme above).
@@ -32,10 +33,14 @@
 //              (128-column blocks; every layer has its own qkv buffer, so no
 //              later layer overwrites keys an attention task still reads)
 //   A(l,h,q)   causal attention of query block q for head h over key tiles
-//              0..q (the online softmax of attention.hip's key-split kernel)
-//   O(l,q,c)   x += ctx . Wo (32-column blocks, K split over the 8 waves)
-//   G(l,q,c)   h = silu(gate) * up of the normalised x (128-column blocks)
-//   D(l,q,c)   x += h . Wd (32-column blocks, K split over the 8 waves)
+//              0..q (the online softmax of attention.hip's key-split kernel),
+//              then that head's share of the O projection: ctx_h . Wo[rows of
+//              head h], stored as a 32 x d partial
+//   G(l,q,c)   the block's x plus the heads' partials in head order (the
+//              attention residual of block.rs:79; column block 0 stores it as
+//              x2), RMS-normalised, times Wgu, h = silu(gate) * up (256 packed
+//              gate/up columns: 128 columns of h per task)
+//   D(l,q,c)   x = x2 + h . Wd (32-column blocks, K split over the 8 waves)
 // then HEAD(q,c): logits of 256 vocabulary rows (final norm folded), per row
 // the (max, sum of exp) pair and the target logit; COMB(q): the rows' losses
 // (ops_reduce.rs:236-259) and their f64 sum.
