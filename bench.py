@@ -216,6 +216,7 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
     ctx.synchronize()
     loss = m.read_loss()
     ms_step = ms / steps
+    fused = m.last_forward_fused()  # the path the timed replays took
     # the same staged step on the per-operation kernels (the default path of a
     # model the fused launch takes is that launch)
     per_op_ms = None
@@ -252,7 +253,7 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
             log(f"shard-fed timing skipped: {e}")
     m.close()
     return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
-            "per_op_ms_per_step": per_op_ms,
+            "fused": fused, "per_op_ms_per_step": per_op_ms,
             "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg,
             "train": train, "checkpoint": ckpt, "data": data}
 
@@ -508,8 +509,8 @@ def main():
         else:
             tiny = time_model(mh, ctx, "tiny", 8, 256, a.steps, a.warmup, per_op=True)
             log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
-                f"loss {tiny['loss']:.5f} (one fused launch; per-operation kernels "
-                f"{tiny['per_op_ms_per_step']:.4f} ms/step, kernel classes below)")
+                f"loss {tiny['loss']:.5f} ({'one fused launch' if tiny['fused'] else 'per-operation kernels'}; "
+                f"per-operation kernels {tiny['per_op_ms_per_step']:.4f} ms/step, kernel classes below)")
         for k, (ms, nl) in tiny["profile"].items():
             log(f"  {k}: {ms:.4f} ms over {nl} launches (HIP events per launch)")
         ctx.close()
@@ -540,7 +541,8 @@ def main():
         tiny = time_model(mh, ctx, "tiny", 8, 256, max(a.steps, 1000), max(a.warmup, 100),
                           per_op=True)
         log(f"tiny: {tiny['ms_per_step']:.3f} ms/step, {tiny['tokens_per_s']:.0f} tok/s "
-            f"(per-operation kernels {tiny['per_op_ms_per_step']:.3f} ms/step)")
+            f"({'one fused launch' if tiny['fused'] else 'per-operation kernels'}; "
+            f"per-operation kernels {tiny['per_op_ms_per_step']:.3f} ms/step)")
 
     flops = model_flops(large["cfg"], 4, 1024)
     nbytes = model_bytes(large["cfg"], 4, 1024)
@@ -650,7 +652,8 @@ def main():
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),
-                "path": "one fused persistent launch (fused_forward.hip)",
+                "path": ("one fused persistent launch (fused_forward.hip)" if tiny["fused"]
+                         else "per-operation kernels (the fused launch did not apply)"),
                 "per_op_ms_per_step": round(tiny["per_op_ms_per_step"], 4),
                 "pcie_inclusive_tokens_per_s": round(tiny["pcie_inclusive_tokens_per_s"], 1),
                 "cpu_baseline": tiny_cpu},
