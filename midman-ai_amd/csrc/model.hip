@@ -285,6 +285,7 @@ struct Model {
     int64_t graph_b = 0, graph_t = 0, warm_b = 0, warm_t = 0;
     const void *graph_act = nullptr, *warm_act = nullptr, *graph_ws = nullptr,
                *graph_arena = nullptr;
+    bool graph_fused = false;  // the captured graph is the fused launch
     // The fused loss-only forward (fused_forward.hip): its arena, laid out for
     // (fused_b, fused_t); forward_path 1 keeps every forward on the
     // per-operation kernels. fused_check: a fused launch ran since the error
@@ -326,6 +327,7 @@ struct Model {
         graph = nullptr;
         graph_b = graph_t = 0;
         graph_act = graph_ws = graph_arena = nullptr;
+        graph_fused = false;
     }
 
     int64_t qkv_cols() const { return cfg.d + 2 * cfg.kv(); }
@@ -716,9 +718,11 @@ struct Model {
     // capture the same launches into a graph. Later calls replay the graph.
     // The graph holds no memset or allocation: only kernel launches.
     void run_staged(int64_t batch, int64_t seq) {
+        // (a graph of the fused launch also needs the arena it was captured
+        // with, still laid out for this shape)
         if (graph_exec && graph_b == batch && graph_t == seq && graph_act == act &&
-            graph_ws == ctx->ws[0] && graph_arena == fused_arena && fused_b == batch &&
-            fused_t == seq && staged_n == batch * seq && staged_targets) {
+            graph_ws == ctx->ws[0] && staged_n == batch * seq && staged_targets &&
+            (!graph_fused || (graph_arena == fused_arena && fused_b == batch && fused_t == seq))) {
             check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
             return;
         }
@@ -750,6 +754,7 @@ struct Model {
         graph_act = act;
         graph_ws = ctx->ws[0];
         graph_arena = fused_arena;
+        graph_fused = last_fused;
         check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
     }
 
