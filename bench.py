@@ -217,6 +217,11 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
     loss = m.read_loss()
     ms_step = ms / steps
     fused = m.last_forward_fused()  # the path the timed replays took
+    # the fused kernel's own duration (per-workgroup clock stamps, launches
+    # back to back), beside the HIP-event time per graph replay
+    kernel_us = None
+    if fused:
+        kernel_us = m.fused_duration(B, T, 200)
     # the same staged step on the per-operation kernels (the default path of a
     # model the fused launch takes is that launch)
     per_op_ms = None
@@ -253,27 +258,69 @@ def time_model(mh, ctx, preset, B, T, steps, warmup, train_steps=0, checkpoint=F
             log(f"shard-fed timing skipped: {e}")
     m.close()
     return {"ms_per_step": ms_step, "tokens_per_s": B * T / (ms_step / 1000), "loss": loss,
-            "fused": fused, "per_op_ms_per_step": per_op_ms,
+            "fused": fused, "fused_kernel_us": kernel_us, "per_op_ms_per_step": per_op_ms,
             "pcie_inclusive_tokens_per_s": B * T / (host_ms / 1000), "profile": prof, "cfg": cfg,
             "train": train, "checkpoint": ckpt, "data": data}
 
 
-def time_block(mh, ctx, hkv, reps=20):
-    """DecoderBlock::forward alone at the benchmark block config: d 1024, 16
-    heads x 64, SwiGLU 2816, B8 T1024, x ~ N(0,1), W ~ N(0,0.02) seeded.
-    HIP events around `reps` calls after 50 ms of warmup (weights packed per call,
-    as the op-level entry point does)."""
+BLOCK = {"B": 8, "T": 1024, "d": 1024, "H": 16, "ff": 2816}
+
+
+def block_inputs(mh, hkv):
+    """The benchmark block config's inputs: x ~ N(0,1) from Rng(0), then, from
+    the same stream, q, k, v, o, gate, up, down ~ N(0,0.02) (each value the
+    f32 product 0.02 * normal(), as Tensor::randn forms it, tensor.rs:158-162);
+    norm weights 1 (norm.rs:60). Returns x [B,T,d] and the block's parameters
+    in DecoderBlock::parameters order (attn_norm, q, k, v, o, mlp_norm, gate,
+    up, down)."""
     import numpy as np
 
-    B, T, d, H, ff = 8, 1024, 1024, 16, 2816
+    B, T, d, H, ff = (BLOCK[k] for k in ("B", "T", "d", "H", "ff"))
+    kv = hkv * (d // H)
+    sizes = [d * d, d * kv, d * kv, d * d, d * ff, d * ff, ff * d]
+    z = mh.randn(B * T * d + sum(sizes), 1.0, 0)  # one stream, std 1: value = normal()
+    x = z[:B * T * d].reshape(B, T, d)
+    parts, at = [], B * T * d
+    for i, n in enumerate(sizes):
+        if i in (0, 4):  # attn_norm before q, mlp_norm before gate
+            parts.append(np.ones(d, np.float32))
+        parts.append(np.float32(0.02) * z[at:at + n])
+        at += n
+    return x, np.concatenate(parts)
+
+
+def tiny_roofline(tiny):
+    """The tiny preset's forward + loss against the fp32 MFMA peak: its
+    5.924 GFLOP (2*M*N*K of every GEMM + the causal attention) over the fused
+    kernel's own duration (median of per-workgroup clock stamps) when the
+    fused launch ran, else over the HIP-event time per step."""
+    flops = sum(model_flops(tiny["cfg"], 8, 256).values())
+    us = tiny["fused_kernel_us"][0] if tiny["fused_kernel_us"] else tiny["ms_per_step"] * 1000
+    achieved = flops / (us * 1e-6) / 1e12
+    return {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP32_MFMA_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+            "traffic": None, "flops_per_step": flops,
+            "kernel": ("forward_team_kernel (the whole forward + loss, one launch)"
+                       if tiny["fused_kernel_us"] else "all kernels of one step"),
+            "kernel_us_median": None if not tiny["fused_kernel_us"] else
+            round(tiny["fused_kernel_us"][0], 2),
+            "kernel_us_min": None if not tiny["fused_kernel_us"] else
+            round(tiny["fused_kernel_us"][1], 2),
+            "duration_source": ("per-workgroup s_memrealtime stamps, 200 launches back to back "
+                                "(mmh_model_fused_duration)" if tiny["fused_kernel_us"]
+                                else "HIP events per step")}
+
+
+def time_block(mh, ctx, hkv, reps=20):
+    """DecoderBlock::forward alone at the benchmark block config: d 1024, 16
+    heads x 64, SwiGLU 2816, B8 T1024, on block_inputs (the seeded stream of
+    the config). HIP events around `reps` calls after 50 ms of warmup
+    (weights packed per call, as the op-level entry point does)."""
+    B, T, d, H, ff = (BLOCK[k] for k in ("B", "T", "d", "H", "ff"))
     hd = d // H
     kv = hkv * hd
-    r = np.random.default_rng(7)
-    x = ctx.to_device(r.standard_normal((B, T, d), dtype=np.float32))
-    n_w = 2 * d + 2 * d * d + 2 * d * kv + 3 * d * ff
-    w = (0.02 * r.standard_normal(n_w, dtype=np.float32))
-    w[:d] = 1.0
-    w[d + 2 * d * d + 2 * d * kv: 2 * d + 2 * d * d + 2 * d * kv] = 1.0
+    xh, w = block_inputs(mh, hkv)
+    x = ctx.to_device(xh)
     dw = ctx.to_device(w)
     out = ctx.empty((B, T, d))
     tabs = mh.RotaryTables(ctx, hd, T, 10000.0)
@@ -511,6 +558,7 @@ def main():
             log(f"tiny: {tiny['ms_per_step']:.4f} ms/step, {tiny['tokens_per_s']:.0f} tok/s, "
                 f"loss {tiny['loss']:.5f} ({'one fused launch' if tiny['fused'] else 'per-operation kernels'}; "
                 f"per-operation kernels {tiny['per_op_ms_per_step']:.4f} ms/step, kernel classes below)")
+            log(f"tiny roofline: {json.dumps(tiny_roofline(tiny))}")
         for k, (ms, nl) in tiny["profile"].items():
             log(f"  {k}: {ms:.4f} ms over {nl} launches (HIP events per launch)")
         ctx.close()
@@ -542,7 +590,8 @@ def main():
                           per_op=True)
         log(f"tiny: {tiny['ms_per_step']:.3f} ms/step, {tiny['tokens_per_s']:.0f} tok/s "
             f"({'one fused launch' if tiny['fused'] else 'per-operation kernels'}; "
-            f"per-operation kernels {tiny['per_op_ms_per_step']:.3f} ms/step)")
+            f"per-operation kernels {tiny['per_op_ms_per_step']:.3f} ms/step; "
+            f"fused kernel {tiny['fused_kernel_us']} us median/min)")
 
     flops = model_flops(large["cfg"], 4, 1024)
     nbytes = model_bytes(large["cfg"], 4, 1024)
@@ -652,6 +701,7 @@ def main():
             "tiny": None if tiny is None else {
                 "tokens_per_s": round(tiny["tokens_per_s"], 1),
                 "ms_per_step": round(tiny["ms_per_step"], 4),
+                "roofline": tiny_roofline(tiny),
                 "path": ("one fused persistent launch (fused_forward.hip)" if tiny["fused"]
                          else "per-operation kernels (the fused launch did not apply)"),
                 "per_op_ms_per_step": round(tiny["per_op_ms_per_step"], 4),

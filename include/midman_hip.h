@@ -116,10 +116,13 @@ int32_t mmh_gemm_tn(mmh_handle ctx, const float *a, const float *b, float *c, in
  * harnesses that forbid hipMalloc). The same kernels and split choices as the
  * three entry points above, so the same bits; the split-K partials live in a
  * fixed 16 MiB device array per GPU instead of the context's workspace. A
- * product whose partials need more (splits x m x n x 4 bytes; split-K is
- * chosen only when the output tiles cannot fill the chip, and every product of
- * the benchmark sweep fits) is refused with MMH_ERR_SHAPE before anything
- * runs. The array is shared by every call on a
+ * product whose partials need more is refused with MMH_ERR_SHAPE before
+ * anything runs: a K split needs splits x m x n x 4 bytes (chosen only when
+ * the output tiles cannot fill the chip; every product of the benchmark sweep
+ * fits), the 128x128 kernel's tail balance 64 KiB per piece of its last
+ * tiles (a grid of q x CUs + R tiles cut into s pieces each: R x s x 64 KiB).
+ * The split choices never depend on the array, so an accepted call gives the
+ * allocating entry point's bits. The array is shared by every call on a
  * GPU: calls that overlap on one GPU (other streams, contexts or threads) race
  * on it. */
 #define MMH_GEMM_NN 0
@@ -263,9 +266,11 @@ int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
  * XCDs dealt equal shares: checked when the context is created, else AUTO
  * means PER_OP); kernels of other streams or processes that hold CUs delay
  * it, and two fused launches on different streams of one GPU can hold each
- * other's CUs until a wait gives up. A fused launch that fails (a dependency
- * wait past its bound of 2^18 polls) makes the next loss read or mmh_model_loss
- * return MMH_ERR_DEVICE. Logits-producing
+ * other's CUs until a wait gives up. Every wait is bounded (2^18 polls), and
+ * a fused launch that gave up is redone on the per-operation kernels from the
+ * ids and targets still staged in HBM, before mmh_model_loss returns or
+ * before mmh_model_read_loss reads the loss (or when new ids are staged
+ * first): the loss returned is always that of a complete forward. Logits-producing
  * forwards, mmh_model_profile and training always use the per-operation
  * kernels. */
 #define MMH_PATH_AUTO 0
@@ -273,8 +278,36 @@ int32_t mmh_model_read_loss(mmh_handle model, float *loss_host);
 int32_t mmh_model_set_forward_path(mmh_handle model, int32_t path);
 /* 1 in *fused when the model's last queued forward (or the graph that
  * mmh_model_run_staged replays) is the fused launch, else 0 (no reference
- * counterpart; lets a caller or a test see which path MMH_PATH_AUTO took). */
+ * counterpart; lets a caller or a test see which path MMH_PATH_AUTO took).
+ * After a fused launch was redone on the per-operation kernels this is 0. */
 int32_t mmh_model_last_forward_fused(mmh_handle model, int32_t *fused);
+/* How many fused launches of this model gave up and were redone on the
+ * per-operation kernels, and the error word of the last one (bit 0: a
+ * dependency wait reached its bound; bit 1: more workgroups landed on one XCD
+ * than its team holds; bit 2: row blocks were left uncombined; higher bits:
+ * set by mmh_model_inject_fused_error). last_error may be NULL. No reference
+ * counterpart. */
+int32_t mmh_model_fused_fallbacks(mmh_handle model, int64_t *redone, int32_t *last_error);
+/* Diagnostic with no reference counterpart: the next fused launch of this
+ * model (eager or a graph replay) starts with `bits` (> 0) in its error word,
+ * so its waits give up as they do when the launch's workgroups are not all
+ * resident; every workgroup still runs to its end. The failure handling
+ * above (the redo, the cleared counters) can then be exercised without
+ * making the GPU wait. */
+int32_t mmh_model_inject_fused_error(mmh_handle model, int32_t bits);
+/* Diagnostic with no reference counterpart (a timing analogue of
+ * forward_traced, model.rs:116-125, for the fused launch, whose kernels
+ * mmh_model_profile cannot separate): runs the staged loss-only forward
+ * `reps` times (1..100000) as the fused launch, back to back, with every
+ * workgroup recording the device's constant-rate wall clock at its start and
+ * end; per launch the duration is the last end minus the first start. Fills
+ * the median (and, when min_us is not NULL, the minimum) in microseconds;
+ * the staged loss is then that of the last launch. MMH_ERR_ARGUMENT when
+ * nothing is staged for (batch, seq) or the fused launch does not take this
+ * model and shape; MMH_ERR_DEVICE when a timed launch gave up (its forward is
+ * redone first). */
+int32_t mmh_model_fused_duration(mmh_handle model, int64_t batch, int64_t seq, int32_t reps,
+                                 float *median_us, float *min_us);
 
 /* Kernel classes timed by mmh_model_profile. */
 #define MMH_PROF_EMBEDDING 0

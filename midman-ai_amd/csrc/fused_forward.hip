@@ -64,6 +64,8 @@ constexpr int kDev = 16;               // sc1: device-coherent load / write-thro
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor: reads 0
 constexpr int kSpinLimit = 1 << 18;
 constexpr int kLdsFloats = 8 * 32 * 33 + 2 * 8 * 32;
+constexpr int kRowStage = 32 * (256 + 4);  // the normalised rows of a task (floats)
+constexpr int kLossSlots = kRowStage / 2;  // f64 row-block sums the last workgroup parks there
 
 // task stages within a layer (stage 2, the O projection, rides on the
 // attention tasks and the gate/up tasks' loads; its counter slot is unused),
@@ -122,6 +124,7 @@ struct FusedP {
     const int32_t *ids;   // staged ids; the targets at ids + tgt_off
     float *loss;
     int32_t *err;         // error bits (a word of the arena, also addressed here)
+    uint64_t *stamps;     // diagnostic clock stamps (start, end) per workgroup, or null
     uint32_t w_bytes, f_bytes, i_bytes, tgt_off;
     // arena regions (float offsets)
     uint32_t o_x, o_h, o_qkv, o_part, o_zt, o_rl, o_p64, o_ctl, o_err, o_cos, o_sin, o_op, o_x2;
@@ -624,13 +627,14 @@ template <int HD>
 __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     __shared__ __attribute__((aligned(16))) float lds[kLdsFloats];
     __shared__ __attribute__((aligned(16))) float s_nw[256];        // norm weights of the task
-    __shared__ __attribute__((aligned(16))) float s_xs[32 * (256 + 4)];  // normalised rows
+    __shared__ __attribute__((aligned(16))) float s_xs[kRowStage];  // normalised rows
     __shared__ float s_cs[32 * 16], s_sn[32 * 16];                 // RoPE rows of the block
     __shared__ float s_inv[32];
     __shared__ int s_ok, s_last, s_x, s_slot;
     const int tid0 = threadIdx.x;
     const int team = gridDim.x >> 3;
     int32_t *ctl = reinterpret_cast<int32_t *>(p.f + p.o_ctl);
+    if (p.stamps && tid0 == 0) p.stamps[2 * blockIdx.x] = __builtin_amdgcn_s_memrealtime();
 
     Res R;
     R.w = rsrc(p.w, p.w_bytes);
@@ -1083,11 +1087,14 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
         s_last = __hip_atomic_fetch_add(ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                  (int)gridDim.x - 1;
     __syncthreads();
-    if (!s_last) return;
+    if (!s_last) {
+        if (p.stamps && tid0 == 0) p.stamps[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+        return;
+    }
     // every row block of every sequence combined? Each thread checks row
     // blocks i = tid, tid + 512, ... and parks their f64 sums in LDS; thread 0
     // then adds them in index order.
-    double *sm_p = reinterpret_cast<double *>(s_xs);  // B * nrb <= 16384 / 32 doubles
+    double *sm_p = reinterpret_cast<double *>(s_xs);  // B * nrb <= kLossSlots (host-checked)
     const int nblk = p.B * nrb;
     int missing = 0;
     for (int i = tid0; i < nblk; i += kNT) {
@@ -1106,6 +1113,11 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     }
     __syncthreads();
     for (int i = tid0; i < (int)p.ctl_ints; i += kNT) st1<kDev>(R.f, 4u * (p.o_ctl + i), 0.0f);
+    if (p.stamps) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid0 == 0) p.stamps[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+    }
 }
 
 // One single-wave workgroup per CU, counted per XCD.
@@ -1149,6 +1161,9 @@ bool fused_forward_fits(const Context &ctx, const FusedShape &s) {
         return false;
     // small work only: one launch with a few hundred tasks per XCD
     if (n > 16384) return false;
+    // the last workgroup parks one f64 sum per (sequence, 32-row block) in
+    // its LDS row stage (32 x 260 floats) before adding them in order
+    if (s.batch * ((s.seq + 31) / 32) > kLossSlots) return false;
     return true;
 }
 
@@ -1201,6 +1216,7 @@ void launch_fused_forward(Context &ctx, const FusedArgs &a) {
     p.ids = a.ids;
     p.loss = a.loss;
     p.err = reinterpret_cast<int32_t *>(a.arena + f.o_err);
+    p.stamps = a.stamps;
     p.w_bytes = (uint32_t)(s.weight_floats * 4);
     p.f_bytes = (uint32_t)(f.floats * 4);
     p.tgt_off = (uint32_t)(a.tgt - a.ids);

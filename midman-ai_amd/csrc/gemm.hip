@@ -1532,8 +1532,16 @@ void gemm(Context &ctx, const GemmDesc &d) {
             }
         }
         const size_t need = (size_t)R * best_s * BM * BN * 4;
-        if (best_s > 1 && best <= 0.95 * (double)(q + 1) &&
-            (!d.scratch || need <= d.scratch_bytes)) {
+        if (best_s > 1 && best <= 0.95 * (double)(q + 1)) {
+            // the choice never depends on the caller's scratch, so a fixed
+            // scratch gives the same summation order (and bits) as the
+            // workspace, or the call is refused
+            if (d.scratch && need > d.scratch_bytes)
+                fail(MMH_ERR_SHAPE, "gemm: the tail pieces of a " + std::to_string(d.m) + " x " +
+                                        std::to_string(d.n) + " product (" + std::to_string(R) +
+                                        " tiles x " + std::to_string(best_s) + " pieces) need " +
+                                        std::to_string(need) + " bytes; the scratch holds " +
+                                        std::to_string(d.scratch_bytes));
             p.tail_first = (int)(tiles - R);
             p.tail_s = best_s;
             p.tail_k = (ktiles + best_s - 1) / best_s * BK;

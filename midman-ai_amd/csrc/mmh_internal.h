@@ -244,6 +244,9 @@ struct FusedArgs {
     // slots of the 8 XCDs, the task counters) and error word zero before
     // the first launch, the rotary tables at o_cos / o_sin
     float *arena = nullptr;
+    // diagnostic: when set, workgroup g stores the device's constant-rate
+    // clock at its start and its end into stamps[2g], stamps[2g + 1]
+    uint64_t *stamps = nullptr;
 };
 // Whether the fused kernel takes this shape (heads of 16 or 32, d a multiple
 // of 32 up to 256, ff a multiple of 4, at most 16384 rows, 32-bit offsets)

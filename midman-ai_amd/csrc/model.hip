@@ -36,6 +36,7 @@
 // then the embedding scatter. The global norm (f64) and one clip + AdamW pass
 // over every parameter follow on the device; the host reads back only the
 // loss and the norm.
+#include <algorithm>
 #include <cmath>
 #include <cstring>
 #include <mutex>
@@ -296,6 +297,16 @@ struct Model {
     int forward_path = 0;
     bool fused_check = false;
     bool last_fused = false;
+    // A fused launch whose error word comes back nonzero is redone on the
+    // per-operation kernels: fused_fallbacks counts those redos, fused_last_error
+    // keeps the last word seen. fused_inject: bits the host writes into the
+    // error word before the next fused launch (a diagnostic: the kernel's waits
+    // then give up as under contention, every workgroup still exits).
+    // run_b, run_t: the shape of the last staged run, for its redo.
+    int64_t fused_fallbacks = 0;
+    int32_t fused_last_error = 0, fused_inject = 0;
+    int64_t run_b = 0, run_t = 0;
+    uint64_t *fused_stamps = nullptr;  // clock stamps for the next fused launch (diagnostic)
 
     // ---- training state, allocated on the first training call ----
     struct TrainBuf {
@@ -530,6 +541,16 @@ struct Model {
         if (cs != hipStreamCaptureStatusNone)
             fail(MMH_ERR_OTHER, "fused forward: arena not prepared before capture");
         const FusedLayout f = fused_layout(fused_shape(batch, seq));
+        // every fill and copy below stays inside the arena, and the table
+        // copies read no more than the tables hold
+        const int64_t tab_have = cfg.max_seq * (cfg.hd() / 2);
+        bool inside = f.nbands > 0 && f.tab_floats == tab_have && f.o_cos >= 0 &&
+                      f.o_sin >= f.o_cos + f.tab_floats && f.o_sin + f.tab_floats <= f.floats &&
+                      f.o_err >= 0 && f.o_err + 1 <= f.floats && f.o_ctl >= 0 &&
+                      f.o_ctl + f.ctl_ints <= f.floats;
+        for (int i = 0; i < f.nbands; ++i)
+            inside = inside && f.bands[i] >= 0 && f.bands[i] + FusedLayout::kBand <= f.floats;
+        if (!inside) fail(MMH_ERR_OTHER, "fused forward: arena layout out of bounds");
         check_hip(hipStreamSynchronize(ctx->stream), "sync");
         if (f.floats > fused_floats) {
             if (fused_arena) (void)hipFree(fused_arena);
@@ -556,25 +577,60 @@ struct Model {
         fused_t = seq;
         fused_check = false;
     }
-    // Raises (and clears the word and the counters) when a fused launch since
-    // the last check reported an error; waits for queued work.
-    void check_fused() {
-        if (!fused_check || !fused_arena) return;
+    // The error bits of the fused launches since the last check (0: none, or
+    // no fused launch ran); waits for queued work. A nonzero word is cleared
+    // together with the counters, so the next launch starts clean.
+    int32_t take_fused_error() {
+        if (!fused_check || !fused_arena) return 0;
         const FusedLayout f = fused_layout(fused_shape(fused_b, fused_t));
         int32_t e = 0;
         check_hip(hipMemcpyAsync(&e, fused_arena + f.o_err, 4, hipMemcpyDeviceToHost, ctx->stream),
                   "fused error word");
         check_hip(hipStreamSynchronize(ctx->stream), "fused error sync");
         fused_check = false;
-        if (e == 0) return;
+        if (e == 0) return 0;
         check_hip(hipMemsetAsync(fused_arena + f.o_ctl, 0, (size_t)f.ctl_ints * 4, ctx->stream),
                   "fused reset");
         check_hip(hipMemsetAsync(fused_arena + f.o_err, 0, 4, ctx->stream), "fused reset");
         check_hip(hipStreamSynchronize(ctx->stream), "fused reset sync");
-        fail(MMH_ERR_DEVICE, std::string("fused forward failed:") +
-                                 ((e & 1) ? " a dependency wait timed out;" : "") +
-                                 ((e & 2) ? " more workgroups landed on one XCD than its team holds;" : "") +
-                                 ((e & 4) ? " row blocks were left uncombined;" : ""));
+        return e;
+    }
+    // When the fused launch of the last loss-only forward (batch x seq) gave
+    // up (a dependency wait past its bound: the team's workgroups were not all
+    // resident at once, as when other work holds CUs), the same forward runs
+    // again on the per-operation kernels from the staged ids and targets,
+    // which are still in HBM; the loss buffer then holds its loss. True when
+    // that happened. Waits for queued work.
+    bool redo_if_fused_failed(int64_t batch, int64_t seq) {
+        const int32_t e = take_fused_error();
+        if (e == 0) return false;
+        fused_last_error = e;
+        ++fused_fallbacks;
+        enqueue(batch, seq, true, false, nullptr, true);
+        check_hip(hipStreamSynchronize(ctx->stream), "fused redo sync");
+        return true;
+    }
+    // Settles a staged fused run whose loss has not been read before its ids,
+    // targets or loss are replaced.
+    void settle_fused() {
+        if (fused_check && staged_n > 0 && staged_n == run_b * run_t && staged_targets)
+            (void)redo_if_fused_failed(run_b, run_t);
+        else
+            (void)take_fused_error();
+    }
+    // The diagnostic error bits into the arena's error word, outside any
+    // capture (a graph holds kernel launches only); kept pending until a
+    // fused arena exists.
+    void apply_fused_inject() {
+        if (!fused_inject || !fused_arena) return;
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        check_hip(hipStreamIsCapturing(ctx->stream, &cs), "capture status");
+        if (cs != hipStreamCaptureStatusNone) return;
+        const FusedLayout f = fused_layout(fused_shape(fused_b, fused_t));
+        check_hip(hipMemsetD32Async(reinterpret_cast<hipDeviceptr_t>(fused_arena + f.o_err),
+                                    fused_inject, 1, ctx->stream),
+                  "fused error preset");
+        fused_inject = 0;
     }
 
     // Checks of model.rs:134-148 and the id ranges (ops_shape.rs:250-252,
@@ -591,6 +647,7 @@ struct Model {
         check_ids(inputs, n, cfg.vocab, "token id");
         if (targets) check_ids(targets, n, cfg.vocab, "target class");
         ctx->select();
+        settle_fused();
         ensure(n);
         check_hip(hipMemcpyAsync(ids, inputs, (size_t)n * 4, hipMemcpyHostToDevice, ctx->stream),
                   "ids upload");
@@ -627,7 +684,7 @@ struct Model {
     // (EPI_CE) and the logits are never written. Queued on the context
     // stream; nothing waits.
     void enqueue(int64_t batch, int64_t seq, bool with_loss, bool want_logits,
-                 Prof *prof = nullptr) {
+                 Prof *prof = nullptr, bool per_op = false) {
         const int64_t n = batch * seq;
         if (n != staged_n || n > cap)
             fail(MMH_ERR_ARGUMENT, "no tokens staged for batch " + std::to_string(batch) +
@@ -636,9 +693,10 @@ struct Model {
         if (with_loss && !staged_targets) fail(MMH_ERR_ARGUMENT, "no targets staged");
         Context &c = *ctx;
         const int64_t d = cfg.d, V = cfg.vocab;
-        last_fused = !prof && use_fused(batch, seq, with_loss, want_logits);
+        last_fused = !prof && !per_op && use_fused(batch, seq, with_loss, want_logits);
         if (last_fused) {
             ensure_fused(batch, seq);
+            apply_fused_inject();
             FusedArgs fa;
             fa.shape = fused_shape(batch, seq);
             fa.w = w;
@@ -649,6 +707,7 @@ struct Model {
             fa.tgt = tgt;
             fa.loss = loss;
             fa.arena = fused_arena;
+            fa.stamps = fused_stamps;
             launch_fused_forward(c, fa);
             fused_check = true;
             return;
@@ -718,12 +777,19 @@ struct Model {
     // capture the same launches into a graph. Later calls replay the graph.
     // The graph holds no memset or allocation: only kernel launches.
     void run_staged(int64_t batch, int64_t seq) {
+        run_b = batch;
+        run_t = seq;
         // (a graph of the fused launch also needs the arena it was captured
         // with, still laid out for this shape)
         if (graph_exec && graph_b == batch && graph_t == seq && graph_act == act &&
             graph_ws == ctx->ws[0] && staged_n == batch * seq && staged_targets &&
             (!graph_fused || (graph_arena == fused_arena && fused_b == batch && fused_t == seq))) {
+            if (graph_fused) apply_fused_inject();
             check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
+            // a replayed fused launch reports through the error word like an
+            // eager one
+            last_fused = graph_fused;
+            fused_check = fused_check || graph_fused;
             return;
         }
         // eager first for a new shape, new activations, or a fused arena laid
@@ -738,6 +804,7 @@ struct Model {
             return;
         }
         drop_graph();
+        if (use_fused(batch, seq, true, false)) apply_fused_inject();
         check_hip(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal), "capture");
         try {
             enqueue(batch, seq, true, false);
@@ -756,6 +823,78 @@ struct Model {
         graph_arena = fused_arena;
         graph_fused = last_fused;
         check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
+        fused_check = fused_check || graph_fused;
+    }
+
+    // The fused launch's own duration: `reps` eager launches on the staged ids,
+    // back to back, each workgroup stamping the device's constant-rate clock
+    // at its start and end; per launch, last end - first start. Fills the
+    // median and the minimum in microseconds.
+    void fused_duration(int64_t batch, int64_t seq, int reps, float *median_us, float *min_us) {
+        if (reps < 1 || reps > 100000) fail(MMH_ERR_ARGUMENT, "reps must be 1 to 100000");
+        if (staged_n != batch * seq || staged_n == 0 || !staged_targets)
+            fail(MMH_ERR_ARGUMENT, "no tokens and targets staged for batch " +
+                                       std::to_string(batch) + " x seq " + std::to_string(seq));
+        if (!use_fused(batch, seq, true, false))
+            fail(MMH_ERR_ARGUMENT, "the fused launch does not take this model and shape");
+        settle_fused();
+        int khz = 0;
+        check_hip(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, ctx->device),
+                  "wall clock rate");
+        if (khz <= 0) fail(MMH_ERR_DEVICE, "the device reports no wall clock rate");
+        const size_t per = 2 * (size_t)ctx->cu_count;
+        std::vector<uint64_t> h((size_t)reps * per);
+        uint64_t *st = nullptr;
+        check_hip(hipMalloc(&st, h.size() * 8), "stamps alloc");
+        try {
+            for (int r = 0; r < reps; ++r) {
+                fused_stamps = st + (size_t)r * per;
+                enqueue(batch, seq, true, false);
+            }
+            fused_stamps = nullptr;
+            check_hip(hipMemcpyAsync(h.data(), st, h.size() * 8, hipMemcpyDeviceToHost, ctx->stream),
+                      "stamps download");
+            check_hip(hipStreamSynchronize(ctx->stream), "stamps sync");
+        } catch (...) {
+            fused_stamps = nullptr;
+            (void)hipStreamSynchronize(ctx->stream);
+            (void)hipFree(st);
+            throw;
+        }
+        (void)hipFree(st);
+        run_b = batch;
+        run_t = seq;
+        if (redo_if_fused_failed(batch, seq))
+            fail(MMH_ERR_DEVICE, "a timed fused launch gave up (error bits " +
+                                     std::to_string(fused_last_error) +
+                                     "): its duration is not the kernel's");
+        std::vector<double> span((size_t)reps);
+        for (int r = 0; r < reps; ++r) {
+            uint64_t lo = UINT64_MAX, hi = 0;
+            for (size_t g = 0; g < per; g += 2) {
+                lo = std::min(lo, h[(size_t)r * per + g]);
+                hi = std::max(hi, h[(size_t)r * per + g + 1]);
+            }
+            span[(size_t)r] = hi > lo ? (double)(hi - lo) * 1000.0 / (double)khz : 0.0;
+        }
+        std::sort(span.begin(), span.end());
+        *median_us = (float)span[span.size() / 2];
+        if (min_us) *min_us = (float)span[0];
+    }
+
+    // The loss of the last staged run (read_loss): a fused run that gave up is
+    // redone on the per-operation kernels first.
+    void read_staged_loss(float *out) {
+        check_hip(hipMemcpyAsync(out, loss, 4, hipMemcpyDeviceToHost, ctx->stream), "loss download");
+        check_hip(hipStreamSynchronize(ctx->stream), "loss sync");
+        if (staged_n > 0 && staged_n == run_b * run_t && staged_targets &&
+            redo_if_fused_failed(run_b, run_t)) {
+            check_hip(hipMemcpyAsync(out, loss, 4, hipMemcpyDeviceToHost, ctx->stream),
+                      "loss download");
+            check_hip(hipStreamSynchronize(ctx->stream), "loss sync");
+        } else {
+            (void)take_fused_error();
+        }
     }
 
     void run(const int32_t *inputs, const int32_t *targets, int64_t batch, int64_t seq,
@@ -771,7 +910,13 @@ struct Model {
                                      hipMemcpyDeviceToHost, c.stream),
                       "logits download");
         check_hip(hipStreamSynchronize(c.stream), "forward sync");
-        check_fused();
+        run_b = batch;
+        run_t = seq;
+        if (redo_if_fused_failed(batch, seq) && loss_out) {
+            check_hip(hipMemcpyAsync(loss_out, loss, 4, hipMemcpyDeviceToHost, c.stream),
+                      "loss download");
+            check_hip(hipStreamSynchronize(c.stream), "forward sync");
+        }
     }
 
     // ---------------------------------------------------------------- training
@@ -1382,10 +1527,37 @@ int32_t mmh_model_read_loss(mmh_handle model_h, float *loss_host) {
         if (!loss_host) fail(MMH_ERR_ARGUMENT, "loss is a null pointer");
         Model &m = model(model_h);
         if (!m.loss) fail(MMH_ERR_ARGUMENT, "nothing has run on this model");
-        check_hip(hipMemcpyAsync(loss_host, m.loss, 4, hipMemcpyDeviceToHost, m.ctx->stream),
-                  "loss download");
-        check_hip(hipStreamSynchronize(m.ctx->stream), "loss sync");
-        m.check_fused();
+        m.ctx->select();
+        m.read_staged_loss(loss_host);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_fused_fallbacks(mmh_handle model_h, int64_t *redone, int32_t *last_error) {
+    return guard([&] {
+        if (!redone) fail(MMH_ERR_ARGUMENT, "redone is a null pointer");
+        const Model &m = model(model_h);
+        *redone = m.fused_fallbacks;
+        if (last_error) *last_error = m.fused_last_error;
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_fused_duration(mmh_handle model_h, int64_t batch, int64_t seq, int32_t reps,
+                                 float *median_us, float *min_us) {
+    return guard([&] {
+        if (!median_us) fail(MMH_ERR_ARGUMENT, "median_us is a null pointer");
+        Model &m = model(model_h);
+        m.ctx->select();
+        m.fused_duration(batch, seq, reps, median_us, min_us);
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_model_inject_fused_error(mmh_handle model_h, int32_t bits) {
+    return guard([&] {
+        if (bits <= 0) fail(MMH_ERR_ARGUMENT, "the injected error bits must be positive");
+        model(model_h).fused_inject = bits;
         return MMH_OK;
     });
 }

@@ -124,6 +124,9 @@ _SIGNATURES = {
     "mmh_model_read_loss": [_h, _f32p],
     "mmh_model_set_forward_path": [_h, _i32],
     "mmh_model_last_forward_fused": [_h, _i32p],
+    "mmh_model_fused_fallbacks": [_h, ctypes.POINTER(_i64), _i32p],
+    "mmh_model_inject_fused_error": [_h, _i32],
+    "mmh_model_fused_duration": [_h, _i64, _i64, _i32, _f32p, _f32p],
     "mmh_model_profile": [_h, _i64, _i64, _f32p, _i32p],
     "mmh_rms_norm_backward": [_h, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp],
     "mmh_apply_rope_backward": [_h, _vp, _i64, _i64, _i64, _vp, _vp, _vp],
@@ -1045,6 +1048,29 @@ class Model:
         v = ctypes.c_int32()
         check(lib().mmh_model_last_forward_fused(self.handle, ctypes.byref(v)))
         return bool(v.value)
+
+    def fused_fallbacks(self) -> tuple:
+        """(how many fused launches gave up and were redone on the
+        per-operation kernels, the error word of the last one)."""
+        n = ctypes.c_int64()
+        e = ctypes.c_int32()
+        check(lib().mmh_model_fused_fallbacks(self.handle, ctypes.byref(n), ctypes.byref(e)))
+        return n.value, e.value
+
+    def inject_fused_error(self, bits: int = 8):
+        """Diagnostic: the next fused launch starts with `bits` in its error
+        word, so its waits give up and the forward is redone."""
+        check(lib().mmh_model_inject_fused_error(self.handle, bits))
+
+    def fused_duration(self, batch: int, seq: int, reps: int = 200) -> tuple:
+        """(median, minimum) duration in microseconds of the fused launch on
+        the staged ids, from per-workgroup clock stamps over `reps` launches
+        run back to back."""
+        med = ctypes.c_float()
+        mn = ctypes.c_float()
+        check(lib().mmh_model_fused_duration(self.handle, batch, seq, reps, ctypes.byref(med),
+                                             ctypes.byref(mn)))
+        return med.value, mn.value
 
     def profile(self, batch: int, seq: int) -> dict:
         """One staged run with per-launch HIP events: {class: (ms, launches)}."""

@@ -147,3 +147,82 @@ def test_unfit_model_and_logits_stay_per_op(ctx):
         assert not m.last_forward_fused()
     finally:
         m.close()
+
+
+def test_fused_failure_is_redone_on_the_per_op_kernels(ctx):
+    # The fused kernel's bounded waits give up once its error word is set (a
+    # wait that reached its bound sets it; here the host presets it, so every
+    # workgroup still runs to its end). The forward is then redone on the
+    # per-operation kernels from the staged ids: the loss is the
+    # per-operation loss bit for bit, the word and the counters are cleared,
+    # and the next fused launch (eager or a graph replay) is right again.
+    cfg = mh.PRESETS["tiny"]
+    print("\n[fused failure] tiny B8 T256 seed 0, error word preset", flush=True)
+    m = mh.Model.new(ctx, cfg, 0)
+    try:
+        x, y = m.lab_tokens(8, 256)
+        m.set_forward_path(mh.PATH_PER_OP)
+        per_op = float(m.loss(x, y, 8, 256))
+        m.set_forward_path(mh.PATH_AUTO)
+        fused = float(m.loss(x, y, 8, 256))
+        assert m.last_forward_fused()
+        assert m.fused_fallbacks() == (0, 0)
+
+        # mmh_model_loss: the redo happens before it returns
+        m.inject_fused_error(8)
+        assert float(m.loss(x, y, 8, 256)) == per_op
+        assert not m.last_forward_fused()
+        n, e = m.fused_fallbacks()
+        assert n == 1 and e & 8, (n, e)
+        assert float(m.loss(x, y, 8, 256)) == fused
+        assert m.last_forward_fused()
+
+        # staged runs: eager, captured, then replays; the preset word reaches a replay
+        m.stage(x, y, 8, 256)
+        for _ in range(3):
+            m.run_staged(8, 256)
+            assert m.read_loss() == fused
+            assert m.last_forward_fused()
+        m.inject_fused_error(8)
+        m.run_staged(8, 256)
+        assert m.read_loss() == per_op
+        assert m.fused_fallbacks()[0] == 2
+        for _ in range(2):
+            m.run_staged(8, 256)
+            assert m.read_loss() == fused
+            assert m.last_forward_fused()
+
+        # a failed replay whose loss is not read before new ids are staged is
+        # redone first; the replays after it are right
+        m.inject_fused_error(16)
+        m.run_staged(8, 256)
+        m.stage(x, y, 8, 256)
+        n, e = m.fused_fallbacks()
+        assert n == 3 and e & 16, (n, e)
+        m.run_staged(8, 256)
+        assert m.read_loss() == fused
+        assert m.broken_guards() == 0
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("batch,fits", [(4160, True), (4161, False)])
+def test_fused_loss_slot_bound(ctx, batch, fits):
+    # The fused launch's last workgroup parks one f64 sum per (sequence,
+    # 32-row block) in a 4160-slot LDS stage before adding them in order; a
+    # shape with more blocks than that stays on the per-operation kernels.
+    cfg = mh.PRESETS["smoke"]
+    print(f"\n[fused slots] smoke B{batch} T1 seed 0", flush=True)
+    m = mh.Model.new(ctx, cfg, 0)
+    try:
+        x, y = m.lab_tokens(batch, 1)
+        got = float(m.loss(x, y, batch, 1))
+        assert m.last_forward_fused() == fits
+        c = oracle_config(cfg)
+        w_ref, _, _ = O.lab_setup(c, 0, batch, 1)
+        ref = float(O.forward_loss(c, w_ref, x, y, batch, 1, want_logits=False)[0])
+        print(f"  device {got:.7f} oracle {ref:.7f}", flush=True)
+        assert abs(got - ref) <= 1e-4 * ref
+        assert m.broken_guards() == 0
+    finally:
+        m.close()

@@ -85,3 +85,38 @@ def test_noalloc_unsplit_product_and_errors(ctx):
     assert lib.mmh_gemm_noalloc(424242, 0, A.ptr, B.ptr, C.ptr, 4, 4, 4, 0) == mh.ERR_ARGUMENT
     for x in (A, B, C):
         x.free()
+
+
+@pytest.mark.parametrize("accumulate", [False, True])
+def test_noalloc_tail_balanced_product(ctx, accumulate):
+    # tiles = CUs + 16 of 128 x 128 (2048 columns): the last 16 tiles are cut
+    # along K into 8 pieces (8 MiB of partials, inside the array) and summed
+    # in piece order by tail_reduce, on both entry points; then a smaller
+    # split product through the same array
+    _, cus = ctx.device_info()
+    m, k, n = 128 * (cus // 16 + 1), 2048, 2048
+    print(f"\n[gemm_noalloc tail] nn {m}x{k}x{n} ({cus} CUs) accumulate={accumulate}", flush=True)
+    for i, (form, mm, kk, nn) in enumerate((("nn", m, k, n), ("tn", 128, 1024, 96))):
+        a, b, c0 = operands(form, mm, kk, nn, seed=11 + i)
+        want = run(ctx, "alloc", form, a, b, c0, mm, kk, nn, accumulate)
+        got = run(ctx, "noalloc", form, a, b, c0, mm, kk, nn, accumulate)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (form, mm, kk, nn)
+
+
+def test_noalloc_refuses_tail_pieces_over_the_array(ctx):
+    # tiles = CUs + (CUs / 2 + 1): the tail takes 8 pieces per tile, about
+    # 66 MiB of partials on 256 CUs: the allocating entry point runs it, the
+    # no-alloc one refuses it (never a different split) and leaves C alone
+    _, cus = ctx.device_info()
+    tiles_n = 11
+    rows = -(-(cus + cus // 2 + 1) // tiles_n)
+    m, k, n = 128 * rows, 2048, 128 * tiles_n
+    print(f"\n[gemm_noalloc tail refusal] nn {m}x{k}x{n}", flush=True)
+    A, B = ctx.empty((m, k)), ctx.empty((k, n))
+    C = ctx.to_device(np.full((m, n), 3.0, np.float32))
+    st = mh.lib().mmh_gemm_noalloc(ctx.handle, 0, A.ptr, B.ptr, C.ptr, m, k, n, 0)
+    assert st == mh.ERR_SHAPE, st
+    assert "tail pieces" in mh.last_error()
+    assert np.all(C.numpy() == 3.0)
+    for x in (A, B, C):
+        x.free()
