@@ -156,7 +156,10 @@ int32_t mmh_rope_tables(mmh_handle ctx, int64_t head_dim, int64_t max_seq_len, f
 int32_t mmh_apply_rope(mmh_handle ctx, const float *x, int64_t bh, int64_t t, int64_t hd,
                        const float *cos_dev, const float *sin_dev, float *out);
 /* attention.rs:97-101: q [B,H,T,hd], k/v [B,Hkv,T,hd] (already rotated),
- * out [B,H,T,hd]; head j reads kv head j / (H/Hkv). hd in {4,8,16,32,64,128}. */
+ * out [B,H,T,hd]; head j reads kv head j / (H/Hkv). hd 4, 8, 16, 32, 64 or
+ * 128 runs on its own kernels; any other even hd below 128 on the next of
+ * those, through copies of the heads padded with zero columns (the scale
+ * stays 1/sqrt(hd)); hd above 128 is MMH_ERR_SHAPE. The backward likewise. */
 int32_t mmh_causal_attention(mmh_handle ctx, const float *q, const float *k, const float *v,
                              int64_t b, int64_t h, int64_t hkv, int64_t t, int64_t hd,
                              float *out);
@@ -202,7 +205,9 @@ int32_t mmh_cross_entropy(mmh_handle ctx, const float *logits, const int32_t *ta
 
 /* model.rs:51-83 with weights given by the caller in the reference parameter
  * order (docs/midman-model.md:20): embed; per block attn_norm, q, k, v, o,
- * mlp_norm, gate, up, down; final_norm; lm_head if untied. */
+ * mlp_norm, gate, up, down; final_norm; lm_head if untied. The config checks
+ * are config.rs:106-138's (MMH_ERR_CONFIG), plus a head width of at most 128
+ * (d_model / n_heads; every even width up to it is taken). */
 int32_t mmh_model_create(mmh_handle ctx, const double config[10], const float *weights_host,
                          int64_t n_weights, mmh_handle *out_model);
 /* MidManModel::with_init_std(config, std, &mut Rng::seed_from_u64(seed))

@@ -719,8 +719,10 @@ template <int HD, bool INV>
 __global__ __launch_bounds__(256) void rope_rows_kernel(float *__restrict__ x, int64_t sb,
                                                         int64_t sh, int64_t st, int nh, int t,
                                                         const float *__restrict__ cos_t,
-                                                        const float *__restrict__ sin_t) {
-    constexpr int HALF = HD / 2;
+                                                        const float *__restrict__ sin_t,
+                                                        int half_any) {
+    // HD 0: a head of any even width, half_any pairs
+    const int HALF = HD ? HD / 2 : half_any;
     const int row = blockIdx.x;
     const int bb = row / t, pos = row - bb * t;
     float *base = x + bb * sb + pos * st;
@@ -770,22 +772,23 @@ template <bool INV>
 void launch_rope_rows(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int nhi,
                       int ti, int64_t hd, const float *cos_t, const float *sin_t, dim3 grid) {
     const dim3 block(256);
+    const int half = (int)(hd / 2);
     switch (hd) {
-        case 4: hipLaunchKernelGGL((rope_rows_kernel<4, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 8: hipLaunchKernelGGL((rope_rows_kernel<8, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 16: hipLaunchKernelGGL((rope_rows_kernel<16, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 32: hipLaunchKernelGGL((rope_rows_kernel<32, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        case 64: hipLaunchKernelGGL((rope_rows_kernel<64, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
-        default: hipLaunchKernelGGL((rope_rows_kernel<128, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t); break;
+        case 4: hipLaunchKernelGGL((rope_rows_kernel<4, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
+        case 8: hipLaunchKernelGGL((rope_rows_kernel<8, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
+        case 16: hipLaunchKernelGGL((rope_rows_kernel<16, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
+        case 32: hipLaunchKernelGGL((rope_rows_kernel<32, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
+        case 64: hipLaunchKernelGGL((rope_rows_kernel<64, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
+        case 128: hipLaunchKernelGGL((rope_rows_kernel<128, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
+        default: hipLaunchKernelGGL((rope_rows_kernel<0, INV>), grid, block, 0, ctx.stream, x, sb, sh, st, nhi, ti, cos_t, sin_t, half); break;
     }
 }
 
 void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,
                          int64_t nh, int64_t t, int64_t hd, const float *cos_t,
                          const float *sin_t, bool inverse) {
-    if (nb * t > 0x7fffffff) fail(MMH_ERR_SHAPE, "rope: too many rows");
-    if (hd != 4 && hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
-        fail(MMH_ERR_SHAPE, "rope: head_dim must be 4, 8, 16, 32, 64 or 128");
+    if (nb * t > 0x7fffffff || nh * (hd / 2) > 0x7fffffff) fail(MMH_ERR_SHAPE, "rope: too many rows");
+    if (hd <= 0 || hd % 2) fail(MMH_ERR_SHAPE, "rope: head_dim must be even");
     const dim3 grid((unsigned)(nb * t));
     if (inverse)
         launch_rope_rows<true>(ctx, x, sb, sh, st, (int)nh, (int)t, hd, cos_t, sin_t, grid);
@@ -794,33 +797,87 @@ void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t
     check_hip(hipGetLastError(), "rope launch");
 }
 
-void attention(Context &ctx, const AttnDesc &d) {
-    if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
-        fail(MMH_ERR_SHAPE, "attention: empty shape");
-    if (d.h % d.hkv != 0) fail(MMH_ERR_SHAPE, "attention: n_heads is not a multiple of n_kv_heads");
-    if (d.b > 65535 || d.h > 0x7fffffff || d.t > 0x3fffffff)
-        fail(MMH_ERR_SHAPE, "attention: shape too large");
-    if (d.hd != 4 && d.hd != 8 && d.hd != 16 && d.hd != 32 && d.hd != 64 && d.hd != 128)
-        fail(MMH_ERR_SHAPE, "attention: head_dim must be 4, 8, 16, 32, 64 or 128");
+bool native_head(int64_t hd) {
+    return hd == 4 || hd == 8 || hd == 16 || hd == 32 || hd == 64 || hd == 128;
+}
+
+int64_t kernel_head(int64_t hd) {
+    for (int64_t w : {4, 8, 16, 32, 64, 128})
+        if (hd <= w) return w;
+    return 0;
+}
+
+namespace {
+
+// Heads of [nb, nh, t, hd] at strides (sb, sh, st) <-> contiguous heads of hp
+// >= hd columns, zero beyond hd: one workgroup per (batch, position) row.
+__global__ __launch_bounds__(256) void pad_heads_kernel(const float *__restrict__ src, int64_t sb,
+                                                        int64_t sh, int64_t st, int nh, int t,
+                                                        int hd, float *__restrict__ dst, int hp) {
+    const int row = blockIdx.x;
+    const int bb = row / t, pos = row - bb * t;
+    const float *s = src + bb * sb + pos * st;
+    for (int i = threadIdx.x; i < nh * hp; i += 256) {
+        const int hh = i / hp, c = i - hh * hp;
+        dst[(((int64_t)bb * nh + hh) * t + pos) * hp + c] = c < hd ? s[hh * sh + c] : 0.0f;
+    }
+}
+
+__global__ __launch_bounds__(256) void unpad_heads_kernel(const float *__restrict__ src, int hp,
+                                                          int nh, int t, int hd,
+                                                          float *__restrict__ dst, int64_t sb,
+                                                          int64_t sh, int64_t st) {
+    const int row = blockIdx.x;
+    const int bb = row / t, pos = row - bb * t;
+    float *o = dst + bb * sb + pos * st;
+    for (int i = threadIdx.x; i < nh * hd; i += 256) {
+        const int hh = i / hd, c = i - hh * hd;
+        o[hh * sh + c] = src[(((int64_t)bb * nh + hh) * t + pos) * hp + c];
+    }
+}
+
+}  // namespace
+
+void launch_pad_heads(Context &ctx, const float *src, int64_t sb, int64_t sh, int64_t st,
+                      int64_t nb, int64_t nh, int64_t t, int64_t hd, float *dst, int64_t hp) {
+    if (nb * t > 0x7fffffff || nh * hp > 0x7fffffff) fail(MMH_ERR_SHAPE, "attention: shape too large");
+    hipLaunchKernelGGL(pad_heads_kernel, dim3((unsigned)(nb * t)), dim3(256), 0, ctx.stream, src,
+                       sb, sh, st, (int)nh, (int)t, (int)hd, dst, (int)hp);
+    check_hip(hipGetLastError(), "pad heads launch");
+}
+
+void launch_unpad_heads(Context &ctx, const float *src, int64_t hp, int64_t nb, int64_t nh,
+                        int64_t t, int64_t hd, float *dst, int64_t sb, int64_t sh, int64_t st) {
+    if (nb * t > 0x7fffffff || nh * hd > 0x7fffffff) fail(MMH_ERR_SHAPE, "attention: shape too large");
+    hipLaunchKernelGGL(unpad_heads_kernel, dim3((unsigned)(nb * t)), dim3(256), 0, ctx.stream, src,
+                       (int)hp, (int)nh, (int)t, (int)hd, dst, sb, sh, st);
+    check_hip(hipGetLastError(), "unpad heads launch");
+}
+
+// q and k rotated in place (the forward's RoPE, or its inverse on gradients);
+// one launch when the k heads directly follow the q heads in each row (the
+// fused QKV layout).
+void rope_qk(Context &ctx, float *q, float *k, int64_t sqb, int64_t sqh, int64_t sqt, int64_t skb,
+             int64_t skh, int64_t skt, int64_t b, int64_t h, int64_t hkv, int64_t t, int64_t hd,
+             const float *cos_t, const float *sin_t, bool inverse) {
+    if (k == q + h * sqh && skb == sqb && skh == sqh && skt == sqt) {
+        launch_rope_strided(ctx, q, sqb, sqh, sqt, b, h + hkv, t, hd, cos_t, sin_t, inverse);
+    } else {
+        launch_rope_strided(ctx, q, sqb, sqh, sqt, b, h, t, hd, cos_t, sin_t, inverse);
+        launch_rope_strided(ctx, k, skb, skh, skt, b, hkv, t, hd, cos_t, sin_t, inverse);
+    }
+}
+
+namespace {
+
+// The kernels on heads of a width they take (4, 8, 16, 32, 64 or 128),
+// scores scaled by `scale`.
+void attention_kernels(Context &ctx, const AttnDesc &d, float scale) {
     const int64_t strides[] = {d.sqb, d.sqh, d.sqt, d.skb, d.skh, d.skt, d.svb, d.svh, d.svt};
     for (int64_t s : strides)
         if (s % 4) fail(MMH_ERR_SHAPE, "attention: strides must be multiples of 4 floats");
     if (!al16(d.q) || !al16(d.k) || !al16(d.v))
         fail(MMH_ERR_ARGUMENT, "attention: q, k and v must be 16-byte aligned");
-    if (d.cos_t) {
-        // q and k rows are rotated in place before the kernel reads them; when
-        // the k heads directly follow the q heads in each row (the fused QKV
-        // layout), one launch covers both.
-        if (d.k == d.q + d.h * d.sqh && d.skb == d.sqb && d.skh == d.sqh && d.skt == d.sqt) {
-            launch_rope_strided(ctx, const_cast<float *>(d.q), d.sqb, d.sqh, d.sqt, d.b,
-                                d.h + d.hkv, d.t, d.hd, d.cos_t, d.sin_t);
-        } else {
-            launch_rope_strided(ctx, const_cast<float *>(d.q), d.sqb, d.sqh, d.sqt, d.b, d.h, d.t,
-                                d.hd, d.cos_t, d.sin_t);
-            launch_rope_strided(ctx, const_cast<float *>(d.k), d.skb, d.skh, d.skt, d.b, d.hkv,
-                                d.t, d.hd, d.cos_t, d.sin_t);
-        }
-    }
     AttnP p{};
     p.q = d.q;
     p.k = d.k;
@@ -839,7 +896,7 @@ void attention(Context &ctx, const AttnDesc &d) {
     const int cus = ctx.cu_count > 0 ? ctx.cu_count : 256;
     const bool split = d.hd <= 64 && d.b * d.h * ((d.t + 127) / 128) < cus;
     p.nqb = (int)(split ? (d.t + 31) / 32 : (d.t + 127) / 128);
-    p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
+    p.scale = scale;
     dim3 grid((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
     // the 16-row kernel stores rows as float4s
     const bool rows16 = al16(d.out) && d.sob % 4 == 0 && d.soh % 4 == 0 && d.sot % 4 == 0;
@@ -852,6 +909,54 @@ void attention(Context &ctx, const AttnDesc &d) {
         default: launch_hd<128>(ctx, p, grid, split, rows16); break;
     }
     check_hip(hipGetLastError(), "attention launch");
+}
+
+}  // namespace
+
+void attention(Context &ctx, const AttnDesc &d) {
+    if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
+        fail(MMH_ERR_SHAPE, "attention: empty shape");
+    if (d.h % d.hkv != 0) fail(MMH_ERR_SHAPE, "attention: n_heads is not a multiple of n_kv_heads");
+    if (d.b > 65535 || d.h > 0x7fffffff || d.t > 0x3fffffff)
+        fail(MMH_ERR_SHAPE, "attention: shape too large");
+    const int64_t hp = kernel_head(d.hd);
+    if (hp == 0 || (!native_head(d.hd) && d.hd % 2))
+        fail(MMH_ERR_SHAPE, "attention: head_dim must be 4, 8, 16, 32, 64 or 128, or even and "
+                            "below 128");
+    // q and k rows are rotated in place before the kernel reads them
+    if (d.cos_t)
+        rope_qk(ctx, const_cast<float *>(d.q), const_cast<float *>(d.k), d.sqb, d.sqh, d.sqt,
+                d.skb, d.skh, d.skt, d.b, d.h, d.hkv, d.t, d.hd, d.cos_t, d.sin_t, false);
+    const float scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
+    if (native_head(d.hd)) {
+        attention_kernels(ctx, d, scale);
+        return;
+    }
+    // Other even widths run on the next kernel width: q, k, v copied into
+    // heads of hp columns, zero beyond hd (a zero column adds nothing to a
+    // score; output columns past hd are dropped), the scale that of hd.
+    const int64_t nq = d.b * d.h * d.t * hp, nk = d.b * d.hkv * d.t * hp;
+    float *qp = static_cast<float *>(
+        ctx.workspace(Context::kPadSlot, (size_t)(2 * nq + 2 * nk) * 4));
+    float *kp = qp + nq, *vp = kp + nk, *op = vp + nk;
+    launch_pad_heads(ctx, d.q, d.sqb, d.sqh, d.sqt, d.b, d.h, d.t, d.hd, qp, hp);
+    launch_pad_heads(ctx, d.k, d.skb, d.skh, d.skt, d.b, d.hkv, d.t, d.hd, kp, hp);
+    launch_pad_heads(ctx, d.v, d.svb, d.svh, d.svt, d.b, d.hkv, d.t, d.hd, vp, hp);
+    AttnDesc e = d;
+    e.q = qp;
+    e.k = kp;
+    e.v = vp;
+    e.out = op;
+    e.sqb = e.sob = d.h * d.t * hp;
+    e.sqh = e.soh = d.t * hp;
+    e.sqt = e.sot = hp;
+    e.skb = e.svb = d.hkv * d.t * hp;
+    e.skh = e.svh = d.t * hp;
+    e.skt = e.svt = hp;
+    e.hd = hp;
+    e.cos_t = e.sin_t = nullptr;
+    attention_kernels(ctx, e, scale);
+    launch_unpad_heads(ctx, op, hp, d.b, d.h, d.t, d.hd, d.out, d.sob, d.soh, d.sot);
 }
 
 }  // namespace mmh

@@ -1088,15 +1088,11 @@ int64_t attention_backward_scratch_floats(int64_t b, int64_t h, int64_t hkv, int
     return h > hkv ? 2 * b * h * t * hd : 0;
 }
 
-void attention_backward(Context &ctx, const AttnBwdDesc &d) {
-    if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
-        fail(MMH_ERR_SHAPE, "attention backward: empty shape");
-    if (d.h % d.hkv != 0)
-        fail(MMH_ERR_SHAPE, "attention backward: n_heads is not a multiple of n_kv_heads");
-    if (d.b > 65535 || d.h > 65535 || d.t > 0x3fffffff)
-        fail(MMH_ERR_SHAPE, "attention backward: shape too large");
-    if (d.hd != 4 && d.hd != 8 && d.hd != 16 && d.hd != 32 && d.hd != 64 && d.hd != 128)
-        fail(MMH_ERR_SHAPE, "attention backward: head_dim must be 4, 8, 16, 32, 64 or 128");
+namespace {
+
+// The kernels on heads of a width they take, scores scaled by `scale`; no
+// rotation (the caller's).
+void backward_kernels(Context &ctx, const AttnBwdDesc &d, float scale) {
     const int64_t strides[] = {d.sqb, d.sqh, d.sqt, d.skb, d.skh, d.skt,
                                d.svb, d.svh, d.svt, d.sob, d.soh, d.sot};
     for (int64_t s : strides)
@@ -1126,7 +1122,7 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
     p.t = (int)d.t;
     p.nqb = (int)((d.t + 127) / 128);
     p.nkb = p.nqb;
-    p.scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
+    p.scale = scale;
     // GQA: per-query-head partials when the caller gave room for them and the
     // head is wide enough for the float4 sum (hd >= 4 always holds).
     // small grids (fewer 128-row blocks than CUs, heads up to 64 wide): the
@@ -1175,17 +1171,68 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d) {
                            d.skh, d.skt, d.dv, d.svb, d.svh, d.svt);
         check_hip(hipGetLastError(), "dk/dv group sum launch");
     }
-    if (d.cos_t) {
-        if (d.dk == d.dq + d.h * d.sqh && d.skb == d.sqb && d.skh == d.sqh && d.skt == d.sqt) {
-            launch_rope_strided(ctx, d.dq, d.sqb, d.sqh, d.sqt, d.b, d.h + d.hkv, d.t, d.hd,
-                                d.cos_t, d.sin_t, true);
-        } else {
-            launch_rope_strided(ctx, d.dq, d.sqb, d.sqh, d.sqt, d.b, d.h, d.t, d.hd, d.cos_t,
-                                d.sin_t, true);
-            launch_rope_strided(ctx, d.dk, d.skb, d.skh, d.skt, d.b, d.hkv, d.t, d.hd, d.cos_t,
-                                d.sin_t, true);
-        }
+}
+
+}  // namespace
+
+void attention_backward(Context &ctx, const AttnBwdDesc &d) {
+    if (d.b <= 0 || d.h <= 0 || d.hkv <= 0 || d.t <= 0 || d.hd <= 0)
+        fail(MMH_ERR_SHAPE, "attention backward: empty shape");
+    if (d.h % d.hkv != 0)
+        fail(MMH_ERR_SHAPE, "attention backward: n_heads is not a multiple of n_kv_heads");
+    if (d.b > 65535 || d.h > 65535 || d.t > 0x3fffffff)
+        fail(MMH_ERR_SHAPE, "attention backward: shape too large");
+    const int64_t hp = kernel_head(d.hd);
+    if (hp == 0 || (!native_head(d.hd) && d.hd % 2))
+        fail(MMH_ERR_SHAPE, "attention backward: head_dim must be 4, 8, 16, 32, 64 or 128, or "
+                            "even and below 128");
+    const float scale = 1.0f / sqrtf((float)d.hd);  // attention.rs:82
+    if (native_head(d.hd)) {
+        backward_kernels(ctx, d, scale);
+    } else {
+        // Other even widths on the next kernel width (as the forward): q, k,
+        // v, o and dO copied into heads of hp columns, zero beyond hd (zero
+        // columns change no score, no dP and no rowsum(dO * O)), the
+        // gradients' columns below hd copied back; the GQA partials in the
+        // same buffer.
+        const int64_t nq = d.b * d.h * d.t * hp, nk = d.b * d.hkv * d.t * hp;
+        const int64_t part = d.h > d.hkv ? 2 * nq : 0;
+        float *qp = static_cast<float *>(
+            ctx.workspace(Context::kPadSlot, (size_t)(4 * nq + 4 * nk + part) * 4));
+        float *op = qp + nq, *gp = op + nq, *kp = gp + nq, *vp = kp + nk, *dqp = vp + nk,
+              *dkp = dqp + nq, *dvp = dkp + nk, *pp = dvp + nk;
+        launch_pad_heads(ctx, d.q, d.sqb, d.sqh, d.sqt, d.b, d.h, d.t, d.hd, qp, hp);
+        launch_pad_heads(ctx, d.k, d.skb, d.skh, d.skt, d.b, d.hkv, d.t, d.hd, kp, hp);
+        launch_pad_heads(ctx, d.v, d.svb, d.svh, d.svt, d.b, d.hkv, d.t, d.hd, vp, hp);
+        launch_pad_heads(ctx, d.o, d.sob, d.soh, d.sot, d.b, d.h, d.t, d.hd, op, hp);
+        launch_pad_heads(ctx, d.dout, d.sob, d.soh, d.sot, d.b, d.h, d.t, d.hd, gp, hp);
+        AttnBwdDesc e = d;
+        e.q = qp;
+        e.k = kp;
+        e.v = vp;
+        e.o = op;
+        e.dout = gp;
+        e.dq = dqp;
+        e.dk = dkp;
+        e.dv = dvp;
+        e.sqb = e.sob = d.h * d.t * hp;
+        e.sqh = e.soh = d.t * hp;
+        e.sqt = e.sot = hp;
+        e.skb = e.svb = d.hkv * d.t * hp;
+        e.skh = e.svh = d.t * hp;
+        e.skt = e.svt = hp;
+        e.hd = hp;
+        e.cos_t = e.sin_t = nullptr;
+        e.scratch = part ? pp : nullptr;
+        backward_kernels(ctx, e, scale);
+        launch_unpad_heads(ctx, dqp, hp, d.b, d.h, d.t, d.hd, d.dq, d.sqb, d.sqh, d.sqt);
+        launch_unpad_heads(ctx, dkp, hp, d.b, d.hkv, d.t, d.hd, d.dk, d.skb, d.skh, d.skt);
+        launch_unpad_heads(ctx, dvp, hp, d.b, d.hkv, d.t, d.hd, d.dv, d.svb, d.svh, d.svt);
     }
+    // RoPE backward on dq and dk
+    if (d.cos_t)
+        rope_qk(ctx, d.dq, d.dk, d.sqb, d.sqh, d.sqt, d.skb, d.skh, d.skt, d.b, d.h, d.hkv, d.t,
+                d.hd, d.cos_t, d.sin_t, true);
 }
 
 }  // namespace mmh

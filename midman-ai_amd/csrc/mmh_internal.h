@@ -53,7 +53,10 @@ void check_hip(hipError_t e, const char *what);
 
 // One device + one stream + growable workspaces.
 struct Context {
-    static constexpr int kSlots = 4;  // 0 split-K partials, 1 ids, 2 op temporaries, 3 losses
+    // 0 split-K partials, 1 ids, 2 op temporaries, 3 losses, 4 attention heads
+    // padded to a kernel width
+    static constexpr int kSlots = 5;
+    static constexpr int kPadSlot = 4;
     int device = 0;
     hipStream_t stream = nullptr;
     hipEvent_t t0 = nullptr, t1 = nullptr;
@@ -62,8 +65,8 @@ struct Context {
     // creation): what the fused forward's per-XCD teams need
     bool xcd_teams = false;
     std::string name;
-    void *ws[kSlots] = {nullptr, nullptr, nullptr, nullptr};
-    size_t ws_bytes[kSlots] = {0, 0, 0, 0};
+    void *ws[kSlots] = {};
+    size_t ws_bytes[kSlots] = {};
     // Allocations made through mmh_alloc, freed at destroy.
     std::vector<void *> owned;
 
@@ -302,5 +305,21 @@ void attention_backward(Context &ctx, const AttnBwdDesc &d);
 void launch_rope_strided(Context &ctx, float *x, int64_t sb, int64_t sh, int64_t st, int64_t nb,
                          int64_t nh, int64_t t, int64_t hd, const float *cos_t,
                          const float *sin_t, bool inverse = false);
+// q and k heads rotated in place (one launch when k's heads follow q's in each
+// row, as in the fused QKV layout).
+void rope_qk(Context &ctx, float *q, float *k, int64_t sqb, int64_t sqh, int64_t sqt, int64_t skb,
+             int64_t skh, int64_t skt, int64_t b, int64_t h, int64_t hkv, int64_t t, int64_t hd,
+             const float *cos_t, const float *sin_t, bool inverse);
+// Head widths the attention kernels take directly; kernel_head(hd) is the
+// smallest of them >= hd (0 above 128): other even widths run on it through
+// zero-padded copies of the heads.
+bool native_head(int64_t hd);
+int64_t kernel_head(int64_t hd);
+// [nb, nh, t, hd] heads at strides (sb, sh, st) into contiguous [nb, nh, t, hp]
+// with zeros beyond hd, and back (columns below hd only).
+void launch_pad_heads(Context &ctx, const float *src, int64_t sb, int64_t sh, int64_t st,
+                      int64_t nb, int64_t nh, int64_t t, int64_t hd, float *dst, int64_t hp);
+void launch_unpad_heads(Context &ctx, const float *src, int64_t hp, int64_t nb, int64_t nh,
+                        int64_t t, int64_t hd, float *dst, int64_t sb, int64_t sh, int64_t st);
 
 }  // namespace mmh

@@ -98,10 +98,12 @@ Config parse_config(const double *v) {
     if (c.d % c.heads) fail(MMH_ERR_CONFIG, "d_model is not divisible by n_heads");
     if (c.heads % c.kv_heads) fail(MMH_ERR_CONFIG, "n_heads is not divisible by n_kv_heads");
     if (c.hd() & 1) fail(MMH_ERR_CONFIG, "head dimension must be even for rotary embeddings");
-    const int64_t hd = c.hd();
-    if (hd != 4 && hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
-        fail(MMH_ERR_CONFIG, "head dimension " + std::to_string(hd) +
-                                 " is not one of the device attention sizes 4, 8, 16, 32, 64, 128");
+    // every even head width the reference accepts (config.rs:130-135) up to
+    // 128: 4, 8, 16, 32, 64 and 128 on their own kernels, the others on the
+    // next of those through zero-padded heads
+    if (c.hd() > 128)
+        fail(MMH_ERR_CONFIG, "head dimension " + std::to_string(c.hd()) +
+                                 " is above the device attention's 128");
     return c;
 }
 
@@ -285,7 +287,7 @@ struct Model {
     hipGraphExec_t graph_exec = nullptr;
     int64_t graph_b = 0, graph_t = 0, warm_b = 0, warm_t = 0;
     const void *graph_act = nullptr, *warm_act = nullptr, *graph_ws = nullptr,
-               *graph_arena = nullptr;
+               *graph_pad = nullptr, *graph_arena = nullptr;
     bool graph_fused = false;  // the captured graph is the fused launch
     // The fused loss-only forward (fused_forward.hip): its arena, laid out for
     // (fused_b, fused_t); forward_path 1 keeps every forward on the
@@ -337,7 +339,7 @@ struct Model {
         graph_exec = nullptr;
         graph = nullptr;
         graph_b = graph_t = 0;
-        graph_act = graph_ws = graph_arena = nullptr;
+        graph_act = graph_ws = graph_pad = graph_arena = nullptr;
         graph_fused = false;
     }
 
@@ -782,7 +784,8 @@ struct Model {
         // (a graph of the fused launch also needs the arena it was captured
         // with, still laid out for this shape)
         if (graph_exec && graph_b == batch && graph_t == seq && graph_act == act &&
-            graph_ws == ctx->ws[0] && staged_n == batch * seq && staged_targets &&
+            graph_ws == ctx->ws[0] && graph_pad == ctx->ws[Context::kPadSlot] &&
+            staged_n == batch * seq && staged_targets &&
             (!graph_fused || (graph_arena == fused_arena && fused_b == batch && fused_t == seq))) {
             if (graph_fused) apply_fused_inject();
             check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");
@@ -820,6 +823,7 @@ struct Model {
         graph_t = seq;
         graph_act = act;
         graph_ws = ctx->ws[0];
+        graph_pad = ctx->ws[Context::kPadSlot];
         graph_arena = fused_arena;
         graph_fused = last_fused;
         check_hip(hipGraphLaunch(graph_exec, ctx->stream), "graph launch");

@@ -653,8 +653,7 @@ int32_t mmh_apply_rope_backward(mmh_handle ctx, const float *dy, int64_t bh, int
         need(sin_dev, "sin");
         positive(bh, "bh");
         positive(t, "time");
-        if (hd != 4 && hd != 8 && hd != 16 && hd != 32 && hd != 64 && hd != 128)
-            fail(MMH_ERR_SHAPE, "rope backward: head_dim must be 4, 8, 16, 32, 64 or 128");
+        if (hd <= 0 || (hd & 1)) fail(MMH_ERR_SHAPE, "rope backward: the last axis must be even");
         if (dx != dy)
             check_hip(hipMemcpyAsync(dx, dy, (size_t)(bh * t * hd) * 4, hipMemcpyDeviceToDevice,
                                      cx.stream),

@@ -125,6 +125,41 @@ def test_small_width_forwards_against_oracle(ctx, cfg, batch, seq):
 
 
 @pytest.mark.parametrize("cfg,batch,seq", [
+    ([20, 12, 2, 2, 1, 16, 16, 10000.0, 1e-5, 1], 2, 13),      # hd 6 on 8, head stride 6
+    ([97, 96, 2, 4, 2, 64, 64, 10000.0, 1e-5, 1], 3, 40),      # hd 24 on 32, GQA
+    ([101, 96, 1, 2, 1, 80, 100, 10000.0, 1e-5, 0], 2, 70),    # hd 48 on 64, untied
+    ([64, 192, 1, 2, 2, 128, 160, 10000.0, 1e-5, 1], 1, 130),  # hd 96 on 128
+])
+def test_padded_head_widths_against_oracle(ctx, cfg, batch, seq):
+    # every even head width the reference accepts (config.rs:130-135): the
+    # ones the attention kernels do not take run on the next kernel width
+    # through zero-padded heads; logits, the loss-only forward and the staged
+    # graph replays against the oracle
+    print(f"\n[model] padded heads {cfg[:7]} B{batch} T{seq}", flush=True)
+    c = oracle_config(cfg)
+    w = O.init_weights(c, O.rng(29), std=0.1)
+    r = np.random.default_rng(seq + cfg[1])
+    x = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    y = r.integers(0, cfg[0], batch * seq).astype(np.int32)
+    m = mh.Model.from_weights(ctx, cfg, w)
+    try:
+        loss, logits = m.forward_loss(x, y, batch, seq)
+        ref_loss, ref_logits = O.forward_loss(c, w, x, y, batch, seq)
+        print(f"  loss gpu {loss:.7f} oracle {ref_loss:.7f}", flush=True)
+        assert abs(loss - ref_loss) / ref_loss <= 1e-4
+        check_logits(logits, ref_logits, "padded-head logits")
+        only = float(m.loss(x, y, batch, seq))
+        assert abs(only - ref_loss) / ref_loss <= 1e-4
+        m.stage(x, y, batch, seq)
+        for _ in range(3):  # eager, captured, replayed
+            m.run_staged(batch, seq)
+            assert m.read_loss() == only
+        assert m.broken_guards() == 0
+    finally:
+        m.close()
+
+
+@pytest.mark.parametrize("cfg,batch,seq", [
     # enough rows x 128-column tiles (>= the CU count) for the 128x128 head
     # kernel, which folds the loss in when only the loss is asked for; the
     # vocabularies end in a partial column tile
@@ -351,6 +386,10 @@ def test_model_errors(ctx):
         m.forward(np.zeros(129, np.int32), 1, 129)  # seq > max_seq_len
     with pytest.raises(mh.ConfigError):
         mh.Model.new(ctx, [256, 64, 2, 3, 1, 176, 128, 10000.0, 1e-5, 1], 0)
+    with pytest.raises(mh.ConfigError):  # an odd head width (config.rs:130-135)
+        mh.Model.new(ctx, [256, 20, 2, 4, 1, 176, 128, 10000.0, 1e-5, 1], 0)
+    with pytest.raises(mh.ConfigError):  # a head above the device's 128
+        mh.Model.new(ctx, [256, 512, 1, 2, 1, 176, 128, 10000.0, 1e-5, 1], 0)
     with pytest.raises(mh.ArgumentError):
         mh.Model.new(ctx, [256.5, 64, 2, 4, 4, 176, 128, 10000.0, 1e-5, 1], 0)
     with pytest.raises(mh.ShapeError):

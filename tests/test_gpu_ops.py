@@ -115,6 +115,15 @@ ATTN_CASES = [
     # the key-split kernel's 8-wave form (blocks of more than 4 key tiles)
     (2, 4, 2, 200, 64),
     (1, 2, 1, 150, 16),
+    # other even widths (config.rs:130-135 takes any), on the next kernel
+    # width through zero-padded heads: key-split, paired and 16-row kernels
+    (2, 4, 2, 37, 6),
+    (1, 4, 2, 130, 24),
+    (2, 2, 1, 300, 48),
+    (1, 4, 4, 200, 96),
+    (4, 16, 8, 512, 48),
+    (2, 16, 8, 1024, 96),
+    (1, 3, 1, 9, 2),
 ]
 
 
@@ -148,10 +157,14 @@ def test_attention_rejects_bad_shapes(ctx):
     k = ctx.empty((1, 2, 4, 8))
     with pytest.raises(mh.ShapeError):
         mh.causal_attention(ctx, q, k, k)
-    q2 = ctx.empty((1, 2, 4, 12))
-    k2 = ctx.empty((1, 2, 4, 12))
-    with pytest.raises(mh.ShapeError):  # head dim outside the device sizes
-        mh.causal_attention(ctx, q2, k2, k2)
+    # every even head width up to 128 is taken (test_causal_attention); an
+    # odd width (no rotation pairs) and one above 128 are refused before any
+    # launch
+    for hd in (7, 130):
+        q2 = ctx.empty((1, 2, 4, hd))
+        k2 = ctx.empty((1, 2, 4, hd))
+        with pytest.raises(mh.ShapeError):
+            mh.causal_attention(ctx, q2, k2, k2)
 
 
 @pytest.mark.parametrize("B,T,d,H,Hkv", [(2, 12, 16, 2, 1), (2, 64, 256, 4, 2),

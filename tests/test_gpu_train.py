@@ -32,6 +32,12 @@ CASES = {
     # the down projection's backward (SwiGLU-backward epilogue) at 352 tiles of
     # 128x128 on 256 CUs: its last 96 tiles run as K-pieces plus tail_reduce
     "tail_pieces_d512_t2048": ([64, 512, 1, 4, 4, 2816, 2048, 10000.0, 1e-5, 1], 1, 2048, 0.05),
+    # head widths the attention kernels take through zero-padded heads (6 on
+    # 8, 24 on 32, 48 and 96 on 64 and 128), GQA, tied and untied
+    "hd6_gqa": ([20, 12, 2, 2, 1, 16, 16, 10000.0, 1e-5, 1], 2, 13, 0.3),
+    "hd24_gqa": ([97, 96, 2, 4, 2, 64, 64, 10000.0, 1e-5, 1], 2, 40, 0.1),
+    "hd48_untied": ([101, 96, 1, 2, 1, 80, 100, 10000.0, 1e-5, 0], 2, 70, 0.1),
+    "hd96_t130": ([64, 192, 1, 2, 2, 128, 160, 10000.0, 1e-5, 1], 1, 130, 0.08),
 }
 
 
@@ -96,6 +102,9 @@ ATTN_SHAPES = [  # B, H, Hkv, T, hd
     (4, 16, 8, 1024, 128), (1, 16, 8, 2048, 128),
     # a lone position and a single partial tile at hd 128 (the 16-row kernels)
     (1, 2, 1, 1, 128), (2, 4, 2, 17, 128),
+    # other even widths, on the next kernel width through zero-padded heads
+    (1, 2, 1, 45, 6), (2, 4, 2, 100, 24), (1, 4, 2, 130, 48), (1, 2, 1, 257, 96),
+    (4, 16, 8, 512, 48), (1, 3, 1, 9, 2),
 ]
 
 
@@ -140,7 +149,7 @@ def test_rms_norm_backward_matches_oracle(ctx, rows, d):
 
 def test_rope_backward_is_bit_exact(ctx):
     r = np.random.default_rng(5)
-    for hd, t in ((4, 9), (16, 33), (64, 100), (128, 64)):
+    for hd, t in ((4, 9), (16, 33), (64, 100), (128, 64), (6, 20), (24, 50), (96, 31)):
         tables = mh.RotaryTables(ctx, hd, 128)
         cos, sin = mo.rope_tables(hd, 128)
         dy = r.standard_normal((3, t, hd)).astype(np.float32)

@@ -283,12 +283,13 @@ def test_rope_formula_and_norm():
     assert y[0, 0, t, 1] == np.float32(want0) and y[0, 0, t, 5] == np.float32(want1)
 
 
-def test_rope_relative_position():
+@pytest.mark.parametrize("hd", [8, 6, 24])
+def test_rope_relative_position(hd):
     # q_i . k_j depends on i - j only (rope.rs:351-368)
-    cos, sin = O.rope_tables(8, 16, 10000.0)
+    cos, sin = O.rope_tables(hd, 16, 10000.0)
     rng = np.random.default_rng(1)
-    q = rng.standard_normal(8).astype(np.float32)
-    k = rng.standard_normal(8).astype(np.float32)
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal(hd).astype(np.float32)
     Q = O.apply_rope(np.tile(q, (16, 1))[None], cos, sin)[0]
     K = O.apply_rope(np.tile(k, (16, 1))[None], cos, sin)[0]
     assert abs(float(Q[5] @ K[2]) - float(Q[9] @ K[6])) < 1e-4
@@ -304,9 +305,12 @@ def test_attention_score_scaling(goldens):
     assert np.all(np.abs(out - want) < 1e-6)
 
 
-def test_attention_against_float64_softmax_and_gqa():
-    rng = np.random.default_rng(3)
-    B, H, Hkv, T, hd = 2, 4, 2, 9, 8
+@pytest.mark.parametrize("hd", [8, 6, 24, 48])
+def test_attention_against_float64_softmax_and_gqa(hd):
+    # head widths the device runs on its own kernels (8) and through padded
+    # heads (6, 24, 48): the oracle's loops take any width
+    rng = np.random.default_rng(3 + hd)
+    B, H, Hkv, T = 2, 4, 2, 9
     q = rng.standard_normal((B, H, T, hd)).astype(np.float32)
     k = rng.standard_normal((B, Hkv, T, hd)).astype(np.float32)
     v = rng.standard_normal((B, Hkv, T, hd)).astype(np.float32)
