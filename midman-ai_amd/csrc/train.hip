@@ -2,8 +2,10 @@
 // attention, the global gradient norm and the fused clip + AdamW update.
 //
 //   cross entropy forward + backward (ops_reduce.rs:236-275), one row per
-//     workgroup: the row's max and sum in one pass, then dlogits written in
-//     place over the logits.
+//     workgroup: rows of up to 32768 columns are held in the workgroup's
+//     registers (read from HBM once: max, exp and sum, then dlogits written in
+//     place over the logits); wider rows take an online max/sum pass and a
+//     second pass for dlogits.
 //   RMSNorm backward (norm.rs:36-38 through mul, mean_axis, add_scalar, powf):
 //     one wave per row with the row in registers; the weight gradient is summed
 //     per workgroup into a partial row, then over workgroups in a fixed order.
@@ -104,6 +106,84 @@ __global__ __launch_bounds__(256) void ce_fwd_bwd_kernel(float *__restrict__ log
     for (int64_t k = v4 * 4 + threadIdx.x; k < v; k += 256) z[k] = grad(z[k], k);
 }
 
+// The same for rows that fit the workgroup's registers (v <= 4096 * NV, v a
+// multiple of 4, 16-byte aligned rows): the row is read from HBM once and
+// written once. NT threads, thread l of the workgroup holding float4s l,
+// l + NT, ...: the row's max, then e = exp(z - max) kept in place of z and
+// their sum, then dlogits = e / sum * scale from the registers.
+template <int NT>
+__device__ __forceinline__ float block_max(float v, float *red) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) red[wave] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) m = fmaxf(m, red[i]);
+    return m;
+}
+
+template <int NT, int NV>
+__global__ __launch_bounds__(NT) void ce_fwd_bwd_regs_kernel(float *__restrict__ logits,
+                                                                const int32_t *__restrict__ targets,
+                                                                int64_t v, float scale,
+                                                                float *__restrict__ row_loss) {
+    __shared__ float red_m[NT / 64], red_s[NT / 64];
+    const int64_t row = blockIdx.x;
+    float4 *z4 = reinterpret_cast<float4 *>(logits + row * v);
+    const int v4 = (int)(v >> 2), tid = threadIdx.x;
+    const int64_t t = targets[row];
+    const float zt = tid == 0 ? logits[row * v + t] : 0.0f;
+    float4 e[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = tid + NT * i;
+        e[i] = q < v4 ? z4[q] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) m = fmaxf(m, fmaxf(fmaxf(e[i].x, e[i].y), fmaxf(e[i].z, e[i].w)));
+    const float M = block_max<NT>(m, red_m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        // positions past the row hold -inf: exp gives 0
+        e[i].x = expf(__fsub_rn(e[i].x, M));
+        e[i].y = expf(__fsub_rn(e[i].y, M));
+        e[i].z = expf(__fsub_rn(e[i].z, M));
+        e[i].w = expf(__fsub_rn(e[i].w, M));
+        sum = __fadd_rn(sum, __fadd_rn(__fadd_rn(e[i].x, e[i].y), __fadd_rn(e[i].z, e[i].w)));
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) sum = __fadd_rn(sum, __shfl_xor(sum, off, 64));
+    if ((tid & 63) == 0) red_s[tid >> 6] = sum;
+    __syncthreads();
+    float S = red_s[0];
+#pragma unroll
+    for (int i = 1; i < NT / 64; ++i) S = __fadd_rn(S, red_s[i]);
+    if (tid == 0) row_loss[row] = __fsub_rn(__fadd_rn(M, logf(S)), zt);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int q = tid + NT * i;
+        if (q >= v4) continue;
+        float4 d;
+        d.x = __fmul_rn(__fdiv_rn(e[i].x, S), scale);
+        d.y = __fmul_rn(__fdiv_rn(e[i].y, S), scale);
+        d.z = __fmul_rn(__fdiv_rn(e[i].z, S), scale);
+        d.w = __fmul_rn(__fdiv_rn(e[i].w, S), scale);
+        const int64_t j = 4 * (int64_t)q;
+        if (t >= j && t < j + 4) {
+            const int c = (int)(t - j);
+            if (c == 0) d.x = __fsub_rn(d.x, scale);
+            if (c == 1) d.y = __fsub_rn(d.y, scale);
+            if (c == 2) d.z = __fsub_rn(d.z, scale);
+            if (c == 3) d.w = __fsub_rn(d.w, scale);
+        }
+        z4[q] = d;
+    }
+}
+
 __global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__ row_loss,
                                                        int64_t n, float *__restrict__ out) {
     __shared__ double part[256];
@@ -126,7 +206,9 @@ __global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__
 // Workgroup = 4 waves x RPW rows; each lane keeps the column partials of the
 // float4 columns it owns (lane + 64 i), the 4 waves' partials are summed in
 // LDS in wave order and written as one partial row per workgroup.
-constexpr int RMS_RPW = 2;  // rows per wave
+// rows per wave: 1 (1024 workgroups at 4096 rows; measured against 2 and 4
+// rows per wave, and against the dx read issued with x and dy)
+constexpr int RMS_RPW = 1;
 
 template <int NV>
 __global__ __launch_bounds__(256) void rms_bwd_rows_kernel(const float *__restrict__ x,
@@ -147,6 +229,7 @@ __global__ __launch_bounds__(256) void rms_bwd_rows_kernel(const float *__restri
         if (row >= rows) break;
         const float4 *x4 = reinterpret_cast<const float4 *>(x + row * d);
         const float4 *g4 = reinterpret_cast<const float4 *>(dy + row * d);
+        float4 *o4 = reinterpret_cast<float4 *>(dx + row * d);
         float4 xv[NV], gv[NV];
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
@@ -179,7 +262,6 @@ __global__ __launch_bounds__(256) void rms_bwd_rows_kernel(const float *__restri
         const float inv = __fdiv_rn(1.0f, __fsqrt_rn(a));
         const float a32 = __fmul_rn(__fmul_rn(inv, inv), inv);  // a^-3/2
         const float ds = __fmul_rn(__fmul_rn(dinv, __fmul_rn(-0.5f, a32)), inv_len);
-        float4 *o4 = reinterpret_cast<float4 *>(dx + row * d);
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int j = lane + 64 * i;
@@ -285,30 +367,38 @@ __global__ __launch_bounds__(256) void rms_dw_cols_kernel(const float *__restric
     partial[(int64_t)blockIdx.y * d + j] = acc;
 }
 
-// out[j] = sum over the partial rows: workgroup = 64 columns x 4 waves; wave w
-// sums rows w, w+4, w+8, ... (four independent loads in flight), then the four
-// wave sums are added in wave order. Fixed order for a given nrows.
-__global__ __launch_bounds__(256) void sum_rows_kernel(const float *__restrict__ partial,
-                                                       int64_t nrows, int64_t d,
-                                                       float *__restrict__ out) {
+// out[j] = sum over the partial rows: workgroup = 64 columns x 16 waves; wave
+// w sums rows w, w+16, w+32, ... in order (eight loads in flight), then the
+// 16 wave sums are added in wave order. Fixed order for a given nrows.
+constexpr int SUM_WAVES = 16;
+
+__global__ __launch_bounds__(64 * SUM_WAVES) void sum_rows_kernel(const float *__restrict__ partial,
+                                                                 int64_t nrows, int64_t d,
+                                                                 float *__restrict__ out) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t j = (int64_t)blockIdx.x * 64 + lane;
     float acc = 0.0f;
     if (j < d) {
+        constexpr int S = SUM_WAVES;
         int64_t r = wave;
-        for (; r + 12 < nrows; r += 16) {
-            const float a0 = partial[r * d + j], a1 = partial[(r + 4) * d + j];
-            const float a2 = partial[(r + 8) * d + j], a3 = partial[(r + 12) * d + j];
-            acc = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(acc, a0), a1), a2), a3);
+        for (; r + 7 * S < nrows; r += 8 * S) {
+            float a[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = partial[(r + u * S) * d + j];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc = __fadd_rn(acc, a[u]);
         }
-        for (; r < nrows; r += 4) acc = __fadd_rn(acc, partial[r * d + j]);
+        for (; r < nrows; r += S) acc = __fadd_rn(acc, partial[r * d + j]);
     }
-    __shared__ float part[4][64];
+    __shared__ float part[SUM_WAVES][64];
     part[wave][lane] = acc;
     __syncthreads();
-    if (wave == 0 && j < d)
-        out[j] = __fadd_rn(__fadd_rn(__fadd_rn(part[0][lane], part[1][lane]), part[2][lane]),
-                           part[3][lane]);
+    if (wave == 0 && j < d) {
+        float s = part[0][lane];
+#pragma unroll
+        for (int w = 1; w < SUM_WAVES; ++w) s = __fadd_rn(s, part[w][lane]);
+        out[j] = s;
+    }
 }
 
 // ---- embedding backward ----------------------------------------------------------
@@ -551,8 +641,24 @@ void launch_cross_entropy_fwd_bwd(Context &ctx, float *logits, const int32_t *ta
                                   float *loss_dev) {
     if (n > 0x7fffffff) fail(MMH_ERR_SHAPE, "cross_entropy: too many rows");
     const int vec = (v % 4 == 0) && al16(logits);
-    hipLaunchKernelGGL(ce_fwd_bwd_kernel, dim3((unsigned)n), dim3(256), 0, ctx.stream, logits,
-                       targets_dev, v, g / (float)n, row_loss, vec);
+    const float scale = g / (float)n;
+    const dim3 grid((unsigned)n);
+    // rows held in registers (read once) up to 32768 columns
+    if (vec && v <= 32768) {
+        // (the widest rows on 512 threads: 2 workgroups of 106 VGPRs share
+        // a CU, where one 1024-thread workgroup would hold it alone)
+        if (v <= 4096)
+            hipLaunchKernelGGL((ce_fwd_bwd_regs_kernel<1024, 1>), grid, dim3(1024), 0, ctx.stream, logits, targets_dev, v, scale, row_loss);
+        else if (v <= 8192)
+            hipLaunchKernelGGL((ce_fwd_bwd_regs_kernel<1024, 2>), grid, dim3(1024), 0, ctx.stream, logits, targets_dev, v, scale, row_loss);
+        else if (v <= 16384)
+            hipLaunchKernelGGL((ce_fwd_bwd_regs_kernel<1024, 4>), grid, dim3(1024), 0, ctx.stream, logits, targets_dev, v, scale, row_loss);
+        else
+            hipLaunchKernelGGL((ce_fwd_bwd_regs_kernel<512, 16>), grid, dim3(512), 0, ctx.stream, logits, targets_dev, v, scale, row_loss);
+    } else {
+        hipLaunchKernelGGL(ce_fwd_bwd_kernel, grid, dim3(256), 0, ctx.stream, logits,
+                           targets_dev, v, scale, row_loss, vec);
+    }
     check_hip(hipGetLastError(), "cross_entropy backward launch");
     hipLaunchKernelGGL(mean_f64_kernel, dim3(1), dim3(256), 0, ctx.stream, row_loss, n,
                        loss_dev);
@@ -573,6 +679,9 @@ void launch_rms_norm_backward(Context &ctx, const float *x, const float *w, cons
     const int vec = (d % 4 == 0) && d <= 4096 && al16(x) && al16(w) && al16(dy) && al16(dx) &&
                     al16(scratch);
     if (vec) {
+        // one row per wave: 8 waves per workgroup (4 at d above 2048, whose
+        // rows hold twice the registers), the rows' weight-gradient terms in
+        // LDS ([waves][d] floats)
         const int64_t blocks = (rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW);
         if (blocks > 0x7fffffff) fail(MMH_ERR_SHAPE, "rms_norm backward: too many rows");
         const dim3 grid((unsigned)blocks), block(256);
@@ -588,8 +697,8 @@ void launch_rms_norm_backward(Context &ctx, const float *x, const float *w, cons
         else
             hipLaunchKernelGGL(rms_bwd_rows_kernel<16>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
         check_hip(hipGetLastError(), "rms_norm backward launch");
-        hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(256), 0, ctx.stream,
-                           scratch, blocks, d, dw);
+        hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(64 * SUM_WAVES), 0,
+                           ctx.stream, scratch, blocks, d, dw);
         check_hip(hipGetLastError(), "rms_norm dw launch");
         return;
     }
@@ -601,8 +710,8 @@ void launch_rms_norm_backward(Context &ctx, const float *x, const float *w, cons
     hipLaunchKernelGGL(rms_dw_cols_kernel, dim3(grid_for(d), (unsigned)chunks), dim3(256), 0,
                        ctx.stream, x, dy, inv, rows, d, (int64_t)64, scratch);
     check_hip(hipGetLastError(), "rms_norm dw launch");
-    hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(256), 0, ctx.stream, scratch,
-                       chunks, d, dw);
+    hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(64 * SUM_WAVES), 0, ctx.stream,
+                       scratch, chunks, d, dw);
     check_hip(hipGetLastError(), "rms_norm dw launch");
 }
 
