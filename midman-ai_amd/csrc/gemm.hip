@@ -1221,12 +1221,47 @@ __global__ __launch_bounds__(512) void mfma_peak_kernel(float *out, int n, uint3
     out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// Sums split partials in split order, then applies the epilogue.
-template <int EPI>
+// Sums split partials in split order, then applies the epilogue. VEC: four
+// consecutive columns per thread (n, ldc multiples of 4, 16-byte aligned C,
+// residual and partials), all splits' loads issued before the adds.
+template <int EPI, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial,
                                                      float *c, const float *resid, int64_t m,
                                                      int64_t n, int64_t ldc, int splits) {
     const int64_t total = m * n;
+    if (VEC) {
+        for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; 4 * q < total;
+             q += (int64_t)gridDim.x * blockDim.x) {
+            const int64_t idx = 4 * q;
+            float4 acc = *reinterpret_cast<const float4 *>(partial + idx);
+            for (int s0 = 1; s0 < splits; s0 += 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (s0 + u < splits)
+                        v[u] = *reinterpret_cast<const float4 *>(partial + (int64_t)(s0 + u) * total + idx);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (s0 + u < splits) {
+                        acc.x = __fadd_rn(acc.x, v[u].x);
+                        acc.y = __fadd_rn(acc.y, v[u].y);
+                        acc.z = __fadd_rn(acc.z, v[u].z);
+                        acc.w = __fadd_rn(acc.w, v[u].w);
+                    }
+            }
+            const int64_t row = idx / n, col = idx - row * n;
+            float4 *dst = reinterpret_cast<float4 *>(c + row * ldc + col);
+            if (EPI == EPI_ACCUM) {
+                const float4 r = *reinterpret_cast<const float4 *>((resid ? resid : c) + row * ldc + col);
+                acc.x = __fadd_rn(r.x, acc.x);
+                acc.y = __fadd_rn(r.y, acc.y);
+                acc.z = __fadd_rn(r.z, acc.z);
+                acc.w = __fadd_rn(r.w, acc.w);
+            }
+            *dst = acc;
+        }
+        return;
+    }
     for (int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; idx < total;
          idx += (int64_t)gridDim.x * blockDim.x) {
         float acc = partial[idx];
@@ -1242,8 +1277,14 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ p
 
 // The tail tiles of a balanced 128x128 launch: each element sums its tile's
 // tail_s pieces in piece order, then takes the epilogue (store, accumulate, or
-// the SwiGLU backward into the (dg, du) pairs). One workgroup per tile.
-template <int EPI>
+// the SwiGLU backward into the (dg, du) pairs). TAIL_PARTS workgroups per
+// tile (grid y), each thread four consecutive columns at a time with every
+// piece's load issued before the adds. VEC: 16-byte aligned C (and residual /
+// gate-up pairs) with ldc (ldaux) a multiple of 4, so interior columns move as
+// float4; otherwise, and past the matrix's last column, one at a time.
+constexpr int TAIL_PARTS = 8;
+
+template <int EPI, bool VEC>
 __global__ __launch_bounds__(256) void tail_reduce(KParams p) {
     const int t = p.tail_first + (int)blockIdx.x;
     int tm, tn;
@@ -1251,21 +1292,63 @@ __global__ __launch_bounds__(256) void tail_reduce(KParams p) {
     const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
     const float *part = p.partial + (int64_t)blockIdx.x * p.tail_s * (BM * BN);
     const float *R = p.resid ? p.resid : p.c;
-    for (int e = threadIdx.x; e < BM * BN; e += 256) {
+    constexpr int PER = BM * BN / TAIL_PARTS;
+    for (int e = (int)blockIdx.y * PER + 4 * (int)threadIdx.x; e < ((int)blockIdx.y + 1) * PER;
+         e += 4 * 256) {
         const int64_t row = m0 + e / BN, col = n0 + e % BN;
         if (row >= p.m || col >= p.n) continue;
-        float v = part[e];
-        for (int i = 1; i < p.tail_s; ++i) v = __fadd_rn(v, part[(int64_t)i * (BM * BN) + e]);
-        if (EPI == EPI_SWIGLU_BWD) {
-            const float *gu = p.aux + row * p.ldaux + 2 * col;
-            const float2 o = swiglu_bwd_f(v, gu[0], gu[1]);
-            float *dst = p.c + row * p.ldc + 2 * col;
-            dst[0] = o.x;
-            dst[1] = o.y;
-        } else if (EPI == EPI_ACCUM) {
-            p.c[row * p.ldc + col] = __fadd_rn(R[row * p.ldc + col], v);
-        } else {
-            p.c[row * p.ldc + col] = v;
+        float4 v = *reinterpret_cast<const float4 *>(part + e);
+        for (int i0 = 1; i0 < p.tail_s; i0 += 4) {
+            float4 w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u < p.tail_s)
+                    w[u] = *reinterpret_cast<const float4 *>(part + (int64_t)(i0 + u) * (BM * BN) + e);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (i0 + u < p.tail_s) {
+                    v.x = __fadd_rn(v.x, w[u].x);
+                    v.y = __fadd_rn(v.y, w[u].y);
+                    v.z = __fadd_rn(v.z, w[u].z);
+                    v.w = __fadd_rn(v.w, w[u].w);
+                }
+        }
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        if (VEC && col + 3 < p.n) {
+            if (EPI == EPI_SWIGLU_BWD) {
+                const float *gu = p.aux + row * p.ldaux + 2 * col;
+                const float4 a = *reinterpret_cast<const float4 *>(gu);
+                const float4 b = *reinterpret_cast<const float4 *>(gu + 4);
+                const float2 o0 = swiglu_bwd_f(vv[0], a.x, a.y), o1 = swiglu_bwd_f(vv[1], a.z, a.w);
+                const float2 o2 = swiglu_bwd_f(vv[2], b.x, b.y), o3 = swiglu_bwd_f(vv[3], b.z, b.w);
+                float4 *dst = reinterpret_cast<float4 *>(p.c + row * p.ldc + 2 * col);
+                dst[0] = make_float4(o0.x, o0.y, o1.x, o1.y);
+                dst[1] = make_float4(o2.x, o2.y, o3.x, o3.y);
+            } else if (EPI == EPI_ACCUM) {
+                const float4 r = *reinterpret_cast<const float4 *>(R + row * p.ldc + col);
+                *reinterpret_cast<float4 *>(p.c + row * p.ldc + col) =
+                    make_float4(__fadd_rn(r.x, vv[0]), __fadd_rn(r.y, vv[1]),
+                                __fadd_rn(r.z, vv[2]), __fadd_rn(r.w, vv[3]));
+            } else {
+                *reinterpret_cast<float4 *>(p.c + row * p.ldc + col) = v;
+            }
+            continue;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t cu = col + u;
+            if (cu >= p.n) break;
+            if (EPI == EPI_SWIGLU_BWD) {
+                const float *gu = p.aux + row * p.ldaux + 2 * cu;
+                const float2 o = swiglu_bwd_f(vv[u], gu[0], gu[1]);
+                float *dst = p.c + row * p.ldc + 2 * cu;
+                dst[0] = o.x;
+                dst[1] = o.y;
+            } else if (EPI == EPI_ACCUM) {
+                p.c[row * p.ldc + cu] = __fadd_rn(R[row * p.ldc + cu], vv[u]);
+            } else {
+                p.c[row * p.ldc + cu] = vv[u];
+            }
         }
     }
 }
@@ -1591,23 +1674,39 @@ void gemm(Context &ctx, const GemmDesc &d) {
     check_hip(hipGetLastError(), "gemm launch");
     if (splits > 1) {
         const int64_t total = d.m * d.n;
-        const unsigned blocks = (unsigned)std::min<int64_t>((total + 255) / 256, 8192);
-        if (d.epi == EPI_ACCUM)
-            hipLaunchKernelGGL(splitk_reduce<EPI_ACCUM>, dim3(blocks), dim3(256), 0, ctx.stream,
-                               p.partial, d.c, d.resid, d.m, d.n, d.ldc, splits);
-        else
-            hipLaunchKernelGGL(splitk_reduce<EPI_STORE>, dim3(blocks), dim3(256), 0, ctx.stream,
-                               p.partial, d.c, nullptr, d.m, d.n, d.ldc, splits);
+        const bool vec = d.n % 4 == 0 && d.ldc % 4 == 0 && aligned16(d.c) &&
+                         aligned16(p.partial) && (!d.resid || aligned16(d.resid));
+        const int64_t items = vec ? total / 4 : total;
+        const unsigned blocks = (unsigned)std::min<int64_t>((items + 255) / 256, 8192);
+#define MMH_SPLITK(E, V)                                                                   \
+    hipLaunchKernelGGL((splitk_reduce<E, V>), dim3(blocks), dim3(256), 0, ctx.stream, p.partial, \
+                       d.c, E == EPI_ACCUM ? d.resid : nullptr, d.m, d.n, d.ldc, splits)
+        if (d.epi == EPI_ACCUM) {
+            if (vec) MMH_SPLITK(EPI_ACCUM, true); else MMH_SPLITK(EPI_ACCUM, false);
+        } else {
+            if (vec) MMH_SPLITK(EPI_STORE, true); else MMH_SPLITK(EPI_STORE, false);
+        }
+#undef MMH_SPLITK
         check_hip(hipGetLastError(), "split-k reduce launch");
     }
     if (p.tail_s > 1) {
-        const dim3 rg((unsigned)(tiles - p.tail_first));
+        const dim3 rg((unsigned)(tiles - p.tail_first), TAIL_PARTS);
+        const bool vec = d.ldc % 4 == 0 && aligned16(d.c) && (!d.resid || aligned16(d.resid)) &&
+                         (epi != EPI_SWIGLU_BWD || (d.ldaux % 4 == 0 && aligned16(d.aux)));
+#define MMH_TAIL(E)                                                                        \
+    do {                                                                                   \
+        if (vec)                                                                           \
+            hipLaunchKernelGGL((tail_reduce<E, true>), rg, dim3(256), 0, ctx.stream, p);   \
+        else                                                                               \
+            hipLaunchKernelGGL((tail_reduce<E, false>), rg, dim3(256), 0, ctx.stream, p);  \
+    } while (0)
         if (epi == EPI_SWIGLU_BWD)
-            hipLaunchKernelGGL(tail_reduce<EPI_SWIGLU_BWD>, rg, dim3(256), 0, ctx.stream, p);
+            MMH_TAIL(EPI_SWIGLU_BWD);
         else if (epi == EPI_ACCUM)
-            hipLaunchKernelGGL(tail_reduce<EPI_ACCUM>, rg, dim3(256), 0, ctx.stream, p);
+            MMH_TAIL(EPI_ACCUM);
         else
-            hipLaunchKernelGGL(tail_reduce<EPI_STORE>, rg, dim3(256), 0, ctx.stream, p);
+            MMH_TAIL(EPI_STORE);
+#undef MMH_TAIL
         check_hip(hipGetLastError(), "tail reduce launch");
     }
     if (rope && !p.rope_cos)
