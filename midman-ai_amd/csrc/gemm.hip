@@ -34,9 +34,11 @@
 // tiles, and tiles are walked in groups of 8 tile-rows so that the tiles an
 // XCD holds at once share A rows and B columns in its L2.
 //
-// Small-tile-count shapes (e.g. M=2048, N=256) are split along K; each split
-// writes a partial tile and a second kernel sums the partials in split order,
-// so the result is deterministic.
+// Small-tile-count shapes (e.g. M=2048, N=256) are split along K; the
+// partials are summed in split order, so the result is deterministic: on the
+// 64x64 and 32x32 tiles by the last split of each tile (the splits store
+// their partial through to memory and count themselves in a per-tile
+// counter), on the 128x128 tiles by a second kernel.
 #include "mmh_internal.h"
 
 #include <utility>
@@ -89,6 +91,12 @@ struct KParams {
     // [BM][BN] blocks, piece-major); tail_reduce sums them in piece order.
     int tail_first, tail_s;
     int64_t tail_k;
+    // Split K on the 64x64 and 32x32 tiles (tickets set): every split stores
+    // its partial tile through to memory and counts itself in tickets[tile];
+    // the last split of a tile sums the tile's partials in split order and
+    // applies the epilogue (split_accum: C = resid (or C) + sum, else C = sum).
+    int32_t *tickets;
+    int split_accum;
     // The value the sums of products start from: +0 (a product, as the
     // reference's fresh zeroed C), or -0 when the sum is added into C (the
     // seam's accumulate: C's own value starts the reference's sum, so a -0 in
@@ -367,6 +375,105 @@ __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__r
 }
 
 // Tile t of the grouped order: GROUP_M tile rows at a time, column by column.
+// Split partials for the in-kernel reduction: stored through to memory and
+// read past the XCD-local L2 (device-scope relaxed atomics: sc1 stores and
+// loads), so the last split of a tile, on any XCD, reads every split's values.
+__device__ __forceinline__ void split_put(float *dst, float v) {
+    __hip_atomic_store(dst, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float split_get(const float *src) {
+    return __hip_atomic_load(const_cast<float *>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// After a workgroup's split_put stores: true in the workgroup that completes
+// the tile (the last of its p.splits splits to get here), which also resets
+// the tile's counter for the next launch. Every thread of the workgroup calls it.
+__device__ __forceinline__ bool split_last(const KParams &p, int tile) {
+    __shared__ int s_last;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int old = __hip_atomic_fetch_add(p.tickets + tile, 1, __ATOMIC_RELAXED,
+                                               __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old == p.splits - 1;
+        if (s_last) __hip_atomic_store(p.tickets + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    return s_last;
+}
+// The last split of a tile: rows [m0, m0 + tr) x columns [n0, n0 + tc) of C
+// (tc a multiple of 4) as the splits' partials added in split order (the
+// caller's own included, read back like the others), then the epilogue
+// (split_accum: C = resid (or C) + sum). The nthreads threads walk the tile
+// row-major, four columns at a time, with four splits' loads in flight;
+// partial rows of N % 4 == 0 move as float4, others one value at a time.
+__device__ __forceinline__ void split_reduce_tile(const KParams &p, int64_t m0, int64_t n0, int tr,
+                                               int tc, int nthreads) {
+    const int64_t M = p.m, N = p.n, total = M * N;
+    const bool vecp = N % 4 == 0;
+    const bool vecc = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0 &&
+                      (!p.resid || (reinterpret_cast<uintptr_t>(p.resid) & 15) == 0);
+    const float *R = p.resid ? p.resid : p.c;
+    for (int e = 4 * (int)threadIdx.x; e < tr * tc; e += 4 * nthreads) {
+        const int64_t row = m0 + e / tc, col = n0 + e % tc;
+        if (row >= M || col >= N) continue;
+        const float *Q = p.partial + row * N + col;
+        if (vecp && col + 3 < N) {
+            float4 acc;
+            for (int s0 = 0; s0 < p.splits; s0 += 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (s0 + u < p.splits) {
+                        const float *src = Q + (int64_t)(s0 + u) * total;
+                        v[u].x = split_get(src);
+                        v[u].y = split_get(src + 1);
+                        v[u].z = split_get(src + 2);
+                        v[u].w = split_get(src + 3);
+                    }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (s0 + u < p.splits) {
+                        if (s0 + u == 0) {
+                            acc = v[u];
+                        } else {
+                            acc.x = __fadd_rn(acc.x, v[u].x);
+                            acc.y = __fadd_rn(acc.y, v[u].y);
+                            acc.z = __fadd_rn(acc.z, v[u].z);
+                            acc.w = __fadd_rn(acc.w, v[u].w);
+                        }
+                    }
+            }
+            float *dst = p.c + row * p.ldc + col;
+            if (p.split_accum) {
+                const float *r = R + row * p.ldc + col;
+                if (vecc) {
+                    const float4 o = *reinterpret_cast<const float4 *>(r);
+                    acc = make_float4(__fadd_rn(o.x, acc.x), __fadd_rn(o.y, acc.y),
+                                      __fadd_rn(o.z, acc.z), __fadd_rn(o.w, acc.w));
+                } else {
+                    acc = make_float4(__fadd_rn(r[0], acc.x), __fadd_rn(r[1], acc.y),
+                                      __fadd_rn(r[2], acc.z), __fadd_rn(r[3], acc.w));
+                }
+            }
+            if (vecc) {
+                *reinterpret_cast<float4 *>(dst) = acc;
+            } else {
+                dst[0] = acc.x;
+                dst[1] = acc.y;
+                dst[2] = acc.z;
+                dst[3] = acc.w;
+            }
+            continue;
+        }
+        for (int u = 0; u < 4 && col + u < N; ++u) {
+            float v = split_get(Q + u);
+            for (int s = 1; s < p.splits; ++s) v = __fadd_rn(v, split_get(Q + (int64_t)s * total + u));
+            float *dst = p.c + row * p.ldc + col + u;
+            *dst = p.split_accum ? __fadd_rn(R[row * p.ldc + col + u], v) : v;
+        }
+    }
+}
+
 __device__ __forceinline__ void grouped_tile(const KParams &p, int t, int &tm, int &tn) {
     const int per_group = GROUP_M * p.tiles_n;
     const int group = t / per_group;
@@ -474,6 +581,8 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
         return;
     }
     if (p.splits > 1) {
+        // (summed by splitk_reduce: a tile's 2-16 partials are too much for
+        // one workgroup of the launch to add up at the end)
         float *P = p.partial + (int64_t)split * M * N;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -935,8 +1044,9 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t row = row_of(r);
-            if (row < M && col < N) P[row * N + col] = acc[r];
+            if (row < M && col < N) split_put(P + row * N + col, acc[r]);
         }
+        if (split_last(p, tm * p.tiles_n + tn)) split_reduce_tile(p, m0, n0, SBM, SBN, 256);
         return;
     }
     float *C = p.c + batch * p.stride_c;
@@ -986,8 +1096,8 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
 // per-lane test of mode 1.) Operands stored k-major (A when TA, B when !TB)
 // are read one value per k, coalesced across the 32 lanes of a half.
 // Split K (grid z > 1): each split covers k_per_split values and writes its
-// partial tile; splitk_reduce sums the splits in order and applies the
-// epilogue.
+// partial tile; the last split of the tile sums the splits in order and
+// applies the epilogue.
 template <bool TA, bool TB, int EPI, bool NORM, int NW, int MODE>
 __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
     __shared__ float part[NW][16][64];
@@ -1123,7 +1233,7 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
         const int64_t row = m0 + rl;
         if (NORM) v = __fmul_rn(v, sm_inv[rl]);
         if (!fin) {
-            if (row < M && col < N) p.partial[((int64_t)split * M + row) * N + col] = v;
+            if (row < M && col < N) split_put(p.partial + ((int64_t)split * M + row) * N + col, v);
         } else if (EPI == EPI_ACCUM) {
             if (row < M && col < N) C[row * p.ldc + col] = __fadd_rn(pre_r[i], v);
         } else if (EPI == EPI_STORE && p.rope_cos) {
@@ -1140,6 +1250,8 @@ __global__ __launch_bounds__(64 * NW) void gemm_f32_mfma_ksplit(KParams p) {
             block32_epilogue<EPI>(p, C, R, row, col, lr, v);
         }
     }
+    if (fin) return;
+    if (split_last(p, tm * p.tiles_n + tn)) split_reduce_tile(p, m0, n0, 32, 32, 64 * NW);
 }
 
 template <bool TA, bool TB, int EPI, bool NORM, int MODE>
@@ -1221,9 +1333,9 @@ __global__ __launch_bounds__(512) void mfma_peak_kernel(float *out, int n, uint3
     out[(int64_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
 }
 
-// Sums split partials in split order, then applies the epilogue. VEC: four
-// consecutive columns per thread (n, ldc multiples of 4, 16-byte aligned C,
-// residual and partials), all splits' loads issued before the adds.
+// Sums the 128x128 kernel's split partials in split order, then applies the
+// epilogue. VEC: four consecutive columns per thread (n, ldc multiples of 4,
+// 16-byte aligned C, residual and partials), four splits' loads in flight.
 template <int EPI, bool VEC>
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial,
                                                      float *c, const float *resid, int64_t m,
@@ -1564,6 +1676,16 @@ void gemm(Context &ctx, const GemmDesc &d) {
     splits = (int)((ktiles + kt_per - 1) / kt_per);
     p.splits = splits;
     if (splits > 1) {
+        // 64x64 and 32x32 tiles: the last split of each tile sums the
+        // partials in split order and applies the epilogue (one launch;
+        // every such grid has fewer tiles than two per CU, far below the
+        // counters); 128x128 tiles: splitk_reduce after the launch
+        if (small || ksplit) {
+            p.tickets = d.scratch ? d.scratch_tickets : ctx.tickets;
+            if (!p.tickets || tiles > Context::kTickets)
+                fail(MMH_ERR_OTHER, "gemm: no split counters for " + std::to_string(tiles) + " tiles");
+            p.split_accum = d.epi == EPI_ACCUM ? 1 : 0;
+        }
         const size_t need_bytes = (size_t)splits * d.m * d.n * 4;
         if (d.scratch) {
             if (need_bytes > d.scratch_bytes)
@@ -1672,7 +1794,7 @@ void gemm(Context &ctx, const GemmDesc &d) {
         dispatch_t<EPI_STORE>(ctx, d.ta, d.tb, p, grid, small);
     }
     check_hip(hipGetLastError(), "gemm launch");
-    if (splits > 1) {
+    if (splits > 1 && !p.tickets) {
         const int64_t total = d.m * d.n;
         const bool vec = d.n % 4 == 0 && d.ldc % 4 == 0 && aligned16(d.c) &&
                          aligned16(p.partial) && (!d.resid || aligned16(d.resid));

@@ -67,6 +67,11 @@ struct Context {
     std::string name;
     void *ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};
+    // One counter per output tile of a K-split GEMM (zero between launches:
+    // the last split of a tile resets its counter), allocated and zeroed
+    // with the context.
+    static constexpr int kTickets = 4096;
+    int32_t *tickets = nullptr;
     // Allocations made through mmh_alloc, freed at destroy.
     std::vector<void *> owned;
 
@@ -137,6 +142,9 @@ struct GemmDesc {
     // partials of the split it chooses need more than scratch_bytes.
     float *scratch = nullptr;
     size_t scratch_bytes = 0;
+    // With scratch: kTickets zeroed tile counters for the in-kernel split
+    // reduction (null: the context's own).
+    int32_t *scratch_tickets = nullptr;
     // EPI_ACCUM with the GEMM seam's rule (kernels.rs:48, C += A.B): C's own
     // value starts the sum. Without it EPI_ACCUM is a residual add of a fresh
     // product (block.rs:79-80: x + matmul(..), the product summed from +0).

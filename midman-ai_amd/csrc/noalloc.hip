@@ -2,17 +2,21 @@
 // allocate device memory (code under HIP graph capture, tight serving loops,
 // harnesses that forbid hipMalloc). The only device memory the GEMM needs
 // beyond its operands is the split-K partials ([splits, m, n] f32, written in
-// full by the splits and summed in split order by splitk_reduce); here they
-// live in a file-scope device array of fixed size instead of the context's
-// growable workspace, so no call allocates or frees anything.
+// full by the splits and summed in split order by the last split of each
+// tile) with one counter per tile, and the tail pieces of the 128x128 kernel
+// (summed by tail_reduce); here they live in file-scope device arrays of
+// fixed size instead of the context's growable workspace and counters, so no
+// call allocates or frees anything.
 //
-// The array exists once per GPU (each device that loads this code object
-// holds its own copy until the process ends). Its device address is looked up
-// with hipGetSymbolAddress once per device, with that device current, and
-// only that address is ever handed to kernels. Every call on one GPU shares
-// the array: calls that overlap on one GPU (two streams, two contexts, two
-// threads) race on it. Nothing in it needs clearing between calls: each
-// split writes every element of its partial tile before the reduce reads it.
+// The arrays exist once per GPU (each device that loads this code object
+// holds its own copy until the process ends). Their device addresses are
+// looked up with hipGetSymbolAddress once per device, with that device
+// current, and only those addresses are ever handed to kernels. Every call on
+// one GPU shares them: calls that overlap on one GPU (two streams, two
+// contexts, two threads) race on them. Nothing in them needs clearing between
+// calls: each split or piece writes every element of its partial tile before
+// it is summed, and the counters start at zero (the arrays are zero when the
+// code object loads) and are reset by the split that completes a tile.
 #include <mutex>
 
 #include "mmh_internal.h"
@@ -23,24 +27,34 @@ namespace {
 constexpr size_t kScratchBytes = size_t(16) << 20;  // 16 MiB per GPU: the benchmark sweep's largest partials
 
 static __device__ __align__(256) float scratch[kScratchBytes / 4];
+// The split-K tile counters (zero when the code object loads; the last split
+// of a tile resets its counter, so they are zero between calls).
+static __device__ __align__(256) int32_t scratch_tickets[Context::kTickets];
 
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 float *g_scratch_ptr[kMaxDevices] = {};
+int32_t *g_tickets_ptr[kMaxDevices] = {};
 
-// The device address of `scratch` on ctx's device (current: context() selects
-// it), looked up on the first call on that device.
-float *scratch_of(const Context &ctx) {
+// The device addresses of `scratch` and `scratch_tickets` on ctx's device
+// (current: context() selects it), looked up on the first call on that device.
+float *scratch_of(const Context &ctx, int32_t **tickets) {
     if (ctx.device < 0 || ctx.device >= kMaxDevices)
         fail(MMH_ERR_ARGUMENT, "gemm_noalloc: device index out of range");
     std::lock_guard<std::mutex> lock(g_scratch_mutex);
     float *&ptr = g_scratch_ptr[ctx.device];
-    if (!ptr) {
-        void *addr = nullptr;
+    int32_t *&tk = g_tickets_ptr[ctx.device];
+    if (!ptr || !tk) {
+        void *addr = nullptr, *taddr = nullptr;
         check_hip(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)), "gemm_noalloc scratch lookup");
-        if (!addr) fail(MMH_ERR_DEVICE, "gemm_noalloc: the scratch array has no device address");
+        check_hip(hipGetSymbolAddress(&taddr, HIP_SYMBOL(scratch_tickets)),
+                  "gemm_noalloc counter lookup");
+        if (!addr || !taddr)
+            fail(MMH_ERR_DEVICE, "gemm_noalloc: the scratch arrays have no device address");
         ptr = static_cast<float *>(addr);
+        tk = static_cast<int32_t *>(taddr);
     }
+    *tickets = tk;
     return ptr;
 }
 
@@ -76,7 +90,7 @@ int32_t mmh_gemm_noalloc(mmh_handle ctx, int32_t form, const float *a, const flo
         d.ldc = n;
         d.epi = accumulate ? EPI_ACCUM : EPI_STORE;
         d.accumulate_into_c = accumulate != 0;
-        d.scratch = scratch_of(cx);
+        d.scratch = scratch_of(cx, &d.scratch_tickets);
         d.scratch_bytes = kScratchBytes;
         gemm(cx, d);
         return MMH_OK;

@@ -108,6 +108,10 @@ int32_t mmh_context_create(int32_t device, mmh_handle *out_ctx) {
         check_hip(hipEventCreate(&c->t0), "event create");
         check_hip(hipEventCreate(&c->t1), "event create");
         c->xcd_teams = probe_xcd_teams(*c);
+        check_hip(hipMalloc(&c->tickets, Context::kTickets * sizeof(int32_t)), "ticket alloc");
+        check_hip(hipMemsetAsync(c->tickets, 0, Context::kTickets * sizeof(int32_t), c->stream),
+                  "ticket clear");
+        check_hip(hipStreamSynchronize(c->stream), "ticket clear sync");
         std::lock_guard<std::mutex> lock(g_mutex);
         g_contexts.push_back(std::move(c));
         *out_ctx = (mmh_handle)g_contexts.size();
@@ -130,6 +134,7 @@ int32_t mmh_context_destroy(mmh_handle ctx) {
         for (void *p : c->owned) (void)hipFree(p);
         for (int s = 0; s < Context::kSlots; ++s)
             if (c->ws[s]) (void)hipFree(c->ws[s]);
+        if (c->tickets) (void)hipFree(c->tickets);
         (void)hipEventDestroy(c->t0);
         (void)hipEventDestroy(c->t1);
         (void)hipStreamDestroy(c->stream);
