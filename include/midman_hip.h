@@ -252,9 +252,11 @@ int32_t mmh_model_check_guards(mmh_handle model, uint64_t *broken_words);
  * stage validates the ids on the host (MMH_ERR_INDEX for id >= V) and copies
  * them into the model's token buffers; run_staged queues forward + loss on
  * them and returns without waiting; read_loss waits and returns the loss of
- * the last staged run. run_staged runs the first call for a (batch, seq)
- * eagerly, captures the second into a HIP graph (kernel launches only) and
- * replays it afterwards; a new shape or re-allocated activations start over. */
+ * the last staged run. On the per-operation kernels run_staged runs the
+ * first call for a (batch, seq) eagerly, captures the second into a HIP graph
+ * (kernel launches only) and replays it afterwards; a new shape or
+ * re-allocated activations start over. The fused forward (one kernel, see
+ * mmh_model_set_forward_path) is launched directly on every call. */
 int32_t mmh_model_stage(mmh_handle model, const int32_t *inputs_host,
                         const int32_t *targets_host, int64_t batch, int64_t seq);
 int32_t mmh_model_run_staged(mmh_handle model, int64_t batch, int64_t seq);

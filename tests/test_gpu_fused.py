@@ -7,7 +7,7 @@ Every case runs the same model and tokens through the fused launch
 compares both with the oracle. Tolerances: fused vs oracle <= 1e-4 relative
 (the stated loss target); fused vs per-operation <= 2e-6 relative (two f32
 paths of the same arithmetic in different orders); repeated fused runs and
-graph replays bit-identical (fixed reduction orders, no atomics on data).
+staged runs bit-identical (fixed reduction orders, no atomics on data).
 """
 import numpy as np
 import pytest
@@ -91,12 +91,12 @@ def test_fused_shapes_against_oracle(ctx, cfg, batch, seq):
         m.close()
 
 
-def test_fused_graph_replays_and_reshapes(ctx):
-    # run_staged captures the fused launch into a graph; replays interleaved
+def test_fused_staged_runs_and_reshapes(ctx):
+    # run_staged launches the fused kernel directly on every call; runs interleaved
     # with eager fused runs, per-operation runs and a run at another shape
     # (the arena is laid out again) must keep returning the eager loss.
     cfg = mh.PRESETS["tiny"]
-    print("\n[fused graph] tiny B8 T256 / B3 T100", flush=True)
+    print("\n[fused staged] tiny B8 T256 / B3 T100", flush=True)
     m = mh.Model.new(ctx, cfg, 7)
     try:
         x, y = m.lab_tokens(8, 256)
@@ -155,7 +155,7 @@ def test_fused_failure_is_redone_on_the_per_op_kernels(ctx):
     # workgroup still runs to its end). The forward is then redone on the
     # per-operation kernels from the staged ids: the loss is the
     # per-operation loss bit for bit, the word and the counters are cleared,
-    # and the next fused launch (eager or a graph replay) is right again.
+    # and the next fused launch (mmh_model_loss or a staged run) is right again.
     cfg = mh.PRESETS["tiny"]
     print("\n[fused failure] tiny B8 T256 seed 0, error word preset", flush=True)
     m = mh.Model.new(ctx, cfg, 0)
@@ -177,7 +177,7 @@ def test_fused_failure_is_redone_on_the_per_op_kernels(ctx):
         assert float(m.loss(x, y, 8, 256)) == fused
         assert m.last_forward_fused()
 
-        # staged runs: eager, captured, then replays; the preset word reaches a replay
+        # staged runs (a direct launch each); the preset word reaches a staged run
         m.stage(x, y, 8, 256)
         for _ in range(3):
             m.run_staged(8, 256)
@@ -192,8 +192,8 @@ def test_fused_failure_is_redone_on_the_per_op_kernels(ctx):
             assert m.read_loss() == fused
             assert m.last_forward_fused()
 
-        # a failed replay whose loss is not read before new ids are staged is
-        # redone first; the replays after it are right
+        # a failed staged run whose loss is not read before new ids are staged
+        # is redone first; the runs after it are right
         m.inject_fused_error(16)
         m.run_staged(8, 256)
         m.stage(x, y, 8, 256)
