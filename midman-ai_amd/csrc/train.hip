@@ -203,115 +203,126 @@ __global__ __launch_bounds__(256) void mean_f64_kernel(const float *__restrict__
 //   dinv = sum_j (dy_j w_j) x_j, ds = dinv * (-0.5 * a^-3/2) * (1/d),
 //   share_j = ((dy_j w_j) inv + ds x_j) + ds x_j,  dx_j = [dx_j +] share_j,
 //   dw_j += dy_j (x_j inv).
-// Workgroup = 4 waves x RPW rows; each lane keeps the column partials of the
-// float4 columns it owns (lane + 64 i), the 4 waves' partials are summed in
-// LDS in wave order and written as one partial row per workgroup.
-// rows per wave: 1 (1024 workgroups at 4096 rows; measured against 2 and 4
-// rows per wave, and against the dx read issued with x and dy)
-constexpr int RMS_RPW = 1;
+// Workgroup = WPB waves, one row per wave. Each lane holds x, dy (and dx when
+// accumulating) of the float4 columns it owns (lane + 64 i) in registers: the
+// three row reads are issued together, at unconditional (clamped) addresses,
+// so a wave waits for memory once. w, shared by every row, is staged in LDS.
+// Each row's weight-gradient term dy (x inv) goes to LDS, and the WPB rows
+// are added per column in wave order into one partial row per workgroup.
+// float4 columns per lane at width d (d <= 4096)
+constexpr int rms_nv(int64_t d) { return d <= 256 ? 1 : d <= 512 ? 2 : d <= 1024 ? 4 : d <= 2048 ? 8 : 16; }
+// Waves (rows) per workgroup: 16 when that still leaves a workgroup for every
+// CU of the part (fewer partial rows to sum), else 4, else 1; the LDS row
+// terms ([WPB][64 NV] float4) stay within 128 KB (8 waves at NV 16).
+// Measured at 4096 x 2048: 16 waves 20.8 / 24.6 us (without / with the dx
+// accumulate read, partial sum included), 8 waves 20.7 / 25.0, 4 waves
+// 21.7 / 27.0.
+int rms_wpb(int64_t rows, int nv) {
+    const int top = nv == 16 ? 8 : 16;
+    return rows >= 256 * top ? top : rows >= 256 * 4 ? 4 : 1;
+}
 
-template <int NV>
-__global__ __launch_bounds__(256) void rms_bwd_rows_kernel(const float *__restrict__ x,
-                                                           const float *__restrict__ w,
-                                                           const float *__restrict__ dy,
-                                                           int64_t rows, int d, float eps,
-                                                           float *__restrict__ dx, int accumulate,
-                                                           float *__restrict__ partial) {
+template <int NV, int WPB>
+__global__ __launch_bounds__(64 * WPB) void rms_bwd_rows_kernel(const float *__restrict__ x,
+                                                                const float *__restrict__ w,
+                                                                const float *__restrict__ dy,
+                                                                int64_t rows, int d, float eps,
+                                                                float *__restrict__ dx,
+                                                                int accumulate,
+                                                                float *__restrict__ partial) {
+    __shared__ float4 ws[64 * NV];
+    __shared__ float4 part[WPB][64 * NV];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int d4 = d >> 2;
+    const int64_t row = (int64_t)blockIdx.x * WPB + wave;
+    const bool live = row < rows;
+    const int64_t r = live ? row : rows - 1;  // loads stay in bounds; a dead row adds nothing
+    const float4 *x4 = reinterpret_cast<const float4 *>(x + r * d);
+    const float4 *g4 = reinterpret_cast<const float4 *>(dy + r * d);
+    float4 *o4 = reinterpret_cast<float4 *>(dx + r * d);
+    float4 xv[NV], gv[NV], ov[NV];
+    if (accumulate) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int jc = min(lane + 64 * i, d4 - 1);
+            xv[i] = x4[jc];
+            gv[i] = g4[jc];
+            ov[i] = o4[jc];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int jc = min(lane + 64 * i, d4 - 1);
+            xv[i] = x4[jc];
+            gv[i] = g4[jc];
+            ov[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    // w after the row loads (the wait for it then covers them too)
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
-    float4 pw[NV];
+    for (int j = threadIdx.x; j < 64 * NV; j += 64 * WPB)
+        ws[j] = j < d4 ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int i = 0; i < NV; ++i) pw[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int i = 0; i < NV; ++i) {
+        const bool in = live && lane + 64 * i < d4;
+        xv[i] = in ? xv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        gv[i] = in ? gv[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    __syncthreads();  // ws
     const float inv_len = __fdiv_rn(1.0f, (float)d);
-    for (int rr = 0; rr < RMS_RPW; ++rr) {
-        const int64_t row = ((int64_t)blockIdx.x * 4 + wave) * RMS_RPW + rr;
-        if (row >= rows) break;
-        const float4 *x4 = reinterpret_cast<const float4 *>(x + row * d);
-        const float4 *g4 = reinterpret_cast<const float4 *>(dy + row * d);
-        float4 *o4 = reinterpret_cast<float4 *>(dx + row * d);
-        float4 xv[NV], gv[NV];
+    float ss = 0.0f, dinv = 0.0f;
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = lane + 64 * i;
-            xv[i] = j < d4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            gv[i] = j < d4 ? g4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        float ss = 0.0f, dinv = 0.0f;
+    for (int i = 0; i < NV; ++i) {
+        const float4 wv = ws[lane + 64 * i];
+        ss = __fadd_rn(ss, __fmul_rn(xv[i].x, xv[i].x));
+        ss = __fadd_rn(ss, __fmul_rn(xv[i].y, xv[i].y));
+        ss = __fadd_rn(ss, __fmul_rn(xv[i].z, xv[i].z));
+        ss = __fadd_rn(ss, __fmul_rn(xv[i].w, xv[i].w));
+        dinv = __fadd_rn(dinv, __fmul_rn(__fmul_rn(gv[i].x, wv.x), xv[i].x));
+        dinv = __fadd_rn(dinv, __fmul_rn(__fmul_rn(gv[i].y, wv.y), xv[i].y));
+        dinv = __fadd_rn(dinv, __fmul_rn(__fmul_rn(gv[i].z, wv.z), xv[i].z));
+        dinv = __fadd_rn(dinv, __fmul_rn(__fmul_rn(gv[i].w, wv.w), xv[i].w));
+    }
+    ss = wave_sum(ss);
+    dinv = wave_sum(dinv);
+    const float a = __fadd_rn(__fmul_rn(ss, inv_len), eps);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(a));
+    const float a32 = __fmul_rn(__fmul_rn(inv, inv), inv);  // a^-3/2
+    const float ds = __fmul_rn(__fmul_rn(dinv, __fmul_rn(-0.5f, a32)), inv_len);
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = lane + 64 * i;
-            const float4 wv = j < d4 ? w4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            ss = __fadd_rn(ss, __fmul_rn(xv[i].x, xv[i].x));
-            ss = __fadd_rn(ss, __fmul_rn(xv[i].y, xv[i].y));
-            ss = __fadd_rn(ss, __fmul_rn(xv[i].z, xv[i].z));
-            ss = __fadd_rn(ss, __fmul_rn(xv[i].w, xv[i].w));
-            // gv becomes dy*w from here on
-            gv[i].x = __fmul_rn(gv[i].x, wv.x);
-            gv[i].y = __fmul_rn(gv[i].y, wv.y);
-            gv[i].z = __fmul_rn(gv[i].z, wv.z);
-            gv[i].w = __fmul_rn(gv[i].w, wv.w);
-            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].x, xv[i].x));
-            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].y, xv[i].y));
-            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].z, xv[i].z));
-            dinv = __fadd_rn(dinv, __fmul_rn(gv[i].w, xv[i].w));
-        }
-        ss = wave_sum(ss);
-        dinv = wave_sum(dinv);
-        const float a = __fadd_rn(__fmul_rn(ss, inv_len), eps);
-        const float inv = __fdiv_rn(1.0f, __fsqrt_rn(a));
-        const float a32 = __fmul_rn(__fmul_rn(inv, inv), inv);  // a^-3/2
-        const float ds = __fmul_rn(__fmul_rn(dinv, __fmul_rn(-0.5f, a32)), inv_len);
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = lane + 64 * i;
-            if (j >= d4) continue;
-            const float4 gd = g4[j];  // dy again (cache) for the weight gradient
-            float4 sh;
+    for (int i = 0; i < NV; ++i) {
+        const int j = lane + 64 * i;
+        const float4 wv = ws[j];
+        float4 sh, pw;
 #define MMH_SHARE(c)                                                                   \
     {                                                                                  \
         const float t = __fmul_rn(ds, xv[i].c);                                        \
-        sh.c = __fadd_rn(__fadd_rn(__fmul_rn(gv[i].c, inv), t), t);                    \
-        pw[i].c = __fadd_rn(pw[i].c, __fmul_rn(gd.c, __fmul_rn(xv[i].c, inv)));        \
+        sh.c = __fadd_rn(__fadd_rn(__fmul_rn(__fmul_rn(gv[i].c, wv.c), inv), t), t);   \
+        pw.c = __fmul_rn(gv[i].c, __fmul_rn(xv[i].c, inv));                            \
+        if (accumulate) sh.c = __fadd_rn(ov[i].c, sh.c);                               \
     }
-            MMH_SHARE(x)
-            MMH_SHARE(y)
-            MMH_SHARE(z)
-            MMH_SHARE(w)
+        MMH_SHARE(x)
+        MMH_SHARE(y)
+        MMH_SHARE(z)
+        MMH_SHARE(w)
 #undef MMH_SHARE
-            if (accumulate) {
-                const float4 o = o4[j];
-                sh.x = __fadd_rn(o.x, sh.x);
-                sh.y = __fadd_rn(o.y, sh.y);
-                sh.z = __fadd_rn(o.z, sh.z);
-                sh.w = __fadd_rn(o.w, sh.w);
-            }
-            o4[j] = sh;
-        }
-    }
-    // Workgroup partial: waves 1..3 park theirs in LDS, wave 0 adds in order.
-    __shared__ float4 part[3][64 * NV];
-    if (wave > 0) {
-#pragma unroll
-        for (int i = 0; i < NV; ++i) part[wave - 1][lane + 64 * i] = pw[i];
+        part[wave][j] = pw;
+        if (live && j < d4) o4[j] = sh;
     }
     __syncthreads();
-    if (wave == 0) {
-        float4 *out = reinterpret_cast<float4 *>(partial + (int64_t)blockIdx.x * d);
+    // column sums over the workgroup's rows, in wave (row) order
+    float4 *out = reinterpret_cast<float4 *>(partial + (int64_t)blockIdx.x * d);
+    for (int j = threadIdx.x; j < d4; j += 64 * WPB) {
+        float4 s = part[0][j];
 #pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int j = lane + 64 * i;
-            if (j >= d4) continue;
-            float4 s = pw[i];
-            for (int wv = 0; wv < 3; ++wv) {
-                const float4 o = part[wv][j];
-                s.x = __fadd_rn(s.x, o.x);
-                s.y = __fadd_rn(s.y, o.y);
-                s.z = __fadd_rn(s.z, o.z);
-                s.w = __fadd_rn(s.w, o.w);
-            }
-            out[j] = s;
+        for (int wv = 1; wv < WPB; ++wv) {
+            const float4 o = part[wv][j];
+            s.x = __fadd_rn(s.x, o.x);
+            s.y = __fadd_rn(s.y, o.y);
+            s.z = __fadd_rn(s.z, o.z);
+            s.w = __fadd_rn(s.w, o.w);
         }
+        out[j] = s;
     }
 }
 
@@ -368,8 +379,9 @@ __global__ __launch_bounds__(256) void rms_dw_cols_kernel(const float *__restric
 }
 
 // out[j] = sum over the partial rows: workgroup = 64 columns x 16 waves; wave
-// w sums rows w, w+16, w+32, ... in order (eight loads in flight), then the
-// 16 wave sums are added in wave order. Fixed order for a given nrows.
+// w sums rows w, w+16, w+32, ... in order (sixteen loads in flight: 256 rows
+// take one round trip), then the 16 wave sums are added in wave order. Fixed
+// order for a given nrows.
 constexpr int SUM_WAVES = 16;
 
 __global__ __launch_bounds__(64 * SUM_WAVES) void sum_rows_kernel(const float *__restrict__ partial,
@@ -381,12 +393,12 @@ __global__ __launch_bounds__(64 * SUM_WAVES) void sum_rows_kernel(const float *_
     if (j < d) {
         constexpr int S = SUM_WAVES;
         int64_t r = wave;
-        for (; r + 7 * S < nrows; r += 8 * S) {
-            float a[8];
+        for (; r + 15 * S < nrows; r += 16 * S) {
+            float a[16];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) a[u] = partial[(r + u * S) * d + j];
+            for (int u = 0; u < 16; ++u) a[u] = partial[(r + u * S) * d + j];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) acc = __fadd_rn(acc, a[u]);
+            for (int u = 0; u < 16; ++u) acc = __fadd_rn(acc, a[u]);
         }
         for (; r < nrows; r += S) acc = __fadd_rn(acc, partial[r * d + j]);
     }
@@ -666,36 +678,50 @@ void launch_cross_entropy_fwd_bwd(Context &ctx, float *logits, const int32_t *ta
 }
 
 int64_t rms_norm_backward_scratch(int64_t rows, int64_t d) {
-    // partial rows (fast path: one per workgroup of 4*RMS_RPW rows; generic: row
+    // partial rows (fast path: one per workgroup of rms_wpb rows; generic: row
     // chunks of 64) plus one inv per row.
-    const int64_t fast = (rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW);
+    // (rms_wpb gives 1 below 1024 rows and at least 4 from there)
+    const int64_t fast = d > 4096 ? 0 : rows < 1024 ? rows : (rows + 3) / 4;
     const int64_t generic = (rows + 63) / 64;
-    return (fast > generic ? fast : generic) * d + rows;
+    return std::max(fast, generic) * d + rows;
 }
 
 void launch_rms_norm_backward(Context &ctx, const float *x, const float *w, const float *dy,
                               int64_t rows, int64_t d, float eps, float *dx, bool accumulate,
                               float *dw, float *scratch) {
-    const int vec = (d % 4 == 0) && d <= 4096 && al16(x) && al16(w) && al16(dy) && al16(dx) &&
-                    al16(scratch);
+    // (the rows kernel clamps its column index to d/4 - 1: d >= 4)
+    const int vec = (d % 4 == 0) && d >= 4 && d <= 4096 && al16(x) && al16(w) && al16(dy) &&
+                    al16(dx) && al16(scratch);
     if (vec) {
-        // one row per wave: 8 waves per workgroup (4 at d above 2048, whose
-        // rows hold twice the registers), the rows' weight-gradient terms in
-        // LDS ([waves][d] floats)
-        const int64_t blocks = (rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW);
+        // one row per wave, rms_wpb waves per workgroup
+        const int nv = rms_nv(d), wpb = rms_wpb(rows, nv);
+        const int64_t blocks = (rows + wpb - 1) / wpb;
         if (blocks > 0x7fffffff) fail(MMH_ERR_SHAPE, "rms_norm backward: too many rows");
-        const dim3 grid((unsigned)blocks), block(256);
+        const dim3 grid((unsigned)blocks), block(64 * wpb);
         const int dd = (int)d, acc = accumulate ? 1 : 0;
-        if (d <= 256)
-            hipLaunchKernelGGL(rms_bwd_rows_kernel<1>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
-        else if (d <= 512)
-            hipLaunchKernelGGL(rms_bwd_rows_kernel<2>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
-        else if (d <= 1024)
-            hipLaunchKernelGGL(rms_bwd_rows_kernel<4>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
-        else if (d <= 2048)
-            hipLaunchKernelGGL(rms_bwd_rows_kernel<8>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
-        else
-            hipLaunchKernelGGL(rms_bwd_rows_kernel<16>, grid, block, 0, ctx.stream, x, w, dy, rows, dd, eps, dx, acc, scratch);
+#define MMH_RMS_LAUNCH(NV, W)                                                                     \
+    hipLaunchKernelGGL((rms_bwd_rows_kernel<NV, W>), grid, block, 0, ctx.stream, x, w, dy, rows, \
+                       dd, eps, dx, acc, scratch)
+#define MMH_RMS_WAVES(NV, TOP)       \
+    if (wpb == TOP)                  \
+        MMH_RMS_LAUNCH(NV, TOP);     \
+    else if (wpb == 4)               \
+        MMH_RMS_LAUNCH(NV, 4);       \
+    else                             \
+        MMH_RMS_LAUNCH(NV, 1);
+        if (nv == 1) {
+            MMH_RMS_WAVES(1, 16)
+        } else if (nv == 2) {
+            MMH_RMS_WAVES(2, 16)
+        } else if (nv == 4) {
+            MMH_RMS_WAVES(4, 16)
+        } else if (nv == 8) {
+            MMH_RMS_WAVES(8, 16)
+        } else {
+            MMH_RMS_WAVES(16, 8)
+        }
+#undef MMH_RMS_WAVES
+#undef MMH_RMS_LAUNCH
         check_hip(hipGetLastError(), "rms_norm backward launch");
         hipLaunchKernelGGL(sum_rows_kernel, dim3(grid_for(d, 64)), dim3(64 * SUM_WAVES), 0,
                            ctx.stream, scratch, blocks, d, dw);

@@ -133,8 +133,10 @@ def test_attention_backward_matches_oracle(ctx, shape):
         assert np.abs(a - b).max() <= 2e-4 * scale, (name, float(np.abs(a - b).max()), scale)
 
 
+# (1029 and 4099 rows: 4 and 16 rows per workgroup with a ragged last
+# workgroup; 2049 x 4096: 8 rows per workgroup at the widest rows)
 @pytest.mark.parametrize("rows,d", [(7, 16), (33, 64), (64, 2048), (9, 4096), (5, 100),
-                                    (3, 4100)])
+                                    (3, 4100), (1029, 256), (4099, 512), (2049, 4096)])
 def test_rms_norm_backward_matches_oracle(ctx, rows, d):
     r = np.random.default_rng(rows * 7 + d)
     x = r.standard_normal((rows, d)).astype(np.float32)
