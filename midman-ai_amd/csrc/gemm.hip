@@ -742,8 +742,13 @@ constexpr int SBM = 64, SBN = 64, SBK = 32;
 // LDS rows hold one output row (A) or column (B) with its 32 k values
 // contiguous, padded to 36 floats: a lane reads its 16 k values of a step as
 // four 16-byte reads, and eight consecutive rows fall in distinct 16-byte bank
-// groups.
+// groups. An operand stored k-major in memory (A when TA, B when !TB) reaches
+// LDS as single values at (row, k), 16 rows 4 apart per 16 lanes: its rows
+// keep their eight float4 groups of k in the order g ^ ((row >> 3) & 7), so
+// those stores spread over the banks (2 lanes per bank instead of 8) while the
+// float4 reads stay aligned and conflict-free.
 constexpr int SKS = SBK + 4;
+__device__ __forceinline__ int sk_swz(int row) { return (row >> 3) & 7; }
 
 // The K loop of one 64x64 tile. MFMA kk of a step takes k = kk from lanes
 // 0-31 and k = 16 + kk from lanes 32-63 (any split of the step's k values
@@ -861,17 +866,17 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
                 *reinterpret_cast<float4 *>(&As[buf][idx >> 3][(idx & 7) * 4]) = va;
             } else {
                 const int k = idx >> 4, row = (idx & 15) * 4;
-                As[buf][row + 0][k] = va.x;
-                As[buf][row + 1][k] = va.y;
-                As[buf][row + 2][k] = va.z;
-                As[buf][row + 3][k] = va.w;
+                As[buf][row + 0][k ^ (4 * sk_swz(row + 0))] = va.x;
+                As[buf][row + 1][k ^ (4 * sk_swz(row + 1))] = va.y;
+                As[buf][row + 2][k ^ (4 * sk_swz(row + 2))] = va.z;
+                As[buf][row + 3][k ^ (4 * sk_swz(row + 3))] = va.w;
             }
             if (!TB) {
                 const int k = idx >> 4, col = (idx & 15) * 4;
-                Bs[buf][col + 0][k] = vb.x;
-                Bs[buf][col + 1][k] = vb.y;
-                Bs[buf][col + 2][k] = vb.z;
-                Bs[buf][col + 3][k] = vb.w;
+                Bs[buf][col + 0][k ^ (4 * sk_swz(col + 0))] = vb.x;
+                Bs[buf][col + 1][k ^ (4 * sk_swz(col + 1))] = vb.y;
+                Bs[buf][col + 2][k ^ (4 * sk_swz(col + 2))] = vb.z;
+                Bs[buf][col + 3][k ^ (4 * sk_swz(col + 3))] = vb.w;
             } else {
                 *reinterpret_cast<float4 *>(&Bs[buf][idx >> 3][(idx & 7) * 4]) = vb;
             }
@@ -881,14 +886,15 @@ __device__ __forceinline__ void small_mainloop(const KParams &p, const float *__
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int lr = lane & 31, lk = lane >> 5;
+    const int ga = TA ? sk_swz(wm * 32 + lr) : 0, gb = TB ? 0 : sk_swz(wn * 32 + lr);
     auto compute = [&](int buf) __attribute__((always_inline)) {
-        const float4 *pa = reinterpret_cast<const float4 *>(&As[buf][wm * 32 + lr][16 * lk]);
-        const float4 *pb = reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + lr][16 * lk]);
+        const float4 *pa = reinterpret_cast<const float4 *>(&As[buf][wm * 32 + lr][0]);
+        const float4 *pb = reinterpret_cast<const float4 *>(&Bs[buf][wn * 32 + lr][0]);
         float4 a[4], b[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            a[q] = pa[q];
-            b[q] = pb[q];
+            a[q] = pa[(4 * lk + q) ^ ga];
+            b[q] = pb[(4 * lk + q) ^ gb];
         }
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
