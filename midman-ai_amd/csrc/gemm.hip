@@ -1519,7 +1519,11 @@ int cus_of(const Context &ctx) { return ctx.cu_count > 0 ? ctx.cu_count : 256; }
 // that one workgroup walking it alone stays cheap.
 bool use_small(const Context &ctx, const GemmDesc &d) {
     const int64_t big_tiles = ((d.m + BM - 1) / BM) * ((d.n + BN - 1) / BN) * d.batch;
-    return d.force_splits == 0 && big_tiles < cus_of(ctx) && d.k <= 1024;
+    // (K up to 2048 for products of at most 2^29 multiply-adds: the 64x64
+    // tiles' splits sum in one launch, where the 128x128 splits need the
+    // reduce kernel; larger products keep the 128x128 tiles' operand reuse)
+    return d.force_splits == 0 && big_tiles < cus_of(ctx) &&
+           (d.k <= 1024 || (d.k <= 2048 && d.m * d.n * d.k <= (int64_t(1) << 29)));
 }
 
 // When the K-split kernel runs: 1 for the small nn shapes of one matrix whose
