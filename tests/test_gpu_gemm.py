@@ -120,6 +120,9 @@ MIN_POSITIVE = np.float32(1.17549435e-38)
 SPECIAL_PATHS = [
     ("128x128 tiles, interior and edges", 1100, 48, 4100),
     ("64x64 tiles, partial K step", 2048, 500, 1024),
+    # K beyond 1024 on the 64x64 tiles (at most 2^29 multiply-adds): 4 splits
+    # of 16 K-steps, the last one short, summed by each tile's last split
+    ("64x64 tiles, K 2000 in 4 splits summed by the last split", 256, 2000, 1024),
     ("32x32 K-split tiles", 2048, 344, 128),
     ("32x32 K-split over 8 workgroups + reduce", 256, 2048, 256),
     ("128x128 split 8 ways along K + reduce", 1024, 8192, 1024),

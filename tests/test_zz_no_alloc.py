@@ -50,6 +50,9 @@ def operands(form, m, k, n, seed):
     # the sweep's largest partials (16 MiB: dB 4096 x 256 from 2048 rows, 4
     # splits), then the smallest sweep dB
     ("tn", (4096, 2048, 256), (256, 2048, 256)),
+    # the sweep's 1 GFLOP dB products: 64x64 tiles, 4 splits summed by each
+    # tile's last split (the counters in the static set)
+    ("tn", (256, 2048, 1024), (1024, 2048, 256)),
 ])
 @pytest.mark.parametrize("accumulate", [False, True])
 def test_noalloc_matches_the_allocating_entry_point(ctx, form, first, second, accumulate):
