@@ -72,6 +72,17 @@ int32_t mmh_context_destroy(mmh_handle ctx);
 int32_t mmh_synchronize(mmh_handle ctx);
 /* Device name (NUL-terminated, truncated to cap) and compute-unit count. */
 int32_t mmh_device_info(mmh_handle ctx, char *name, uint32_t cap, int32_t *cu_count);
+/* Diagnostic with no reference counterpart: how the fused forward (see
+ * MMH_PATH_AUTO) gives its workgroups their per-XCD team slots on this
+ * context. *teams = 1 when the context's probe found 8 XCDs dealt equal
+ * shares (else the fused launch is not used). *round_robin = 1 when the probe
+ * also found the dispatch dealing workgroup b to XCD (b + o) % 8 with o fixed
+ * per launch, so a workgroup's slot is b / 8 with no atomic (each launch still
+ * checks that all its workgroups saw one offset, else the forward is redone on
+ * the per-operation kernels); 0: one returning atomic per workgroup. The
+ * environment variable MMH_FUSED_ATOMIC_SLOTS=1 at context creation forces
+ * the atomic slots. Either pointer may be NULL. */
+int32_t mmh_context_fused_slots(mmh_handle ctx, int32_t *teams, int32_t *round_robin);
 /* Diagnostic with no reference counterpart: the fp32 MFMA rate the whole chip
  * sustains on register operands with no memory traffic (4 independent
  * 32x32x2 chains per wave, 4 waves per SIMD, operands with pseudo-random

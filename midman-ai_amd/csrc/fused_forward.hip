@@ -47,6 +47,8 @@
 //
 // Every global access goes through a buffer descriptor sized to its buffer,
 // so an index outside it reads zero / writes nothing instead of faulting.
+#include <vector>
+
 #include "mmh_internal.h"
 
 #include <type_traits>
@@ -125,6 +127,7 @@ struct FusedP {
     float *loss;
     int32_t *err;         // error bits (a word of the arena, also addressed here)
     uint64_t *stamps;     // diagnostic clock stamps (start, end) per workgroup, or null
+    int32_t rr;           // team slots from the dispatch order (blockIdx / 8), see the kernel
     uint32_t w_bytes, f_bytes, i_bytes, tgt_off;
     // arena regions (float offsets)
     uint32_t o_x, o_h, o_qkv, o_part, o_zt, o_rl, o_p64, o_ctl, o_err, o_cos, o_sin, o_op, o_x2;
@@ -644,11 +647,26 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     // The XCD this workgroup runs on and its slot in that XCD's team (the
     // dispatcher deals workgroups round-robin over the XCDs, but not always
     // from XCD 0: as a graph node the first one lands elsewhere).
+    // rr: the context's probe found the dispatch round-robin over the XCDs
+    // with one offset per launch (workgroup b on XCD (b + o) % 8), so the
+    // workgroups of an XCD are b = c, c + 8, ... and b / 8 is a slot of its
+    // own, with no atomic (32 returning atomics on one counter per XCD put
+    // 1.5-4.5 us before the first task). Each workgroup records its offset
+    // (xcc - b) % 8 in a mask; the last one out flags (error bit 2) a launch
+    // whose workgroups saw more than one. Otherwise: a returning atomic per XCD.
     if (tid0 == 0) {
         const int xr = xcc_id();
-        const int sl = xr < 8 ? __hip_atomic_fetch_add(ctl + 1 + xr, 1, __ATOMIC_RELAXED,
-                                                       __HIP_MEMORY_SCOPE_AGENT)
-                              : team;
+        int sl = team;
+        if (xr < 8) {
+            if (p.rr) {
+                sl = (int)(blockIdx.x >> 3);
+                __hip_atomic_fetch_or(ctl + 1, 1 << ((xr - (int)blockIdx.x) & 7), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+            } else {
+                sl = __hip_atomic_fetch_add(ctl + 1 + xr, 1, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
         s_x = xr & 7;
         s_slot = sl;
         if (sl >= team) __hip_atomic_fetch_or(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1105,6 +1123,10 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     }
     if (__any(missing != 0) && (tid0 & 63) == 0)
         __hip_atomic_fetch_or(p.err, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // rr: every workgroup's offset recorded before it counted itself out
+    if (p.rr && tid0 == 0 &&
+        __builtin_popcount(__hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) != 1)
+        __hip_atomic_fetch_or(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (tid0 == 0) {
         double sum = 0.0;
@@ -1120,10 +1142,14 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     }
 }
 
-// One single-wave workgroup per CU, counted per XCD.
-__global__ __launch_bounds__(64) void xcd_probe_kernel(int *counts) {
-    if (threadIdx.x == 0)
-        __hip_atomic_fetch_add(counts + (xcc_id() & 15), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// One single-wave workgroup per CU, counted per XCD; each workgroup's XCD
+// recorded by its index.
+__global__ __launch_bounds__(64) void xcd_probe_kernel(int *counts, int *order) {
+    if (threadIdx.x == 0) {
+        const int x = xcc_id();
+        __hip_atomic_fetch_add(counts + (x & 15), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        order[blockIdx.x] = x;
+    }
 }
 
 }  // namespace
@@ -1131,18 +1157,30 @@ __global__ __launch_bounds__(64) void xcd_probe_kernel(int *counts) {
 // ---- host side -------------------------------------------------------------
 
 bool probe_xcd_teams(Context &ctx) {
+    ctx.xcd_rr = false;
     if (ctx.cu_count < 8 || ctx.cu_count % 8 != 0) return false;
+    const int g = ctx.cu_count;
     int *counts = nullptr;
+    std::vector<int> order((size_t)g);
     int h[16] = {};
-    bool ok = hipMalloc(&counts, sizeof(h)) == hipSuccess;
-    ok = ok && hipMemset(counts, 0, sizeof(h)) == hipSuccess;
-    if (ok) {
-        hipLaunchKernelGGL(xcd_probe_kernel, dim3((unsigned)ctx.cu_count), dim3(64), 0, nullptr, counts);
+    bool ok = hipMalloc(&counts, sizeof(h) + (size_t)g * 4) == hipSuccess;
+    // three launches: equal XCD shares in each; the round-robin order (block b
+    // on XCD (b + o) % 8, o fixed within a launch) in every one of them
+    bool rr = true;
+    for (int run = 0; run < 3 && ok; ++run) {
+        ok = hipMemset(counts, 0, sizeof(h) + (size_t)g * 4) == hipSuccess;
+        if (!ok) break;
+        hipLaunchKernelGGL(xcd_probe_kernel, dim3((unsigned)g), dim3(64), 0, nullptr, counts,
+                           counts + 16);
         ok = hipGetLastError() == hipSuccess && hipDeviceSynchronize() == hipSuccess &&
-             hipMemcpy(h, counts, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess;
+             hipMemcpy(h, counts, sizeof(h), hipMemcpyDeviceToHost) == hipSuccess &&
+             hipMemcpy(order.data(), counts + 16, (size_t)g * 4, hipMemcpyDeviceToHost) == hipSuccess;
+        for (int x = 0; x < 16 && ok; ++x) ok = h[x] == (x < 8 ? g / 8 : 0);
+        const int o = (order[0] & 7);
+        for (int b = 0; b < g && ok; ++b) rr = rr && order[b] < 8 && order[b] == ((b + o) & 7);
     }
     if (counts) (void)hipFree(counts);
-    for (int x = 0; x < 16 && ok; ++x) ok = h[x] == (x < 8 ? ctx.cu_count / 8 : 0);
+    ctx.xcd_rr = ok && rr;
     return ok;
 }
 
@@ -1217,6 +1255,7 @@ void launch_fused_forward(Context &ctx, const FusedArgs &a) {
     p.loss = a.loss;
     p.err = reinterpret_cast<int32_t *>(a.arena + f.o_err);
     p.stamps = a.stamps;
+    p.rr = ctx.xcd_rr ? 1 : 0;
     p.w_bytes = (uint32_t)(s.weight_floats * 4);
     p.f_bytes = (uint32_t)(f.floats * 4);
     p.tgt_off = (uint32_t)(a.tgt - a.ids);

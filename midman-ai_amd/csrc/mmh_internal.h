@@ -64,6 +64,9 @@ struct Context {
     // 8 XCDs, each dealt cu_count / 8 of a cu_count-workgroup grid (probed at
     // creation): what the fused forward's per-XCD teams need
     bool xcd_teams = false;
+    // the dispatch deals workgroup b to XCD (b + o) % 8 with o fixed per
+    // launch (checked at creation): the fused forward's team slots are b / 8
+    bool xcd_rr = false;
     std::string name;
     void *ws[kSlots] = {};
     size_t ws_bytes[kSlots] = {};

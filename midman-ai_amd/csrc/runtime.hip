@@ -8,6 +8,8 @@
 #include <mutex>
 #include <new>
 
+#include <cstdlib>
+
 #include "mmh_internal.h"
 
 namespace mmh {
@@ -108,6 +110,8 @@ int32_t mmh_context_create(int32_t device, mmh_handle *out_ctx) {
         check_hip(hipEventCreate(&c->t0), "event create");
         check_hip(hipEventCreate(&c->t1), "event create");
         c->xcd_teams = probe_xcd_teams(*c);
+        if (const char *e = std::getenv("MMH_FUSED_ATOMIC_SLOTS"))
+            if (e[0] == '1') c->xcd_rr = false;
         check_hip(hipMalloc(&c->tickets, Context::kTickets * sizeof(int32_t)), "ticket alloc");
         check_hip(hipMemsetAsync(c->tickets, 0, Context::kTickets * sizeof(int32_t), c->stream),
                   "ticket clear");
@@ -158,6 +162,15 @@ int32_t mmh_device_info(mmh_handle ctx, char *name, uint32_t cap, int32_t *cu_co
             name[n] = '\0';
         }
         if (cu_count) *cu_count = c.cu_count;
+        return MMH_OK;
+    });
+}
+
+int32_t mmh_context_fused_slots(mmh_handle ctx, int32_t *teams, int32_t *round_robin) {
+    return guard([&] {
+        Context &c = context(ctx);
+        if (teams) *teams = c.xcd_teams ? 1 : 0;
+        if (round_robin) *round_robin = c.xcd_teams && c.xcd_rr ? 1 : 0;
         return MMH_OK;
     });
 }

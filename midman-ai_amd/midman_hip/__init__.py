@@ -83,6 +83,7 @@ _SIGNATURES = {
     "mmh_context_destroy": [_h],
     "mmh_synchronize": [_h],
     "mmh_device_info": [_h, ctypes.c_char_p, ctypes.c_uint32, ctypes.POINTER(_i32)],
+    "mmh_context_fused_slots": [_h, ctypes.POINTER(_i32), ctypes.POINTER(_i32)],
     "mmh_mfma_peak_probe": [_h, ctypes.POINTER(ctypes.c_double)],
     "mmh_alloc": [_h, ctypes.c_uint64, ctypes.POINTER(_vp)],
     "mmh_free": [_h, _vp],
@@ -301,6 +302,14 @@ class Context:
         cu = _i32()
         check(lib().mmh_device_info(self.handle, buf, 256, ctypes.byref(cu)))
         return buf.value.decode(), cu.value
+
+    def fused_slots(self):
+        """(teams, round_robin): whether the fused forward runs on this
+        context, and whether its workgroups take their team slots from the
+        dispatch order (True) or from one atomic each (False)."""
+        teams, rr = _i32(), _i32()
+        check(lib().mmh_context_fused_slots(self.handle, ctypes.byref(teams), ctypes.byref(rr)))
+        return bool(teams.value), bool(rr.value)
 
     def mfma_peak_tflops(self) -> float:
         """The fp32 MFMA rate the chip sustains with no memory traffic (a

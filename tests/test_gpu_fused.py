@@ -226,3 +226,45 @@ def test_fused_loss_slot_bound(ctx, batch, fits):
         assert m.broken_guards() == 0
     finally:
         m.close()
+
+
+def test_team_slots_from_the_dispatch_order_match_the_atomic_slots(ctx):
+    # The context's probe decides how the fused launch's workgroups get their
+    # per-XCD team slots: from the dispatch order (blockIdx / 8, checked by
+    # every launch) or from one returning atomic each. Both give the same
+    # tasks to the same XCD teams, so the same loss bit for bit, with no
+    # launch redone. MMH_FUSED_ATOMIC_SLOTS=1 at context creation forces the
+    # atomic slots.
+    import os
+    teams, rr = ctx.fused_slots()
+    print(f"\n[fused slots] default context: teams {teams}, round-robin {rr}", flush=True)
+    assert teams
+    os.environ["MMH_FUSED_ATOMIC_SLOTS"] = "1"
+    try:
+        actx = mh.Context(0)
+    finally:
+        del os.environ["MMH_FUSED_ATOMIC_SLOTS"]
+    try:
+        assert actx.fused_slots() == (True, False)
+        cfg = mh.PRESETS["tiny"]
+        losses = []
+        for c in (ctx, actx):
+            m = mh.Model.new(c, cfg, 0)
+            try:
+                x, y = m.lab_tokens(8, 256)
+                m.stage(x, y, 8, 256)
+                for _ in range(3):
+                    m.run_staged(8, 256)
+                staged = m.read_loss()
+                direct = float(m.loss(x, y, 8, 256))
+                assert m.last_forward_fused()
+                assert m.fused_fallbacks()[0] == 0
+                assert np.float32(staged) == np.float32(direct)
+                losses.append(np.float32(direct))
+            finally:
+                m.close()
+        print(f"  loss {float(losses[0]):.7f} (slot mode of the default context), "
+              f"{float(losses[1]):.7f} (atomic slots)", flush=True)
+        assert losses[0].view(np.uint32) == losses[1].view(np.uint32)
+    finally:
+        actx.close()
