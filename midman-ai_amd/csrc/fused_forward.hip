@@ -605,22 +605,25 @@ __device__ __forceinline__ void attention_task(int tid, const FusedP &p, const R
 // The head's A operand for vocabulary block b (256 rows), K step stp: the
 // wave's 32 vocabulary rows 256 b + 32 w + l % 32 (clamped to V - 1), k =
 // 32 stp + 16 (l / 32) + j, from the tied embedding [V, d] (TIE) or lm_head [d, V].
+// oob: the loads read past the descriptor (zeros, no memory access): the
+// loop's last refill, whose values are never used, costs no round trip that
+// the task's final wait would sit out.
 template <bool TIE>
 __device__ __forceinline__ void head_load_a(int tid, const FusedP &p, const Res &R, int b, int stp,
-                                            int wave, float *a) {
+                                            int wave, float *a, bool oob = false) {
     const int lane = tid & 63, lr = lane & 31, lk = lane >> 5;
     const int v = min(256 * b + 32 * wave + lr, p.V - 1);
     if constexpr (TIE) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const float4 ev = ld4s<0>(R.w, 4u * (uint32_t)v * (uint32_t)p.d + 64u * lk + 16u * i, 128 * stp);
+            const float4 ev = ld4s<0>(R.w, oob ? kOOB : 4u * (uint32_t)v * (uint32_t)p.d + 64u * lk + 16u * i, 128 * stp);
             a[4 * i + 0] = ev.x;
             a[4 * i + 1] = ev.y;
             a[4 * i + 2] = ev.z;
             a[4 * i + 3] = ev.w;
         }
     } else {
-        const uint32_t vh = 4u * ((uint32_t)(p.o_head + v) + 16u * lk * (uint32_t)p.V);
+        const uint32_t vh = oob ? kOOB : 4u * ((uint32_t)(p.o_head + v) + 16u * lk * (uint32_t)p.V);
 #pragma unroll
         for (int jj = 0; jj < 16; ++jj) a[jj] = ld1s<0>(R.w, vh, 4 * (32 * stp + jj) * p.V);
     }
@@ -1009,11 +1012,11 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
                         // (scheduling barriers keep the loads where they are
                         // written: the scheduler would sink them to the end)
                         __builtin_amdgcn_sched_barrier(0);
-                        head_load_a<TIE>(tid, p, R, nb, ns, wave, gp.v);
+                        head_load_a<TIE>(tid, p, R, nb, ns, wave, gp.v, last);
                         __builtin_amdgcn_sched_barrier(0);
                         head_step(stp + 1, stp + 2 < hns ? stp + 2 : 0, gp.v + 16, x0);
                         __builtin_amdgcn_sched_barrier(0);
-                        head_load_a<TIE>(tid, p, R, nb, ns + 1, wave, gp.v + 16);
+                        head_load_a<TIE>(tid, p, R, nb, ns + 1, wave, gp.v + 16, last);
                         __builtin_amdgcn_sched_barrier(0);
                     }
                     head_block(b);
@@ -1114,6 +1117,9 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     // then adds them in index order.
     double *sm_p = reinterpret_cast<double *>(s_xs);  // B * nrb <= kLossSlots (host-checked)
     const int nblk = p.B * nrb;
+    // rr: every workgroup's offset recorded before it counted itself out
+    // (the word read first, so its round trip overlaps the loads below)
+    const int rr_mask = p.rr && tid0 == 0 ? __hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 1;
     int missing = 0;
     for (int i = tid0; i < nblk; i += kNT) {
         const int ss_ = i / nrb, qq = i - ss_ * nrb;
@@ -1123,9 +1129,7 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     }
     if (__any(missing != 0) && (tid0 & 63) == 0)
         __hip_atomic_fetch_or(p.err, 4, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // rr: every workgroup's offset recorded before it counted itself out
-    if (p.rr && tid0 == 0 &&
-        __builtin_popcount(__hip_atomic_load(ctl + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) != 1)
+    if (__builtin_popcount(rr_mask) != 1)
         __hip_atomic_fetch_or(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (tid0 == 0) {
