@@ -1113,8 +1113,8 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
         return;
     }
     // every row block of every sequence combined? Each thread checks row
-    // blocks i = tid, tid + 512, ... and parks their f64 sums in LDS; thread 0
-    // then adds them in index order.
+    // blocks i = tid, tid + 512, ... and parks their f64 sums in LDS; wave 0
+    // then adds them in a fixed order.
     double *sm_p = reinterpret_cast<double *>(s_xs);  // B * nrb <= kLossSlots (host-checked)
     const int nblk = p.B * nrb;
     // rr: every workgroup's offset recorded before it counted itself out
@@ -1132,10 +1132,14 @@ __global__ __launch_bounds__(kNT, 1) void forward_team_kernel(FusedP p) {
     if (__builtin_popcount(rr_mask) != 1)
         __hip_atomic_fetch_or(p.err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (tid0 == 0) {
+    if (tid0 < 64) {
+        // fixed order: lane l adds blocks l, l + 64, ... in turn, then the 64
+        // lane sums meet in a fixed tree
         double sum = 0.0;
-        for (int i = 0; i < nblk; ++i) sum += sm_p[i];
-        *p.loss = (float)(sum / (double)p.n);
+        for (int i = tid0; i < nblk; i += 64) sum += sm_p[i];
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+        if (tid0 == 0) *p.loss = (float)(sum / (double)p.n);
     }
     __syncthreads();
     for (int i = tid0; i < (int)p.ctl_ints; i += kNT) st1<kDev>(R.f, 4u * (p.o_ctl + i), 0.0f);
