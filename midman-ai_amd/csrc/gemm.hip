@@ -562,16 +562,34 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
         const int64_t c0 = CL == 1 ? n0 + wn * 64 + lr : n0 + wn * 32 + lr;
         const bool rot = p.rope_cos != nullptr && c0 < p.rope_cols;
         float *C = p.c + batch * p.stride_c;
+        // The rows' table values are all read before the first store: the
+        // compiler cannot tell the tables from C, so a read placed after a
+        // store waits for that store's completion (one memory round trip per
+        // row). Rows past M read a valid table row (row % seq) and are dropped.
+        // Positions: the lane's first row modulo the sequence once; register
+        // r adds 8*(r/4) + r%4 < 28 to it, at most one wrap when seq >= 28.
+        float cs[16], sn[16];
+        if (rot) {
+            const uint32_t seq = (uint32_t)p.rope_seq;
+            const uint32_t base = (uint32_t)((m0 + row_local(0)) % p.rope_seq);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                uint32_t pos = base + (uint32_t)(8 * (r >> 2) + (r & 3));
+                if (seq < 28) pos %= seq;
+                else if (pos >= seq) pos -= seq;
+                const uint32_t t = pos * (uint32_t)half + (uint32_t)hc;
+                cs[r] = p.rope_cos[t];
+                sn[r] = p.rope_sin[t];
+            }
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t row = m0 + row_local(r);
             if (row >= M) continue;
             float x1 = acc[0][r], x2 = acc[1][r];
             if (rot) {
-                const int64_t t = (row % p.rope_seq) * half + hc;
-                const float cs = p.rope_cos[t], sn = p.rope_sin[t];
-                const float y1 = x1 * cs - x2 * sn;
-                const float y2 = x2 * cs + x1 * sn;
+                const float y1 = x1 * cs[r] - x2 * sn[r];
+                const float y2 = x2 * cs[r] + x1 * sn[r];
                 x1 = y1;
                 x2 = y2;
             }
