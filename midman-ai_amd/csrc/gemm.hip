@@ -47,6 +47,8 @@ namespace mmh {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int NT = 512;  // threads of the 128x128 kernel: 8 waves
@@ -413,6 +415,57 @@ __device__ __forceinline__ void split_reduce_tile(const KParams &p, int64_t m0, 
     const bool vecc = p.ldc % 4 == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0 &&
                       (!p.resid || (reinterpret_cast<uintptr_t>(p.resid) & 15) == 0);
     const float *R = p.resid ? p.resid : p.c;
+    const int iters = tr * tc / (4 * nthreads);
+    if (m0 + tr <= M && n0 + tc <= N && vecp && vecc && iters <= 4 &&
+        iters * 4 * nthreads == tr * tc) {
+        // The whole tile in range: every element's reads (the residual, then
+        // the partials) before the first store, so no read waits for a store.
+        float4 res[4];
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            if (it >= iters) break;
+            const int e = 4 * (int)threadIdx.x + it * 4 * nthreads;
+            const int64_t row = m0 + e / tc, col = n0 + e % tc;
+            const float4 o = p.split_accum ? *reinterpret_cast<const float4 *>(R + row * p.ldc + col)
+                                           : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float *Q = p.partial + row * N + col;
+            float4 acc;
+            for (int s0 = 0; s0 < p.splits; s0 += 4) {
+                float4 v[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (s0 + u < p.splits) {
+                        const float *src = Q + (int64_t)(s0 + u) * total;
+                        v[u].x = split_get(src);
+                        v[u].y = split_get(src + 1);
+                        v[u].z = split_get(src + 2);
+                        v[u].w = split_get(src + 3);
+                    }
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (s0 + u < p.splits) {
+                        if (s0 + u == 0) {
+                            acc = v[u];
+                        } else {
+                            acc.x = __fadd_rn(acc.x, v[u].x);
+                            acc.y = __fadd_rn(acc.y, v[u].y);
+                            acc.z = __fadd_rn(acc.z, v[u].z);
+                            acc.w = __fadd_rn(acc.w, v[u].w);
+                        }
+                    }
+            }
+            res[it] = p.split_accum ? make_float4(__fadd_rn(o.x, acc.x), __fadd_rn(o.y, acc.y),
+                                                  __fadd_rn(o.z, acc.z), __fadd_rn(o.w, acc.w))
+                                    : acc;
+        }
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+            if (it >= iters) break;
+            const int e = 4 * (int)threadIdx.x + it * 4 * nthreads;
+            *reinterpret_cast<float4 *>(p.c + (m0 + e / tc) * p.ldc + n0 + e % tc) = res[it];
+        }
+        return;
+    }
     for (int e = 4 * (int)threadIdx.x; e < tr * tc; e += 4 * nthreads) {
         const int64_t row = m0 + e / tc, col = n0 + e % tc;
         if (row >= M || col >= N) continue;
@@ -674,6 +727,39 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     if (EPI == EPI_SWIGLU_BWD) {
         // acc is dh[row][col, col+1]; their (g, u) pairs sit at aux columns
         // 2*col .. 2*col+3 and the (dg, du) pairs go to the same columns of C.
+        if (m0 + BM <= M && n0 + BN <= N && p.ldc < (int64_t(1) << 20) &&
+            p.ldaux < (int64_t(1) << 20)) {
+            // The whole tile in range: unconditional buffer accesses from the
+            // tile's first row (see the residual epilogue below), eight rows'
+            // pairs read before their eight stores.
+            const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(p.aux + m0 * p.ldaux), (short)0, kBufferRange, kBufferFlags);
+            const __amdgpu_buffer_rsrc_t rc =
+                __builtin_amdgcn_make_buffer_rsrc(C + m0 * p.ldc, (short)0, kBufferRange, kBufferFlags);
+            const uint32_t la = 4u * (uint32_t)p.ldaux, lc = 4u * (uint32_t)p.ldc;
+            const uint32_t va = (uint32_t)row_local(0) * la + 8u * (uint32_t)col;
+            const uint32_t vc = (uint32_t)row_local(0) * lc + 8u * (uint32_t)col;
+#pragma unroll
+            for (int r0 = 0; r0 < 16; r0 += 8) {
+                float4 g[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int r = r0 + j;
+                    g[j] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                          ra, va + (8 * (r >> 2) + (r & 3)) * la, 0, 0));
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int r = r0 + j;
+                    const float2 a = swiglu_bwd_f(acc[0][r], g[j].x, g[j].y);
+                    const float2 b2 = swiglu_bwd_f(acc[1][r], g[j].z, g[j].w);
+                    __builtin_amdgcn_raw_buffer_store_b128(
+                        __builtin_bit_cast(u32x4_t, make_float4(a.x, a.y, b2.x, b2.y)), rc,
+                        vc + (8 * (r >> 2) + (r & 3)) * lc, 0, 0);
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int r0 = 0; r0 < 16; r0 += 8) {
             float4 g[8];
@@ -708,6 +794,36 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     const bool pair = p.vec_c && col + 1 < N;
     if (EPI == EPI_ACCUM && pair) {
         float2 o[16];
+        if (m0 + BM <= M && p.ldc < (int64_t(1) << 21)) {
+            // Every row in range: no per-row branches, so the compiler counts
+            // the reads exactly and each store waits only for its own read
+            // (with the reads and stores under row tests, every store waited
+            // for all earlier stores as well: one store round trip per row).
+            // Buffer accesses from the tile's first row with 32-bit offsets
+            // (64-bit addresses for 16 rows took the kernel past the registers
+            // of four waves per SIMD). Each row's offset is added into the
+            // lane offset, never passed as the scalar offset: with computed
+            // scalar offsets the compiler reused an SGPR that a v_div_scale
+            // had just written as its carry-out, and one row of a tile read
+            // another row's values (found by the tail-pieces training test).
+            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<float *>(R + m0 * p.ldc), (short)0, kBufferRange, kBufferFlags);
+            const __amdgpu_buffer_rsrc_t rc =
+                __builtin_amdgcn_make_buffer_rsrc(C + m0 * p.ldc, (short)0, kBufferRange, kBufferFlags);
+            const uint32_t ldb4 = 4u * (uint32_t)p.ldc;
+            const uint32_t vo = (uint32_t)row_local(0) * ldb4 + 4u * (uint32_t)col;
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                o[r] = __builtin_bit_cast(
+                    float2, __builtin_amdgcn_raw_buffer_load_b64(rr, vo + (8 * (r >> 2) + (r & 3)) * ldb4, 0, 0));
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                __builtin_amdgcn_raw_buffer_store_b64(
+                    __builtin_bit_cast(u32x2_t, make_float2(__fadd_rn(o[r].x, acc[0][r]),
+                                                            __fadd_rn(o[r].y, acc[1][r]))),
+                    rc, vo + (8 * (r >> 2) + (r & 3)) * ldb4, 0, 0);
+            return;
+        }
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int64_t row = m0 + row_local(r);
@@ -1074,6 +1190,34 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
         return;
     }
     float *C = p.c + batch * p.stride_c;
+    // A tile inside [M, N): the epilogue's reads all go out before its first
+    // store, with no per-row branches (under row tests each read waited for
+    // the stores before it: one memory round trip per row). Buffer accesses
+    // from the tile's first row, each row's offset in the lane offset (as in
+    // the 128x128 kernel's epilogues).
+    const bool inside = m0 + SBM <= M && n0 + SBN <= N && p.ldc < (int64_t(1) << 21) &&
+                        (EPI != EPI_SWIGLU_BWD || p.ldaux < (int64_t(1) << 21));
+    const uint32_t lc = 4u * (uint32_t)p.ldc;
+    const uint32_t vrow = (uint32_t)(wm * 32 + 4 * lk);  // row_of(r) - m0 - (8*(r/4) + r%4)
+    if (EPI == EPI_SWIGLU_BWD && inside) {
+        const uint32_t la = 4u * (uint32_t)p.ldaux;
+        const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(p.aux + m0 * p.ldaux), (short)0, kBufferRange, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rc =
+            __builtin_amdgcn_make_buffer_rsrc(C + m0 * p.ldc, (short)0, kBufferRange, kBufferFlags);
+        float2 gu[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            gu[r] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(
+                                                   ra, (vrow + 8 * (r >> 2) + (r & 3)) * la + 8u * (uint32_t)col,
+                                                   0, 0));
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_buffer_store_b64(
+                __builtin_bit_cast(u32x2_t, swiglu_bwd_f(acc[r], gu[r].x, gu[r].y)), rc,
+                (vrow + 8 * (r >> 2) + (r & 3)) * lc + 8u * (uint32_t)col, 0, 0);
+        return;
+    }
     if (EPI == EPI_SWIGLU_BWD) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -1086,6 +1230,23 @@ __global__ __launch_bounds__(256) void gemm_f32_mfma_small(KParams p) {
         return;
     }
     const float *R = p.resid ? p.resid + batch * p.stride_c : C;
+    if (EPI == EPI_ACCUM && inside) {
+        const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float *>(R + m0 * p.ldc), (short)0, kBufferRange, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t rc =
+            __builtin_amdgcn_make_buffer_rsrc(C + m0 * p.ldc, (short)0, kBufferRange, kBufferFlags);
+        const uint32_t vo = vrow * lc + 4u * (uint32_t)col;
+        float o[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            o[r] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 rr, vo + (8 * (r >> 2) + (r & 3)) * lc, 0, 0));
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, __fadd_rn(o[r], acc[r])), rc,
+                                                  vo + (8 * (r >> 2) + (r & 3)) * lc, 0, 0);
+        return;
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) block32_epilogue<EPI>(p, C, R, row_of(r), col, lr, acc[r]);
 }
