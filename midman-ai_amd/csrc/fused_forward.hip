@@ -545,30 +545,47 @@ __device__ __forceinline__ void attention_task(int tid, const FusedP &p, const R
             if (i + 1 < NS)
                 sacc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[i + 1], qr[i + 1], sacc1, 0, 0, 0);
         }
+        // (the matrix core and the VALU take turns on a SIMD, so the VALU work
+        // between the products is kept short: the mask only on the tiles that
+        // need it, no rescale of the zero sums on a wave's first tile, the
+        // hardware exp2 (probabilities below 2^-126 flush to zero))
         const int k0 = kt * 32;
         float pv[16];
         float mloc = -INFINITY;
+        if (k0 + 31 > q0 || k0 + 32 > T) {
+            // the diagonal tile or the sequence's partial last one
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            const float sv = (sacc[r] + sacc1[r]) * sc;
-            pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
-            mloc = fmaxf(mloc, pv[r]);
+            for (int r = 0; r < 16; ++r) {
+                const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
+                const float sv = (sacc[r] + sacc1[r]) * sc;
+                pv[r] = (key <= qi && key < T) ? sv : -INFINITY;
+                mloc = fmaxf(mloc, pv[r]);
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                pv[r] = (sacc[r] + sacc1[r]) * sc;
+                mloc = fmaxf(mloc, pv[r]);
+            }
         }
         mloc = pair32_max(mloc);
-        const bool need = mloc > m_run + 8.0f;
-        if (__any(need)) {
-            const float m_new = need ? mloc : m_run;
-            const float alpha = exp2f(m_run - m_new);
-            l_run *= alpha;
+        if (kt == wave) {
+            m_run = mloc;  // o and l are still zero
+        } else {
+            const bool need = mloc > m_run + 8.0f;
+            if (__any(need)) {
+                const float m_new = need ? mloc : m_run;
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                l_run *= alpha;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) o[r] *= alpha;
-            m_run = m_new;
+                for (int r = 0; r < 16; ++r) o[r] *= alpha;
+                m_run = m_new;
+            }
         }
         float lsum = 0.0f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            pv[r] = exp2f(pv[r] - m_run);
+            pv[r] = __builtin_amdgcn_exp2f(pv[r] - m_run);
             lsum += pv[r];
         }
         l_run += pair32_sum(lsum);
@@ -585,8 +602,8 @@ __device__ __forceinline__ void attention_task(int tid, const FusedP &p, const R
     for (int w = 1; w < 8; ++w) mx = fmaxf(mx, sm_m[w * 32 + lq]);
     float Ls = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 8; ++w) Ls += sm_l[w * 32 + lq] * exp2f(sm_m[w * 32 + lq] - mx);
-    const float f = exp2f(m_run - mx) / Ls;  // 0 for a wave that saw no key
+    for (int w = 0; w < 8; ++w) Ls += sm_l[w * 32 + lq] * __builtin_amdgcn_exp2f(sm_m[w * 32 + lq] - mx);
+    const float f = __builtin_amdgcn_exp2f(m_run - mx) / Ls;  // 0 for a wave that saw no key
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
         const int dd = 8 * (r >> 2) + 4 * lh + (r & 3);
