@@ -714,7 +714,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
             if (p.aux && col + 1 < N)
                 *reinterpret_cast<float2 *>(p.aux + row * p.ldaux + col) =
                     make_float2(acc[0][r], acc[1][r]);
-            if (f < p.swiglu_ff) C[row * p.ldc + f] = __fmul_rn(silu_f(acc[0][r]), acc[1][r]);
+            if (f < p.swiglu_ff) C[row * p.ldc + f] = __fmul_rn(silu_fast(acc[0][r]), acc[1][r]);
         }
         return;
     }

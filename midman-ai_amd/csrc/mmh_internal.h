@@ -20,6 +20,14 @@ __device__ __forceinline__ float silu_f(float x) {
     const float s = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-x)));
     return __fmul_rn(x, s);
 }
+// silu through the hardware exp2 and reciprocal (a few ulp from silu_f): 5
+// VALU instructions instead of ~25 for the libm exp and the IEEE division.
+// The VALU's cycles add to the matrix core's on a SIMD, so the 128x128 GEMM
+// epilogue that finishes SwiGLU takes this form.
+__device__ __forceinline__ float silu_fast(float x) {
+    const float e = __builtin_amdgcn_exp2f(x * -1.4426950408889634f);
+    return x * __builtin_amdgcn_rcpf(1.0f + e);
+}
 
 // Backward of h = silu(g) * u (mul then silu, ops_elementwise.rs:287, :355-364):
 // dsilu = dh*u, du = dh*silu(g), dg = dsilu * s*(1 + g*(1 - s)); returns (dg, du).
