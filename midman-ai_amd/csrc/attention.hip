@@ -369,10 +369,21 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
     const int ltid = PER >= 1 ? tid : tid % F4;
     const int lj = (4 * ltid) / HD, lc = (4 * ltid) % HD;
     float4 kreg, vreg;
+    // Buffer loads over the sequence's T rows: 32-bit offsets (the 64-bit
+    // address arithmetic was a dozen VALU instructions per tile, and the VALU
+    // takes its cycles from the matrix core), keys past T read zeros (finite;
+    // their scores are masked and their P is 0). The host keeps T * stride
+    // below 2^29 floats for this kernel.
+    const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(K), (short)0, (int)(4 * (int64_t)T * p.skt), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(V), (short)0, (int)(4 * (int64_t)T * p.svt), 0x00020000);
+    const uint32_t klane = 4u * ((uint32_t)lj * (uint32_t)p.skt + (uint32_t)lc);
+    const uint32_t vlane = 4u * ((uint32_t)lj * (uint32_t)p.svt + (uint32_t)lc);
+    const uint32_t ktile = 128u * (uint32_t)p.skt, vtile = 128u * (uint32_t)p.svt;
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
-        const int key = min(kt * 32 + lj, T - 1);
-        kreg = *reinterpret_cast<const float4 *>(K + (int64_t)key * p.skt + lc);
-        vreg = *reinterpret_cast<const float4 *>(V + (int64_t)key * p.svt + lc);
+        kreg = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, klane + (uint32_t)kt * ktile, 0, 0));
+        vreg = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, vlane + (uint32_t)kt * vtile, 0, 0));
     };
     auto store_tile = [&](int kt) __attribute__((always_inline)) {
         if (loader) {
@@ -386,12 +397,14 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
     for (int db = 0; db < 4 * NH; ++db) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // sum / max over a query's four lanes (i, i+16, i+32, i+48)
+    // sum / max over a query's four lanes (i, i+16, i+32, i+48); the max as
+    // med3(a, b, +inf), which needs none of the quieting moves fmaxf takes
+    // around values from lane swaps (scores are finite or -inf)
     auto quad_max = [](float v) __attribute__((always_inline)) {
         auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+        v = __builtin_amdgcn_fmed3f(__uint_as_float(a[0]), __uint_as_float(a[1]), INFINITY);
         auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+        return __builtin_amdgcn_fmed3f(__uint_as_float(c[0]), __uint_as_float(c[1]), INFINITY);
     };
     auto quad_sum = [](float v) __attribute__((always_inline)) {
         auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -473,13 +486,14 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
                 for (int r = 0; r < 4; ++r) o[db][r] *= alpha;
             m_run = m_new;
         }
-        float lsum = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            pv[j] = __builtin_amdgcn_exp2f(pv[j] - m_run);
-            lsum += pv[j];
-        }
-        l_run += quad_sum(lsum);
+        for (int j = 0; j < 8; ++j) pv[j] = __builtin_amdgcn_exp2f(pv[j] - m_run);
+        float lsum = pv[0];
+#pragma unroll
+        for (int j = 1; j < 8; ++j) lsum += pv[j];
+        // the lane's own share: the four lanes of a query rescale together
+        // (one m_run), so their shares are summed once, when the strip ends
+        l_run += lsum;
     };
     auto pv_apply = [&](int kt) __attribute__((always_inline)) {
         __builtin_amdgcn_sched_barrier(0);
@@ -496,6 +510,7 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
         __builtin_amdgcn_sched_barrier(0);
+        if (kt == my_tiles - 1) l_run = quad_sum(l_run);
         if (kt == my_tiles - 1 && qi < T) {
             // this strip is done: its rows leave now, straight from the accumulators
             const float inv = 1.0f / l_run;
@@ -898,8 +913,10 @@ void attention_kernels(Context &ctx, const AttnDesc &d, float scale) {
     p.nqb = (int)(split ? (d.t + 31) / 32 : (d.t + 127) / 128);
     p.scale = scale;
     dim3 grid((unsigned)d.h, (unsigned)d.b, (unsigned)p.nqb);
-    // the 16-row kernel stores rows as float4s
-    const bool rows16 = al16(d.out) && d.sob % 4 == 0 && d.soh % 4 == 0 && d.sot % 4 == 0;
+    // the 16-row kernel stores rows as float4s and reads K and V through
+    // 32-bit buffer offsets over the sequence's rows
+    const bool rows16 = al16(d.out) && d.sob % 4 == 0 && d.soh % 4 == 0 && d.sot % 4 == 0 &&
+                        d.t * std::max(d.skt, d.svt) < (int64_t(1) << 29);
     switch (d.hd) {
         case 4: launch_hd<4>(ctx, p, grid, split, false); break;
         case 8: launch_hd<8>(ctx, p, grid, split, false); break;
