@@ -51,6 +51,15 @@ struct BwdP {
     float scale;
 };
 
+// A raw buffer over everything from base on (32-bit offsets, no range
+// check that matters) and its 16-byte load.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_all(const float *base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+__device__ __forceinline__ float4 ld4b(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 __device__ __forceinline__ floatx16 mfma(float a, float b, floatx16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
@@ -602,14 +611,19 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq16_kernel(BwdP p) {
     float4 kreg0, vreg0, kreg1, vreg1;
     const int j0 = (4 * tid) / HD, c0 = (4 * tid) % HD;
     const int j1 = (4 * (tid + NT)) / HD, c1 = (4 * (tid + NT)) % HD;
+    // 32-bit buffer offsets (the host keeps them below 2^31 bytes for these
+    // kernels): the 64-bit address arithmetic was VALU work, whose cycles the
+    // matrix core loses
+    const __amdgpu_buffer_rsrc_t rk = rsrc_all(K), rv = rsrc_all(V);
+    const uint32_t skt4 = 4u * (uint32_t)p.skt, svt4 = 4u * (uint32_t)p.svt;
     auto load_tile = [&](int kt) __attribute__((always_inline)) {
-        const int key0 = min(kt * 32 + j0, T - 1);
-        kreg0 = *reinterpret_cast<const float4 *>(K + (int64_t)key0 * p.skt + c0);
-        vreg0 = *reinterpret_cast<const float4 *>(V + (int64_t)key0 * p.svt + c0);
+        const uint32_t key0 = (uint32_t)min(kt * 32 + j0, T - 1);
+        kreg0 = ld4b(rk, key0 * skt4 + 4u * c0);
+        vreg0 = ld4b(rv, key0 * svt4 + 4u * c0);
         if constexpr (PER > 1) {
-            const int key1 = min(kt * 32 + j1, T - 1);
-            kreg1 = *reinterpret_cast<const float4 *>(K + (int64_t)key1 * p.skt + c1);
-            vreg1 = *reinterpret_cast<const float4 *>(V + (int64_t)key1 * p.svt + c1);
+            const uint32_t key1 = (uint32_t)min(kt * 32 + j1, T - 1);
+            kreg1 = ld4b(rk, key1 * skt4 + 4u * c1);
+            vreg1 = ld4b(rv, key1 * svt4 + 4u * c1);
         }
     };
     auto store_tile = [&](int kt) __attribute__((always_inline)) {
@@ -713,19 +727,22 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv16_kernel(BwdP p) {
     const int j0 = (4 * tid) / HD, c0 = (4 * tid) % HD;
     const int j1 = (4 * (tid + NT)) / HD, c1 = (4 * (tid + NT)) % HD;
     float lreg = 0.0f;
+    // 32-bit buffer offsets from the batch element's first head (the host
+    // keeps them below 2^31 bytes for these kernels)
+    const __amdgpu_buffer_rsrc_t rq = rsrc_all(p.q + b * p.sqb), rg = rsrc_all(p.dout + b * p.sob);
+    const uint32_t sqt4 = 4u * (uint32_t)p.sqt, sot4 = 4u * (uint32_t)p.sot;
     auto load_tile = [&](int it) __attribute__((always_inline)) {
         const int hh = it / per_head;
         const int qt = qt_first + (it - hh * per_head);
         const int head = kvh * groups + g0 + hh;
-        const float *Qh = p.q + b * p.sqb + head * p.sqh;
-        const float *Gh = p.dout + b * p.sob + head * p.soh;
-        const int q0r = min(qt * 32 + j0, T - 1);  // rows past T: finite, P = 0
-        qreg0 = *reinterpret_cast<const float4 *>(Qh + (int64_t)q0r * p.sqt + c0);
-        greg0 = *reinterpret_cast<const float4 *>(Gh + (int64_t)q0r * p.sot + c0);
+        const uint32_t qh4 = 4u * (uint32_t)(head * p.sqh), gh4 = 4u * (uint32_t)(head * p.soh);
+        const uint32_t q0r = (uint32_t)min(qt * 32 + j0, T - 1);  // rows past T: finite, P = 0
+        qreg0 = ld4b(rq, qh4 + q0r * sqt4 + 4u * c0);
+        greg0 = ld4b(rg, gh4 + q0r * sot4 + 4u * c0);
         if constexpr (PER > 1) {
-            const int q1r = min(qt * 32 + j1, T - 1);
-            qreg1 = *reinterpret_cast<const float4 *>(Qh + (int64_t)q1r * p.sqt + c1);
-            greg1 = *reinterpret_cast<const float4 *>(Gh + (int64_t)q1r * p.sot + c1);
+            const uint32_t q1r = (uint32_t)min(qt * 32 + j1, T - 1);
+            qreg1 = ld4b(rq, qh4 + q1r * sqt4 + 4u * c1);
+            greg1 = ld4b(rg, gh4 + q1r * sot4 + 4u * c1);
         }
         // lanes 0-31 of each wave fetch the tile's log-sum-exps, 32-63 its D
         const int q = min(qt * 32 + (tid & 31), T - 1);
@@ -1136,6 +1153,11 @@ void backward_kernels(Context &ctx, const AttnBwdDesc &d, float scale) {
     const unsigned strips = (unsigned)((d.t + 31) / 32);
     const dim3 sq((unsigned)d.h, (unsigned)d.b, strips), sk((unsigned)d.hkv, (unsigned)d.b, strips);
     const dim3 blk(256);
+    // the 16-row kernels read q, k, v and dout through 32-bit byte offsets
+    // from a batch element's first row (and head)
+    const int64_t span = d.t * std::max(std::max(d.sqt, d.skt), std::max(d.svt, d.sot)) +
+                         d.h * std::max(d.sqh, d.soh) + d.hd;
+    const bool off32 = span < (int64_t(1) << 29);
 #define MMH_BWD_CASE(HD)                                                                   \
     case HD:                                                                               \
         if constexpr (HD <= 64) {                                                          \
@@ -1146,9 +1168,11 @@ void backward_kernels(Context &ctx, const AttnBwdDesc &d, float scale) {
             }                                                                              \
         }                                                                                  \
         if constexpr (HD == 64 || HD == 128) {                                             \
+          if (off32) {                                                                     \
             hipLaunchKernelGGL((attn_bwd_dq16_kernel<HD>), gq, dim3(512), 0, ctx.stream, p);  \
             hipLaunchKernelGGL((attn_bwd_dkv16_kernel<HD>), gk, dim3(512), 0, ctx.stream, p); \
             break;                                                                         \
+          }                                                                                \
         }                                                                                  \
         hipLaunchKernelGGL((attn_bwd_dq_kernel<HD>), gq, blk, 0, ctx.stream, p);           \
         hipLaunchKernelGGL((attn_bwd_dkv_kernel<HD>), gk, blk, 0, ctx.stream, p);          \
