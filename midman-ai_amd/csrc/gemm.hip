@@ -165,14 +165,19 @@ __device__ __forceinline__ float half_sum32(float v) {
 // columns c and c + 64 of the tile (wave wn takes c = 32*wn .. +31), so the
 // RoPE pair (c, c + hd/2) of a head of 64 (CL 1) or 128 (CL 2) columns sits
 // in one lane.
-template <bool TA, bool TB, bool FAST, int SLOTS, int CL>
+template <bool TA, bool TB, bool FAST, int SLOTS, int CL, bool OPQ = false>
 __device__ __forceinline__ void gemm_mainloop(const KParams &p, const float *__restrict__ A,
                                               const float *__restrict__ B, int64_t m0, int64_t n0,
                                               int64_t kbeg, int64_t kend,
                                               float (*As)[BK][LdsA<TA>::S],
                                               float (*Bs)[BK][LdsB<TB>::S],
                                               floatx16 (&acc)[2]) {
-    const int tid = threadIdx.x;
+    // OPQ: the thread index through an empty asm. The register assignment
+    // and schedule the compiler then picks ran the residual-epilogue forms
+    // 0.8-1.4% faster on the large forward's o and down products, and the
+    // SwiGLU and loss forms 2% slower, so only the former take it.
+    int tid = threadIdx.x;
+    if constexpr (OPQ) asm volatile("" : "+v"(tid));
     const int64_t M = p.m, N = p.n;
     // A K-tile of each operand is 128 x BK floats = 32*BK float4; thread tid
     // moves float4 idx = tid + NT*i, i < NL.
@@ -583,7 +588,7 @@ __global__ __launch_bounds__(NT, 2) void gemm_f32_mfma(KParams p) {
     const bool fast = p.vec_a && p.vec_b && m0 + BM <= M && n0 + BN <= N &&
                       (kend - kbeg) % BK == 0;
     if (fast)
-        gemm_mainloop<TA, TB, true, KSLOTS, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
+        gemm_mainloop<TA, TB, true, KSLOTS, CL, EPI == EPI_ACCUM>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
     else
         gemm_mainloop<TA, TB, false, 1, CL>(p, A, B, m0, n0, kbeg, kend, As, Bs, acc);
 
