@@ -327,7 +327,9 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
     auto Ks = [&](int kt) { return smem + ((kt >> 1) & 1) * 64 * KS + (kt & 1) * 32 * KS; };
     auto Vs = [&](int kt) { return smem + 128 * KS + ((kt >> 1) & 1) * 64 * HD + (kt & 1) * 32 * HD; };
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index through readfirstlane: uniform, so what derives from it
+    // (strip, rows, tile counts, their tests) is scalar work in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, li = lane & 15;
     const int half = wave >> 3, w8 = wave & 7;
     const int strip = w8 < 4 ? w8 : 11 - w8;

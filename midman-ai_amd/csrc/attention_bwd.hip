@@ -570,7 +570,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq16_kernel(BwdP p) {
     auto Ks = [&](int kt) { return smem + ((kt >> 1) & 1) * 128 * KS + (kt & 1) * 32 * KS; };
     auto Vs = [&](int kt) { return Ks(kt) + 64 * KS; };
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index through readfirstlane: uniform, so what derives from it
+    // (strip, rows, tile counts, their tests) is scalar work in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, li = lane & 15;
     const int strip = wave < 4 ? wave : 11 - wave;
     const int head = blockIdx.x, b = blockIdx.y;
@@ -655,13 +657,22 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq16_kernel(BwdP p) {
             rows_dot<NS, KS, RA, 0>(Vs(kt), li, g, gr, dp, [] {});
             const int k0 = kt * 32;
             const bool full = k0 + 31 <= q0 && k0 + 31 < T;
+            // dS = P (dP - D); masked keys enter the exponential as -inf (P = 0)
+            // through a select, on the diagonal and partial tiles only (written
+            // as one select per key around the exponential, the compiler
+            // branched around each exponential instead)
             float ds[8];
+            if (full) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int key = k0 + 16 * (j >> 2) + 4 * g + (j & 3);
-                const float e = __builtin_amdgcn_exp2f(s[j >> 2][j & 3] - L2);
-                const float pr = (full || (key <= qi && key < T)) ? e : 0.0f;
-                ds[j] = pr * (dp[j >> 2][j & 3] - Dq);
+                for (int j = 0; j < 8; ++j)
+                    ds[j] = __builtin_amdgcn_exp2f(s[j >> 2][j & 3] - L2) * (dp[j >> 2][j & 3] - Dq);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int key = k0 + 16 * (j >> 2) + 4 * g + (j & 3);
+                    const float x = key <= qi && key < T ? s[j >> 2][j & 3] - L2 : -INFINITY;
+                    ds[j] = __builtin_amdgcn_exp2f(x) * (dp[j >> 2][j & 3] - Dq);
+                }
             }
             cols_acc<NH, KS, RA>(Ks(kt), li, g, ds, dqa);
             if (kt == my_tiles - 1 && qi < T) {
@@ -696,7 +707,9 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv16_kernel(BwdP p) {
     auto Ls = [&](int it) { return smem + ((it >> 1) & 1) * STAGE + 128 * KS + (it & 1) * 32; };
     auto Ds = [&](int it) { return Ls(it) + 64; };
 
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    // the wave index through readfirstlane: uniform, so what derives from it
+    // (strip, rows, tile counts, their tests) is scalar work in scalar registers
+    const int tid = threadIdx.x, wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
     const int g = lane >> 4, li = lane & 15;
     const int strip = wave < 4 ? wave : 11 - wave;
     const int groups = p.h / p.hkv;
@@ -791,14 +804,23 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv16_kernel(BwdP p) {
             const float lv[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
             const float dv8[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
             const bool full = qt * 32 >= k0 + 15 && qt * 32 + 31 < T && k0 + 15 < T;
+            // masked queries enter the exponential as -inf (P = 0) through a
+            // select, on the diagonal and partial tiles only
             float pv[8], ds[8];
+            if (full) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int q = qt * 32 + 16 * (j >> 2) + 4 * g + (j & 3);
-                const float e = __builtin_amdgcn_exp2f(s[j >> 2][j & 3] - lv[j]);
-                const float pr = (full || (kj <= q && q < T && kj < T)) ? e : 0.0f;
-                pv[j] = pr;
-                ds[j] = pr * (dp[j >> 2][j & 3] - dv8[j]);
+                for (int j = 0; j < 8; ++j) {
+                    pv[j] = __builtin_amdgcn_exp2f(s[j >> 2][j & 3] - lv[j]);
+                    ds[j] = pv[j] * (dp[j >> 2][j & 3] - dv8[j]);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int q = qt * 32 + 16 * (j >> 2) + 4 * g + (j & 3);
+                    const float x = kj <= q && q < T && kj < T ? s[j >> 2][j & 3] - lv[j] : -INFINITY;
+                    pv[j] = __builtin_amdgcn_exp2f(x);
+                    ds[j] = pv[j] * (dp[j >> 2][j & 3] - dv8[j]);
+                }
             }
             cols_acc<NH, KS, RA>(Gs(it), li, g, pv, dva);
             cols_acc<NH, KS, RA>(Qs(it), li, g, ds, dka);
