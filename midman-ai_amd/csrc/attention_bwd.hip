@@ -239,8 +239,8 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dq_kernel(BwdP p) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
                 const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-                const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - L2);
-                const float pr = (full || (key <= qi && key < T)) ? e : 0.0f;
+                // masked keys enter the exponential as -inf (a select; P = 0)
+                const float pr = __builtin_amdgcn_exp2f(full || (key <= qi && key < T) ? (s0[r] + s1[r]) - L2 : -INFINITY);
                 ds[r] = pr * ((g0[r] + g1[r]) - Dq);
             }
 #pragma unroll
@@ -409,8 +409,7 @@ __global__ __launch_bounds__(256, 1) void attn_bwd_dkv_kernel(BwdP p) {
             for (int r = 0; r < 16; ++r) {
                 const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
                 const int q = qt * 32 + row;
-                const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - Lb[row]);
-                const float pr = (full || (kj <= q && q < T && kj < T)) ? e : 0.0f;
+                const float pr = __builtin_amdgcn_exp2f(full || (kj <= q && q < T && kj < T) ? (s0[r] + s1[r]) - Lb[row] : -INFINITY);
                 pv[r] = pr;
                 ds[r] = pr * ((g0[r] + g1[r]) - Db[row]);
             }
@@ -930,8 +929,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_split_kernel(BwdP p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             const int key = k0 + 8 * (r >> 2) + 4 * lh + (r & 3);
-            const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - L2);
-            const float pr = (full || (key <= qi && key < T)) ? e : 0.0f;
+            // masked keys enter the exponential as -inf (a select; P = 0)
+            const float pr = __builtin_amdgcn_exp2f(full || (key <= qi && key < T) ? (s0[r] + s1[r]) - L2 : -INFINITY);
             ds[r] = pr * ((g0[r] + g1[r]) - Dq);
         }
 #pragma unroll
@@ -1033,8 +1032,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_split_kernel(BwdP p) {
             const int row = 8 * (r >> 2) + 4 * lh + (r & 3);
             const int q = qt * 32 + row;
             const float lrow = __shfl(lreg, row, 64), drow = __shfl(lreg, 32 + row, 64);
-            const float e = __builtin_amdgcn_exp2f((s0[r] + s1[r]) - lrow);
-            const float pr = (full || (kj <= q && q < T && kj < T)) ? e : 0.0f;
+            const float pr = __builtin_amdgcn_exp2f(full || (kj <= q && q < T && kj < T) ? (s0[r] + s1[r]) - lrow : -INFINITY);
             pv[r] = pr;
             ds[r] = pr * ((g0[r] + g1[r]) - drow);
         }
