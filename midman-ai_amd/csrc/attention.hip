@@ -399,14 +399,26 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
     for (int db = 0; db < 4 * NH; ++db) o[db] = floatx4{0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // sum / max over a query's four lanes (i, i+16, i+32, i+48); the max as
-    // med3(a, b, +inf), which needs none of the quieting moves fmaxf takes
-    // around values from lane swaps (scores are finite or -inf)
-    auto quad_max = [](float v) __attribute__((always_inline)) {
+    // sum / max over a query's four lanes (i, i+16, i+32, i+48). Maxima as
+    // bare v_max_f32 / v_max3_f32: fmaxf (and med3 with +inf, which the
+    // compiler folds into it) takes a quieting max of each operand it cannot
+    // prove canonical first (lane-swapped values, selects), and scores here
+    // are finite or -inf, never NaN
+    auto vmax = [](float x, float y) __attribute__((always_inline)) {
+        float r;
+        asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+        return r;
+    };
+    auto vmax3 = [](float x, float y, float z) __attribute__((always_inline)) {
+        float r;
+        asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+        return r;
+    };
+    auto quad_max = [&](float v) __attribute__((always_inline)) {
         auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        v = __builtin_amdgcn_fmed3f(__uint_as_float(a[0]), __uint_as_float(a[1]), INFINITY);
+        v = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
         auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-        return __builtin_amdgcn_fmed3f(__uint_as_float(c[0]), __uint_as_float(c[1]), INFINITY);
+        return vmax(__uint_as_float(c[0]), __uint_as_float(c[1]));
     };
     auto quad_sum = [](float v) __attribute__((always_inline)) {
         auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -430,28 +442,37 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
     auto qk_softmax = [&](int kt, int nxt) __attribute__((always_inline)) {
         const float *Kb = Ks(kt);
         // 16 float4 K operands per tile, step i = 2t + kb: K[16kb + li][g*NS + 4t ..],
-        // each feeding 4 MFMAs; read RA steps ahead through a ring of RA+1
-        // registers so the LDS latency hides behind the MFMAs of earlier steps.
+        // each feeding 4 MFMAs. Steps go in pairs (2t, 2t+1), whose MFMAs
+        // alternate between the two accumulators (no MFMA waits on the one
+        // before it); a ring of four registers holds the pair in use and the
+        // next one, the pair after that read as soon as a pair is used.
         floatx4 sacc[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-        float4 ring[RA + 1];
+        constexpr int NK = 2 * (NS / 4);
+        float4 ring[4];
         auto kread = [&](int i) __attribute__((always_inline)) {
             return reinterpret_cast<const float4 *>(Kb + (16 * (i & 1) + li) * KS + g * NS)[i >> 1];
         };
 #pragma unroll
-        for (int i = 0; i < RA; ++i) ring[i] = kread(i);
-        __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+        for (int i = 0; i < 4; ++i) ring[i] = kread(i);
+        __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-        for (int i = 0; i < 2 * (NS / 4); ++i) {
-            if (i + RA < 2 * (NS / 4)) ring[(i + RA) % (RA + 1)] = kread(i + RA);
-            const float4 kv = ring[i % (RA + 1)];
-            const int kb = i & 1, t = i >> 1;
-            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, qr[4 * t + 0], sacc[kb], 0, 0, 0);
-            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, qr[4 * t + 1], sacc[kb], 0, 0, 0);
-            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, qr[4 * t + 2], sacc[kb], 0, 0, 0);
-            sacc[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, qr[4 * t + 3], sacc[kb], 0, 0, 0);
-            if (i + RA < 2 * (NS / 4)) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-            if (i == 1) {
+        for (int t = 0; t < NK / 2; ++t) {
+            const float4 ka = ring[(2 * t) % 4], kc = ring[(2 * t + 1) % 4];
+            sacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.x, qr[4 * t + 0], sacc[0], 0, 0, 0);
+            sacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc.x, qr[4 * t + 0], sacc[1], 0, 0, 0);
+            sacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.y, qr[4 * t + 1], sacc[0], 0, 0, 0);
+            sacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc.y, qr[4 * t + 1], sacc[1], 0, 0, 0);
+            sacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.z, qr[4 * t + 2], sacc[0], 0, 0, 0);
+            sacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc.z, qr[4 * t + 2], sacc[1], 0, 0, 0);
+            sacc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(ka.w, qr[4 * t + 3], sacc[0], 0, 0, 0);
+            sacc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(kc.w, qr[4 * t + 3], sacc[1], 0, 0, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+            if (2 * t + 4 < NK) {
+                ring[(2 * t) % 4] = kread(2 * t + 4);
+                ring[(2 * t + 1) % 4] = kread(2 * t + 5);
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+            }
+            if (t == 0) {
                 load_tile(nxt);
                 __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
             }
@@ -461,21 +482,20 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
         __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
         __builtin_amdgcn_sched_barrier(0);
         const int k0 = kt * 32;
-        float mloc = -INFINITY;
-        if (k0 + 31 <= q0 && k0 + 31 < T) {
+        // the scores stay in the accumulator registers; diagonal and partial
+        // tiles overwrite their masked keys with -inf in place (a full tile
+        // moves nothing)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                pv[j] = sacc[j >> 2][j & 3];
-                mloc = fmaxf(mloc, pv[j]);
-            }
-        } else {
+        for (int j = 0; j < 8; ++j) pv[j] = sacc[j >> 2][j & 3];
+        if (!(k0 + 31 <= q0 && k0 + 31 < T)) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int key = k0 + 16 * (j >> 2) + 4 * g + (j & 3);
-                pv[j] = (key <= qi && key < T) ? sacc[j >> 2][j & 3] : -INFINITY;
-                mloc = fmaxf(mloc, pv[j]);
+                pv[j] = key <= qi && key < T ? pv[j] : -INFINITY;
             }
         }
+        float mloc = vmax3(vmax3(vmax3(pv[0], pv[1], pv[2]), pv[3], pv[4]), pv[5], pv[6]);
+        mloc = vmax(mloc, pv[7]);
         mloc = quad_max(mloc);
         const bool need = mloc > m_run + 8.0f;  // lazy rescale, as attn_fwd_kernel
         if (__any(need)) {

@@ -498,31 +498,40 @@ __device__ __forceinline__ float quad_sum(float v) {
 }
 
 // acc[blk] += X[16 blk + i][32g + s] . y[s] over s: the 2 x NS/4 float4
-// operands of an LDS tile (row stride RS) read RA groups ahead. The tile's
-// next global loads (a lambda) are issued after the second group.
-template <int NS, int RS, int RA, int NLOAD, class Load>
+// operands of an LDS tile (row stride RS). Operands go in pairs (one per
+// block, the same y), whose MFMAs alternate between the two accumulators (no
+// MFMA waits on the one before it); a ring of four registers holds the pair
+// in use and the next, the pair after that read as soon as a pair is used.
+// The tile's next global loads (a lambda) are issued after the first pair.
+template <int NS, int RS, int NLOAD, class Load>
 __device__ __forceinline__ void rows_dot(const float *X, int i, int g, const float (&y)[NS],
                                          floatx4 (&acc)[2], Load &&load) {
     constexpr int N = 2 * (NS / 4);
-    float4 ring[RA + 1];
+    float4 ring[4];
     auto rd = [&](int e) __attribute__((always_inline)) {
         return reinterpret_cast<const float4 *>(X + (16 * (e & 1) + i) * RS + g * NS)[e >> 1];
     };
 #pragma unroll
-    for (int e = 0; e < RA; ++e) ring[e] = rd(e);
-    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);
+    for (int e = 0; e < 4; ++e) ring[e] = rd(e);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
 #pragma unroll
-    for (int e = 0; e < N; ++e) {
-        if (e + RA < N) ring[(e + RA) % (RA + 1)] = rd(e + RA);
-        const float4 x = ring[e % (RA + 1)];
-        const int blk = e & 1, t = e >> 1;
-        acc[blk] = mfma16(x.x, y[4 * t + 0], acc[blk]);
-        acc[blk] = mfma16(x.y, y[4 * t + 1], acc[blk]);
-        acc[blk] = mfma16(x.z, y[4 * t + 2], acc[blk]);
-        acc[blk] = mfma16(x.w, y[4 * t + 3], acc[blk]);
-        if (e + RA < N) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-        if (NLOAD > 0 && e == 1) {
+    for (int t = 0; t < N / 2; ++t) {
+        const float4 xa = ring[(2 * t) % 4], xb = ring[(2 * t + 1) % 4];
+        acc[0] = mfma16(xa.x, y[4 * t + 0], acc[0]);
+        acc[1] = mfma16(xb.x, y[4 * t + 0], acc[1]);
+        acc[0] = mfma16(xa.y, y[4 * t + 1], acc[0]);
+        acc[1] = mfma16(xb.y, y[4 * t + 1], acc[1]);
+        acc[0] = mfma16(xa.z, y[4 * t + 2], acc[0]);
+        acc[1] = mfma16(xb.z, y[4 * t + 2], acc[1]);
+        acc[0] = mfma16(xa.w, y[4 * t + 3], acc[0]);
+        acc[1] = mfma16(xb.w, y[4 * t + 3], acc[1]);
+        __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);
+        if (2 * t + 4 < N) {
+            ring[(2 * t) % 4] = rd(2 * t + 4);
+            ring[(2 * t + 1) % 4] = rd(2 * t + 5);
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        }
+        if (NLOAD > 0 && t == 0) {
             load();
             __builtin_amdgcn_sched_group_barrier(0x020, NLOAD, 0);
         }
@@ -652,8 +661,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dq16_kernel(BwdP p) {
         if (kt < my_tiles) {
             floatx4 s[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
             floatx4 dp[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-            rows_dot<NS, KS, RA, 2 * PER>(Ks(kt), li, g, qr, s, [&] { load_tile(nxt); });
-            rows_dot<NS, KS, RA, 0>(Vs(kt), li, g, gr, dp, [] {});
+            rows_dot<NS, KS, 2 * PER>(Ks(kt), li, g, qr, s, [&] { load_tile(nxt); });
+            rows_dot<NS, KS, 0>(Vs(kt), li, g, gr, dp, [] {});
             const int k0 = kt * 32;
             const bool full = k0 + 31 <= q0 && k0 + 31 < T;
             // dS = P (dP - D); masked keys enter the exponential as -inf (P = 0)
@@ -793,8 +802,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_dkv16_kernel(BwdP p) {
         if (qt >= my_first && k0 < T) {
             floatx4 s[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
             floatx4 dp[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-            rows_dot<NS, KS, RA, 2 * PER>(Qs(it), li, g, kr, s, [&] { load_tile(nxt); });
-            rows_dot<NS, KS, RA, 0>(Gs(it), li, g, vr, dp, [] {});
+            rows_dot<NS, KS, 2 * PER>(Qs(it), li, g, kr, s, [&] { load_tile(nxt); });
+            rows_dot<NS, KS, 0>(Gs(it), li, g, vr, dp, [] {});
             // the tile's lse2 and D for the queries 16qb + 4g + r of this lane
             const float4 l0 = *reinterpret_cast<const float4 *>(Ls(it) + 4 * g);
             const float4 l1 = *reinterpret_cast<const float4 *>(Ls(it) + 16 + 4 * g);
