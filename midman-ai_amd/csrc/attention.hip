@@ -555,7 +555,7 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
         store_tile(1);
     }
     __syncthreads();
-    for (int kt = 0; kt < ntiles; ++kt) {
+    auto step = [&](int kt) __attribute__((always_inline)) {
         // during tile kt, the tile two ahead goes to the other stage
         const int nxt = min(kt + 2, ntiles - 1);  // the last steps reload a tile they never store
         if (kt < my_tiles) {
@@ -565,7 +565,15 @@ __global__ __launch_bounds__(1024) void attn_fwd16_kernel(AttnP p) {
             load_tile(nxt);
         }
         if (kt + 2 < ntiles) store_tile(kt + 2);
-        if ((kt & 1) && kt + 1 < ntiles) __syncthreads();
+    };
+    // one stage (two tiles) per iteration: each tile's position in the stage
+    // is then a constant, and its LDS offsets immediates
+    for (int m = 0; 2 * m < ntiles; ++m) {
+        step(2 * m);
+        if (2 * m + 1 < ntiles) {
+            step(2 * m + 1);
+            if (2 * m + 2 < ntiles) __syncthreads();
+        }
     }
 }
 
