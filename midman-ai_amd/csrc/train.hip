@@ -135,11 +135,19 @@ __global__ __launch_bounds__(NT) void ce_fwd_bwd_regs_kernel(float *__restrict__
     const int v4 = (int)(v >> 2), tid = threadIdx.x;
     const int64_t t = targets[row];
     const float zt = tid == 0 ? logits[row * v + t] : 0.0f;
+    // the row streams through once each way: nontemporal loads and stores
+    // (the logits, hundreds of MB, are read nowhere else; the head's backward
+    // products that read the dlogits next are bound by their matrix work)
     float4 e[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         const int q = tid + NT * i;
-        e[i] = q < v4 ? z4[q] : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        if (q < v4) {
+            const nt4 t4 = __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(z4 + q));
+            e[i] = make_float4(t4[0], t4[1], t4[2], t4[3]);
+        } else {
+            e[i] = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
     }
     float m = -INFINITY;
 #pragma unroll
@@ -180,7 +188,7 @@ __global__ __launch_bounds__(NT) void ce_fwd_bwd_regs_kernel(float *__restrict__
             if (c == 2) d.z = __fsub_rn(d.z, scale);
             if (c == 3) d.w = __fsub_rn(d.w, scale);
         }
-        z4[q] = d;
+        __builtin_nontemporal_store(nt4{d.x, d.y, d.z, d.w}, reinterpret_cast<nt4 *>(z4 + q));
     }
 }
 
@@ -241,20 +249,27 @@ __global__ __launch_bounds__(64 * WPB) void rms_bwd_rows_kernel(const float *__r
     const float4 *g4 = reinterpret_cast<const float4 *>(dy + r * d);
     float4 *o4 = reinterpret_cast<float4 *>(dx + r * d);
     float4 xv[NV], gv[NV], ov[NV];
+    // x and dy with the nontemporal hint: read once here, nothing after this
+    // kernel reads them again soon (dx, which the next layer's backward reads,
+    // keeps the default)
+    auto ntl = [](const float4 *q) __attribute__((always_inline)) {
+        const nt4 t = __builtin_nontemporal_load(reinterpret_cast<const nt4 *>(q));
+        return make_float4(t[0], t[1], t[2], t[3]);
+    };
     if (accumulate) {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int jc = min(lane + 64 * i, d4 - 1);
-            xv[i] = x4[jc];
-            gv[i] = g4[jc];
+            xv[i] = ntl(x4 + jc);
+            gv[i] = ntl(g4 + jc);
             ov[i] = o4[jc];
         }
     } else {
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
             const int jc = min(lane + 64 * i, d4 - 1);
-            xv[i] = x4[jc];
-            gv[i] = g4[jc];
+            xv[i] = ntl(x4 + jc);
+            gv[i] = ntl(g4 + jc);
             ov[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
     }
