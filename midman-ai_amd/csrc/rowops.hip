@@ -109,8 +109,11 @@ __global__ __launch_bounds__(256) void rms_norm_kernel(const float *__restrict__
 }
 
 // The same for rows of d <= 256*NV floats (d % 4 == 0): the wave keeps its row
-// in registers, so x is read once, and all NV float4 loads per lane are issued
-// before the first is used.
+// in registers, so x is read once, and all NV float4 loads per lane (and the
+// matching w ones) are issued before the first is used: at clamped,
+// unconditional addresses (a guarded load per float4 was compiled into its
+// own branch, and each w load after the reduction into a round trip before
+// its store), the columns past d then zeroed by selects.
 template <int NV>
 __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *__restrict__ x,
                                                             const float *__restrict__ w,
@@ -121,11 +124,23 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *__restr
     if (row >= rows) return;
     const int d4 = d >> 2;
     const float4 *x4 = reinterpret_cast<const float4 *>(x + row * d);
-    float4 v[NV];
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float4 v[NV], wv[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
-        const int j = lane + 64 * i;
-        v[i] = j < d4 ? x4[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        const int jc = min(lane + 64 * i, d4 - 1);
+        v[i] = x4[jc];
+        wv[i] = w4[jc];
+    }
+    if (d4 < 64 * NV) {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const bool in = lane + 64 * i < d4;
+            v[i].x = in ? v[i].x : 0.0f;
+            v[i].y = in ? v[i].y : 0.0f;
+            v[i].z = in ? v[i].z : 0.0f;
+            v[i].w = in ? v[i].w : 0.0f;
+        }
     }
     float ss = 0.0f;
 #pragma unroll
@@ -138,20 +153,24 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float *__restr
     ss = wave_sum(ss);
     const float mean = __fmul_rn(ss, __fdiv_rn(1.0f, (float)d));
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(mean, eps)));
-    const float4 *w4 = reinterpret_cast<const float4 *>(w);
     float4 *o4 = reinterpret_cast<float4 *>(out + row * d);
+    auto res = [&](int i) __attribute__((always_inline)) {
+        float4 r;
+        r.x = __fmul_rn(__fmul_rn(v[i].x, inv), wv[i].x);
+        r.y = __fmul_rn(__fmul_rn(v[i].y, inv), wv[i].y);
+        r.z = __fmul_rn(__fmul_rn(v[i].z, inv), wv[i].z);
+        r.w = __fmul_rn(__fmul_rn(v[i].w, inv), wv[i].w);
+        return r;
+    };
+    if (d4 == 64 * NV) {
+        // rows that fill every lane's float4s: stores without guards, so no
+        // store waits on the ones before it
 #pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        const int j = lane + 64 * i;
-        if (j < d4) {
-            const float4 g = w4[j];
-            float4 r;
-            r.x = __fmul_rn(__fmul_rn(v[i].x, inv), g.x);
-            r.y = __fmul_rn(__fmul_rn(v[i].y, inv), g.y);
-            r.z = __fmul_rn(__fmul_rn(v[i].z, inv), g.z);
-            r.w = __fmul_rn(__fmul_rn(v[i].w, inv), g.w);
-            o4[j] = r;
-        }
+        for (int i = 0; i < NV; ++i) o4[lane + 64 * i] = res(i);
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if (lane + 64 * i < d4) o4[lane + 64 * i] = res(i);
     }
 }
 
